@@ -1,0 +1,95 @@
+"""ctypes binding of libmathbrain_hip.so, the gfx950 C-ABI library.
+
+The library is loaded after torch so that it binds to the HIP runtime torch has
+already loaded (both carry the soname libamdhip64.so.7) and therefore shares
+torch's devices, memory and streams.  There is no fallback: if the library is
+missing every entry point raises, naming the build command.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmathbrain_hip.so")
+
+MB_OK = 0
+MB_ERR_INVALID_ARGUMENT = -1
+MB_ERR_UNSUPPORTED = -2
+MB_ERR_WORKSPACE = -3
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+
+# name -> argtypes; every entry is declared in include/mathbrain_hip.h
+SIGNATURES = {
+    "mb_last_error": ([], ctypes.c_char_p),
+    "mb_abi_version": ([], _i),
+    "mb_ema_query_scan": ([_p, _i64, _i64, _i, _i, _p, _i, _i64, _p, _p, _i, _p, _p, _p, _p, _p], _i),
+    "mb_ema_boundary_states": ([_p, _i64, _i64, _i, _i, _p, _i, _p, _i, _i, _p, _i64, _p, _p, _i, _p], _i),
+}
+
+_lib = None
+
+
+class HipKernelError(RuntimeError):
+    """A C-ABI call rejected its arguments or its launch failed."""
+
+
+class HipLibraryMissing(RuntimeError):
+    """libmathbrain_hip.so is not built (python -m mathbrain_amd.build)."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HipLibraryMissing(
+                f"{LIB_PATH} is missing; build it with `python -m mathbrain_amd.build` "
+                "(mathbrain_amd has no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def call(name, *args):
+    """Calls C-ABI entry `name`; raises HipKernelError with the library's message on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != MB_OK:
+        msg = lib().mb_last_error().decode(errors="replace")
+        kind = {MB_ERR_INVALID_ARGUMENT: "invalid argument", MB_ERR_UNSUPPORTED: "unsupported",
+                MB_ERR_WORKSPACE: "workspace too small"}.get(rc, f"HIP error {rc}")
+        raise HipKernelError(f"{name}: {kind}: {msg}")
+
+
+def ptr(t):
+    """Device address of a tensor (None for None)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream(device):
+    """The current torch stream of `device` as a raw hipStream_t."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu(*tensors, what="mathbrain_amd"):
+    """Every tensor must live on one ROCm GPU: the product has no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise NotImplementedError(
+                f"{what}: tensors must be on an MI355X GPU (got device {t.device}); "
+                "this implementation has no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{what}: tensors on different devices ({dev} and {t.device})")
+    return dev

@@ -1,0 +1,40 @@
+// Error reporting and version entry points of the mathbrain C ABI.
+#include "common.h"
+
+namespace mb {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+}
+
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+        return (int)e;
+    }
+    return MB_OK;
+}
+
+}  // namespace mb
+
+extern "C" const char* mb_last_error(void) { return mb::g_last_error.c_str(); }
+
+extern "C" int mb_abi_version(void) { return 1; }

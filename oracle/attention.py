@@ -1,0 +1,184 @@
+"""TEST INFRASTRUCTURE ONLY: CPU restatement of flash-EMA gated attention (the checker).
+
+Three forms of the same attention, all in torch on the CPU:
+
+``dense``      flash_ema_attention.flash_ema_forward (mathbrain/flash_ema_attention.py
+               :19-85): one loop over L with a dense [B, V, N] counter state, decay ->
+               gate -> attend over all V slots -> count.  Two generalisations, both
+               no-ops for the reference's own inputs: an optional key-side initial
+               state ``c_global`` (the reference starts from zeros, :36), and an
+               out-of-place count update so autograd can differentiate it (the
+               reference's in-place ``C[...] += 1`` at :82 makes backward fail).
+``sparse``     the same attention over the unique slots of each sequence only, with
+               the (V - K_b) absent slots -- whose counters stay zero, so their gate
+               is SiLU(0) = 0 and their score 0 -- folded into the softmax
+               denominator as (V - K_b) * exp(0 - m).  ``absent_mass=False`` gives
+               the Triton kernel as executed (triton_flash_ema.py:215-229 wipes the
+               absent mass).  ``gate_bf16=True`` rounds the gate operands to
+               bfloat16 as triton_flash_ema.py:188-190 does.
+``sparse_backward_formulas``
+               the reference's closed-form gradients (triton_flash_ema.py:336-350
+               and :446-465), evaluated loop by loop; autograd of ``sparse`` must
+               agree with it.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def silu_grad(x):
+    """SiLU'(x) = sig(x) * (1 + x * (1 - sig(x)))  (triton_flash_ema.py:458)."""
+    s = torch.sigmoid(x)
+    return s * (1 + x * (1 - s))
+
+
+def dense(Q, x, E_k_slots, E_v_slots, rhos, pe_weight, n_heads, use_silu=True, c_global=None):
+    """flash_ema_attention.flash_ema_forward (flash_ema_attention.py:19-85).
+
+    Q [B, L, D], x [B, L] int64, E_k_slots / E_v_slots [V, D], rhos [N],
+    pe_weight [D, N] (= pe_proj.weight), c_global [B, V, N] or None.
+    Returns out [B, L, D].
+    """
+    B, L, D = Q.shape
+    V = E_k_slots.shape[0]
+    N = rhos.shape[0]
+    H = n_heads
+    hd = D // H
+    C = torch.zeros(B, V, N, dtype=Q.dtype) if c_global is None else c_global.to(Q.dtype)
+    E_k = E_k_slots.reshape(V, H, hd).unsqueeze(0)
+    E_v = E_v_slots.reshape(V, H, hd).unsqueeze(0)
+    rho = rhos.to(Q.dtype).reshape(1, 1, N)
+    outs = []
+    for t in range(L):
+        C = C * rho                                                  # :48
+        p_lin = (C @ pe_weight.t().to(Q.dtype)).reshape(B, V, H, hd)  # :51
+        gate = F.silu(p_lin) if use_silu else p_lin                  # :52-55
+        Kt = (E_k * gate).transpose(1, 2)                            # :58 [B,H,V,hd]
+        Vt = (E_v * gate).transpose(1, 2)                            # :59
+        q_t = Q[:, t].reshape(B, H, 1, hd)                           # :73
+        attn = (q_t @ Kt.transpose(-2, -1)) / math.sqrt(hd)          # :76
+        attn = torch.softmax(attn, dim=-1)                           # :77
+        outs.append(attn @ Vt)                                       # :79 [B,H,1,hd]
+        onehot = F.one_hot(x[:, t], V).to(Q.dtype).unsqueeze(-1)     # :82, out of place
+        C = C + onehot
+    O = torch.cat(outs, dim=2)                                       # [B,H,L,hd]
+    return O.transpose(1, 2).reshape(B, L, D)                       # :84
+
+
+def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=True,
+           absent_mass=True, gate_bf16=False, return_lse=False):
+    """Unique-slot flash-EMA attention.
+
+    Q [B, H, L, hd]; x [B, L]; E_k / E_v [B, K, D]; W_pe [N, D] (= pe_proj.weight.T);
+    unique [B, K] int64 with -1 padding; c_init [B, K, N] key-side state at t=0
+    (C_bounds[:, 0]).  Returns O [B, H, L, hd] (and LSE [B, H, L]).
+
+    The per-step order is the reference's: c_dec = C * rho (triton_flash_ema.py:185),
+    g = SiLU(c_dec @ W_pe[:, head]) (:188-196), s = q.(e_k*g)/sqrt(hd) over valid
+    slots (:205-207), online softmax (:224-234), then C = c_dec + match (:241).
+    """
+    B, H, L, hd = Q.shape
+    K = unique.shape[1]
+    N = rhos.shape[0]
+    D = H * hd
+    dt = Q.dtype
+    valid = unique != -1                                             # [B, K]
+    Kb = valid.sum(1)                                                # [B]
+    C = torch.zeros(B, K, N, dtype=dt) if c_init is None else c_init[:, :, :N].to(dt)
+    C = C * valid.unsqueeze(-1).to(dt)
+    rho = rhos.to(dt).reshape(1, 1, N)
+    W = W_pe[:N].to(dt)
+    if gate_bf16:
+        W = W.to(torch.bfloat16).to(dt)
+    Ek = E_k.reshape(B, K, H, hd).to(dt)
+    Ev = E_v.reshape(B, K, H, hd).to(dt)
+    log_absent = torch.log((V_total - Kb).clamp(min=0).to(dt))       # -inf if none absent
+    outs, lses = [], []
+    for t in range(L):
+        c_dec = C * rho
+        cg = c_dec.to(torch.bfloat16).to(dt) if gate_bf16 else c_dec
+        pre = (cg @ W).reshape(B, K, H, hd)
+        g = F.silu(pre) if use_silu else pre
+        q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
+        s = (q_t * Ek * g).sum(-1) / math.sqrt(hd)                   # [B,K,H]
+        s = s.masked_fill(~valid.unsqueeze(-1), float("-inf"))
+        if absent_mass:
+            extra = log_absent.reshape(B, 1, 1).expand(B, 1, H)
+            lse = torch.logsumexp(torch.cat([s, extra], dim=1), dim=1)    # [B,H]
+        else:
+            lse = torch.logsumexp(s, dim=1)
+        p = torch.exp(s - lse.unsqueeze(1))                          # [B,K,H]
+        o = (p.unsqueeze(-1) * Ev * g).sum(1)                        # [B,H,hd]
+        outs.append(o)
+        lses.append(lse)
+        match = (x[:, t].unsqueeze(1) == unique) & valid
+        C = c_dec + match.unsqueeze(-1).to(dt)
+    O = torch.stack(outs, dim=2)                                     # [B,H,L,hd]
+    LSE = torch.stack(lses, dim=2)                                   # [B,H,L]
+    return (O, LSE) if return_lse else O
+
+
+@torch.no_grad()
+def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_init=None,
+                             use_silu=True, absent_mass=True):
+    """The reference's closed-form backward, loop by loop (float64 recommended).
+
+    D = (dO*O).sum(-1) (triton_flash_ema.py:602); p = exp(s - LSE) (:336);
+    ds = p (dO.v - D) (:339-340); dQ = sum_k ds k_dyn/sqrt(hd) (:343);
+    dE_k = sum_t ds q*g/sqrt(hd) (:349); dE_v = sum_t p dO*g (:350);
+    dpre = (ds q/sqrt(hd)*e_k + p dO*e_v) * SiLU'(pre) (:453-461);
+    dW_pe[:, head] = sum c_dec^T dpre (:465).
+    Returns dQ [B,H,L,hd], dE_k [B,K,D], dE_v [B,K,D], dW_pe [N,D].
+    """
+    B, H, L, hd = Q.shape
+    K = unique.shape[1]
+    N = rhos.shape[0]
+    D = H * hd
+    dt = Q.dtype
+    O, LSE = sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init, use_silu,
+                    absent_mass, return_lse=True)
+    Dv = (dO * O).sum(-1)                                            # [B,H,L]
+    valid = unique != -1
+    C = torch.zeros(B, K, N, dtype=dt) if c_init is None else c_init[:, :, :N].to(dt)
+    C = C * valid.unsqueeze(-1).to(dt)
+    rho = rhos.to(dt).reshape(1, 1, N)
+    W = W_pe[:N].to(dt)
+    Ek = E_k.reshape(B, K, H, hd).to(dt)
+    Ev = E_v.reshape(B, K, H, hd).to(dt)
+    dQ = torch.zeros_like(Q)
+    dEk = torch.zeros(B, K, H, hd, dtype=dt)
+    dEv = torch.zeros(B, K, H, hd, dtype=dt)
+    dW = torch.zeros(N, D, dtype=dt)
+    scale = 1.0 / math.sqrt(hd)
+    for t in range(L):
+        c_dec = C * rho
+        pre = (c_dec @ W).reshape(B, K, H, hd)
+        g = F.silu(pre) if use_silu else pre
+        gp = silu_grad(pre) if use_silu else torch.ones_like(pre)
+        q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
+        do_t = dO[:, :, t].unsqueeze(1)
+        s = (q_t * Ek * g).sum(-1) * scale
+        p = torch.exp(s - LSE[:, :, t].unsqueeze(1)) * valid.unsqueeze(-1).to(dt)
+        dp = (do_t * Ev * g).sum(-1)
+        ds = p * (dp - Dv[:, :, t].unsqueeze(1))                     # [B,K,H]
+        dQ[:, :, t] = (ds.unsqueeze(-1) * Ek * g).sum(1) * scale
+        dEk += ds.unsqueeze(-1) * q_t * g * scale
+        dEv += p.unsqueeze(-1) * do_t * g
+        dpre = (ds.unsqueeze(-1) * q_t * scale * Ek + p.unsqueeze(-1) * do_t * Ev) * gp
+        dW += torch.einsum("bkn,bkd->nd", c_dec, dpre.reshape(B, K, D))
+        match = (x[:, t].unsqueeze(1) == unique) & valid
+        C = c_dec + match.unsqueeze(-1).to(dt)
+    return dQ, dEk.reshape(B, K, D), dEv.reshape(B, K, D), dW
+
+
+def scatter_c_global(unique, c_init, V):
+    """Dense key-side initial state [B, V, N] from the unique-slot one (pads dropped)."""
+    B, K, N = c_init.shape
+    Cg = torch.zeros(B, V, N, dtype=c_init.dtype)
+    for b in range(B):
+        for k in range(K):
+            u = int(unique[b, k])
+            if u >= 0:
+                Cg[b, u] = c_init[b, k]
+    return Cg
