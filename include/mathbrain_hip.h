@@ -89,6 +89,44 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
                            const float *c_init, int64_t c_init_stride_k, const int64_t *doc_ids,
                            float *C_bounds, int Np, void *stream);
 
+/* Flags of the flash-EMA entry points. */
+#define MB_FLASH_SILU 1        /* gate = SiLU(pre); otherwise the linear gate (use_silu=False) */
+#define MB_FLASH_ABSENT_MASS 2 /* softmax also over the V - K_b absent slots (score 0) */
+
+/*
+ * Flash-EMA gated cross-attention forward.  Replaces flash_ema_forward and its kernel
+ * _flash_ema_fwd (mathbrain/triton_flash_ema.py:529-568, :121-241).  For sequence b,
+ * head h, step t and valid slot k (unique[b,k] >= 0):
+ *
+ *   c_dec[t,k,:] = C_bounds[b, t/Br, k, :N] rho^(t - Br*(t/Br) + 1)
+ *                  + sum_{Br*(t/Br) <= s < t, x_s = unique[b,k]} rho^(t-s)
+ *   g[t,k,:]     = SiLU(c_dec[t,k,:] . W_pe[:, h*hd:(h+1)*hd])   (bf16 operands)
+ *   s[t,k]       = Q[b,h,t] . (E_k[b,k,h] * g[t,k]) / sqrt(hd)
+ *   O[b,h,t]     = sum_k softmax_k(s) E_v[b,k,h] * g[t,k]
+ *   LSE[b,h,t]   = log(sum_k exp s[t,k] (+ V_total - K_b with MB_FLASH_ABSENT_MASS))
+ *
+ * With MB_FLASH_ABSENT_MASS the softmax holds all V_total slots as the dense PyTorch
+ * reference does (mathbrain/flash_ema_attention.py:76-77); without it, only the valid
+ * slots, as the Triton kernel computes (triton_flash_ema.py:215-229).
+ *
+ *   Q         [B, H, L, hd] fp32, element strides q_sb, q_sh, q_sl, q_sd
+ *   x         [B, L] int64, element strides x_sb, x_sl
+ *   E_k, E_v  [B, K, H*hd] fp32 contiguous
+ *   W_pe      [N, H*hd] fp32 contiguous (pe_proj.weight transposed)
+ *   rhos      [N] fp32
+ *   unique    [B, K] int64 contiguous, -1 = padding slot
+ *   C_bounds  [B, nc, K, Np] fp32 contiguous (mb_ema_boundary_states), nc >= ceil(L/Br)
+ *   O         [B, H, L, hd] fp32 contiguous output; LSE [B, H, L] fp32 output
+ *
+ * Supported: hd in {32, 64}, 4 <= H <= 8, N <= 128, Br <= 32 or Br == 64.
+ */
+int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,
+                     const int64_t *x, int64_t x_sb, int64_t x_sl, const float *E_k,
+                     const float *E_v, const float *W_pe, const float *rhos,
+                     const int64_t *unique, const float *C_bounds, int B, int H, int L, int hd,
+                     int K, int N, int Np, int nc, int Br, int64_t V_total, int flags, float *O,
+                     float *LSE, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

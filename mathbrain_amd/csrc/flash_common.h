@@ -1,0 +1,242 @@
+// Pieces shared by the flash-EMA forward and backward kernels (gfx950).
+//
+// Both kernels work on one (sequence b, 32-step block) per workgroup and walk the valid
+// slots of b in batches of SB.  For every batch the whole workgroup first builds, in LDS,
+//   cdec[j][t][n]  (bf16)  the decayed key-side counter c_dec[t, u_j, n] that gates step t,
+//   E[j][0|1][D]   (fp32)  the slot's key and value embeddings,
+// and every wave then consumes the batch for its head(s).  The counter comes from the
+// chunk-start state S = C_bounds[b, t0 / Br, k] and the slot's occurrences inside the
+// window [cb, t0 + 32) (cb = chunk start):
+//   c_dec[t] = S rho^(t-cb+1) + sum_{cb <= s < t, x_s = u} rho^(t-s)
+// which is the reference's per-step  c_dec = C * rho ; C = c_dec + match
+// (mathbrain/triton_flash_ema.py:150-153, 175, 185, 241) unrolled from the chunk start.
+#pragma once
+
+#include <hip/hip_bf16.h>
+
+#include "common.h"
+
+namespace mb {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr int kTB = 32;      // time steps per workgroup
+constexpr int kMaxWin = 64;  // positions [cb, t0 + 32) of the match window
+
+struct FlashArgs {
+    const float* Q;
+    int64_t q_sb, q_sh, q_sl, q_sd;
+    const int64_t* x;
+    int64_t x_sb, x_sl;
+    const float* Ek;  // [B, K, D]
+    const float* Ev;  // [B, K, D]
+    const float* W;   // [N, D]  (pe_proj.weight transposed)
+    const float* rhos;
+    const int64_t* unique;  // [B, K], -1 = padding
+    const float* Cb;        // [B, nc, K, Np]
+    int B, H, L, hd, K, N, Np, Br, nc;
+    float v_total;  // vocabulary size; < 0 drops the absent-slot softmax mass
+    int silu;
+    float* O;    // [B, H, L, hd]
+    float* LSE;  // [B, H, L]
+    // backward only
+    const float* dO;   // [B, H, L, hd], same strides as Q
+    const float* Oin;  // forward output, [B, H, L, hd] contiguous
+    const float* LSEin;
+    float* dQ;   // [B, H, L, hd] contiguous
+    float* dEk;  // [B, K, D], accumulated with atomics (zeroed by the host)
+    float* dEv;
+    float* dW;   // [N, D], accumulated with atomics (zeroed by the host)
+    int head_groups;  // backward: workgroups per (b, block) along heads
+};
+
+__device__ inline f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Workgroup id -> logical id so that consecutive logical ids (the blocks of one
+// sequence, which share its slot embeddings) land on the same XCD and its L2:
+// the dispatcher hands workgroups to the 8 XCDs round-robin.
+__device__ inline int xcd_major(int bid, int G) {
+    if (G % 8) return bid;
+    return (bid % 8) * (G / 8) + bid / 8;
+}
+
+// LDS carve-up of the per-batch staging buffers.
+template <int NPAD, int SB>
+struct Stage {
+    static constexpr int CROW = NPAD + 8;  // bf16 per cdec row (16 B pad against conflicts)
+    static constexpr int CDEC = SB * kTB * CROW;  // bf16 elements per buffer
+    __host__ __device__ static size_t bytes(int D) {
+        return (size_t)CDEC * 2 + (size_t)SB * 2 * D * 4;
+    }
+};
+
+struct BatchMeta {
+    int64_t u;
+    uint64_t mask;
+};
+
+// Per-workgroup setup shared by both kernels: the match window tokens, the rho^j table
+// (j = 0..64) and the valid-slot range of sequence b.
+template <int NPAD>
+__device__ void flash_setup(const FlashArgs& a, int b, int t0, int cb, int64_t* win,
+                            float* powt, int* kinfo) {
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+    for (int p = tid; p < kMaxWin; p += nthr) {
+        const int pos = cb + p;
+        win[p] = (pos < a.L && pos < t0 + kTB) ? a.x[(int64_t)b * a.x_sb + (int64_t)pos * a.x_sl]
+                                              : (int64_t)-1;
+    }
+    for (int i = tid; i < 65 * NPAD; i += nthr) {
+        const int j = i / NPAD;
+        const int n = i % NPAD;
+        float v = 0.0f;
+        if (n < a.N) {
+            float hi, lo;
+            log2_split(a.rhos[n], hi, lo);
+            v = pow_steps(hi, lo, j);
+        }
+        powt[i] = v;
+    }
+    if (tid == 0) {
+        kinfo[0] = 0;   // valid slots K_b
+        kinfo[1] = 0;   // one past the last valid slot
+    }
+    __syncthreads();
+    int cnt = 0, last = 0;
+    for (int k = tid; k < a.K; k += nthr) {
+        if (a.unique[(int64_t)b * a.K + k] >= 0) {
+            ++cnt;
+            last = k + 1;
+        }
+    }
+    if (cnt) atomicAdd(&kinfo[0], cnt);
+    if (last) atomicMax(&kinfo[1], last);
+    __syncthreads();
+}
+
+// Slot ids and 64-bit occurrence masks of batch `bi`: wave j < SB handles slot j.
+template <int SB>
+__device__ void flash_batch_meta(const FlashArgs& a, int b, int bi, int kend, const int64_t* win,
+                                 BatchMeta* meta) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int nwaves = blockDim.x >> 6;
+    for (int j = wave; j < SB; j += nwaves) {
+        const int k = bi * SB + j;
+        const int64_t u = (k < kend) ? a.unique[(int64_t)b * a.K + k] : (int64_t)-1;
+        const bool hit = u >= 0 && win[lane] == u;
+        const uint64_t m = __ballot(hit);
+        if (lane == 0) {
+            meta[j].u = u;
+            meta[j].mask = m;
+        }
+    }
+}
+
+// Producer registers: each thread owns up to MAXI items (t, 4 rates) of the cdec tile and
+// up to MAXE float4 of the embedding copy.
+template <int NPAD, int SB, int MAXI, int MAXE>
+struct Producer {
+    float4 s[MAXI][SB];
+    float4 e[MAXE];
+
+    __device__ void load(const FlashArgs& a, int b, int cbi, int bi, int kend, int D) {
+        const int tid = threadIdx.x;
+        const int nthr = blockDim.x;
+        const int nitems = kTB * (NPAD / 4);
+#pragma unroll
+        for (int ii = 0; ii < MAXI; ++ii) {
+            const int item = tid + ii * nthr;
+            const int n0 = (item % (NPAD / 4)) * 4;
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                const int k = bi * SB + j;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (item < nitems && k < kend) {
+                    const float* src = a.Cb + (((int64_t)b * a.nc + cbi) * a.K + k) * a.Np + n0;
+                    if (n0 + 3 < a.N && (a.Np & 3) == 0) {
+                        v = *reinterpret_cast<const float4*>(src);
+                    } else {
+                        if (n0 + 0 < a.N) v.x = src[0];
+                        if (n0 + 1 < a.N) v.y = src[1];
+                        if (n0 + 2 < a.N) v.z = src[2];
+                        if (n0 + 3 < a.N) v.w = src[3];
+                    }
+                }
+                s[ii][j] = v;
+            }
+        }
+        const int nvec = SB * 2 * (D / 4);
+#pragma unroll
+        for (int ie = 0; ie < MAXE; ++ie) {
+            const int i = tid + ie * nthr;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < nvec) {
+                const int j = i / (2 * (D / 4));
+                const int r = i % (2 * (D / 4));
+                const int which = r / (D / 4);
+                const int c4 = r % (D / 4);
+                const int k = bi * SB + j;
+                if (k < kend) {
+                    const float* src = (which ? a.Ev : a.Ek) + ((int64_t)b * a.K + k) * D + c4 * 4;
+                    v = *reinterpret_cast<const float4*>(src);
+                }
+            }
+            e[ie] = v;
+        }
+    }
+
+    // Builds cdec and E of the batch into the staging buffer.
+    __device__ void store(const FlashArgs& a, int t0, int cb, const float* powt,
+                          const BatchMeta* meta, __bf16* cdec, float* E, int D) {
+        using S = Stage<NPAD, SB>;
+        const int tid = threadIdx.x;
+        const int nthr = blockDim.x;
+        const int nitems = kTB * (NPAD / 4);
+#pragma unroll
+        for (int ii = 0; ii < MAXI; ++ii) {
+            const int item = tid + ii * nthr;
+            if (item >= nitems) continue;
+            const int tl = item / (NPAD / 4);
+            const int n0 = (item % (NPAD / 4)) * 4;
+            const int tr = t0 - cb + tl;  // 0 .. 63
+            const float4 pw = *reinterpret_cast<const float4*>(powt + (tr + 1) * NPAD + n0);
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                const float4 sv = s[ii][j];
+                float c0 = sv.x * pw.x, c1 = sv.y * pw.y, c2 = sv.z * pw.z, c3 = sv.w * pw.w;
+                uint64_t m = meta[j].mask & ((tr >= 64) ? ~0ull : ((1ull << tr) - 1ull));
+                while (m) {
+                    const int p = __builtin_ctzll(m);
+                    m &= m - 1;
+                    const float4 q = *reinterpret_cast<const float4*>(powt + (tr - p) * NPAD + n0);
+                    c0 += q.x;
+                    c1 += q.y;
+                    c2 += q.z;
+                    c3 += q.w;
+                }
+                bf16x4 w;
+                w[0] = (__bf16)c0;
+                w[1] = (__bf16)c1;
+                w[2] = (__bf16)c2;
+                w[3] = (__bf16)c3;
+                *reinterpret_cast<bf16x4*>(cdec + (j * kTB + tl) * S::CROW + n0) = w;
+            }
+        }
+        const int nvec = SB * 2 * (D / 4);
+#pragma unroll
+        for (int ie = 0; ie < (MAXE); ++ie) {
+            const int i = tid + ie * nthr;
+            if (i < nvec) reinterpret_cast<float4*>(E)[i] = e[ie];
+        }
+    }
+};
+
+}  // namespace mb

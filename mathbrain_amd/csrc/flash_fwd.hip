@@ -1,0 +1,300 @@
+// Flash-EMA gated cross-attention forward on gfx950.
+//
+// Replaces _flash_ema_fwd and flash_ema_forward (mathbrain/triton_flash_ema.py:121-241,
+// :529-568).  Semantics, per sequence b, head h, step t and valid slot k:
+//   g[t,k,:] = SiLU(c_dec[t,k,:] . W_pe[:, h])         (bf16 operands, fp32 accumulate)
+//   s[t,k]   = q_t . (e_k[k] * g[t,k]) / sqrt(hd)
+//   O_t      = sum_k softmax_k(s) e_v[k] * g[t,k],   LSE_t = log sum_k exp(s)
+// where, when v_total >= 0, the softmax also holds the V - K_b absent slots of the
+// dense reference (mathbrain/flash_ema_attention.py:76-77): their counters are zero,
+// so their gate SiLU(0) = 0 gives score 0 and value 0, i.e. they add (V - K_b) e^0 to
+// the denominator and nothing to the numerator.
+//
+// Layout: one workgroup per (b, 32-step block) with one wave per head.  The gate GEMM
+// is computed transposed, pre^T[d, t] = W^T[d, :] c_dec^T[:, t], with
+// v_mfma_f32_16x16x32_bf16, so each lane owns one step t (lane % 16 of a 16-step tile)
+// and 16 of the head's 64 dims (rows 16*dt + 4*(lane/16) + i): the score's sum over d
+// stays in registers (plus two cross-lane adds), and O_t's sum over slots accumulates
+// in registers across the slot loop.  The online softmax runs in the log2 domain
+// (W is pre-scaled by log2 e) and rescales only when a score beats the running max by
+// more than 2^8, which keeps every exponential <= 256.
+#include "flash_common.h"
+
+namespace mb {
+
+constexpr float kTau = 8.0f;
+
+template <int HD, int NS, int SB, int MAXI, int MAXE>
+__global__ void __launch_bounds__(512, 1)
+flash_ema_fwd_kernel(FlashArgs a) {
+    constexpr int NPAD = 32 * NS;
+    constexpr int DT = HD / 16;
+    using S = Stage<NPAD, SB>;
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int D = a.H * HD;
+    const int ntb = (a.L + kTB - 1) / kTB;
+    const int logical = xcd_major(blockIdx.x, gridDim.x);
+    const int b = logical / ntb;
+    const int t0 = (logical % ntb) * kTB;
+    const int cbi = t0 / a.Br;
+    const int cb = cbi * a.Br;
+
+    // LDS: two staging buffers, a 3-deep ring of batch slot info (batch i+2's info is
+    // written while batch i is still being read), the window, the power table.
+    const size_t stage_bytes = S::bytes(D);
+    unsigned char* bufs[2] = {smem, smem + stage_bytes};
+    BatchMeta* metas = reinterpret_cast<BatchMeta*>(smem + 2 * stage_bytes);
+    int64_t* win = reinterpret_cast<int64_t*>(metas + 3 * SB);
+    float* powt = reinterpret_cast<float*>(win + kMaxWin);
+    int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
+    auto cdec_of = [&](int i) { return reinterpret_cast<__bf16*>(bufs[i]); };
+    auto E_of = [&](int i) { return reinterpret_cast<float*>(bufs[i] + (size_t)S::CDEC * 2); };
+    auto meta_of = [&](int batch) { return metas + (batch % 3) * SB; };
+
+    flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
+    const int kvalid = kinfo[0];
+    const int kend = kinfo[1];
+    const int nb = (kend + SB - 1) / SB;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int c16 = lane & 15;
+    const int g = lane >> 4;
+    const int h = wave;
+
+    // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
+    bf16x8 wf[DT][NS];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int n = 32 * ns + 8 * g + e;
+                const float w = n < a.N ? a.W[(int64_t)n * D + h * HD + 16 * dt + c16] * kLog2e : 0.f;
+                wf[dt][ns][e] = (__bf16)w;
+            }
+
+    // Queries of this lane's steps, pre-scaled by 1/sqrt(hd).
+    const float qscale = 1.0f / sqrtf((float)HD);
+    f32x4 qs[2][DT], o[2][DT];
+    float m[2], l[2];
+    const float absent = a.v_total >= 0.f ? fmaxf(a.v_total - (float)kvalid, 0.f) : 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int t = t0 + 16 * tt + c16;
+        const float* qrow = a.Q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)t * a.q_sl;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 16 * dt + 4 * g + i;
+                qs[tt][dt][i] = t < a.L ? qrow[(int64_t)d * a.q_sd] * qscale : 0.f;
+                o[tt][dt][i] = 0.f;
+            }
+        }
+        m[tt] = a.v_total >= 0.f ? 0.f : -INFINITY;
+        l[tt] = absent;
+    }
+
+    Producer<NPAD, SB, MAXI, MAXE> prod;
+    if (nb > 0) {
+        flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
+        prod.load(a, b, cbi, 0, kend, D);
+        __syncthreads();
+        prod.store(a, t0, cb, powt, meta_of(0), cdec_of(0), E_of(0), D);
+        if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
+        __syncthreads();
+    }
+
+    for (int bi = 0; bi < nb; ++bi) {
+        const int cur = bi & 1;
+        if (bi + 1 < nb) prod.load(a, b, cbi, bi + 1, kend, D);
+        const __bf16* cdec = cdec_of(cur);
+        const float* E = E_of(cur);
+        const BatchMeta* meta = meta_of(bi);
+        for (int j = 0; j < SB; ++j) {
+            if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
+            bf16x8 cf[2][NS];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns)
+                    cf[tt][ns] = *reinterpret_cast<const bf16x8*>(
+                        cdec + (j * kTB + 16 * tt + c16) * S::CROW + 32 * ns + 8 * g);
+            f32x4 ek[DT], ev[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                ek[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 0) * D + h * HD + 16 * dt + 4 * g);
+                ev[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 1) * D + h * HD + 16 * dt + 4 * g);
+            }
+            f32x4 gt[2][DT];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cf[tt][ns], acc);
+                    gt[tt][dt] = acc;
+                }
+            float s[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                float sacc = 0.f;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float x = gt[tt][dt][i];
+                        float gv = x;
+                        if (a.silu) {
+                            const float ex = __builtin_amdgcn_exp2f(-x);
+                            gv = x * __builtin_amdgcn_rcpf(1.0f + ex);
+                        }
+                        gt[tt][dt][i] = gv;
+                        sacc = __builtin_fmaf(qs[tt][dt][i], ek[dt][i] * gv, sacc);
+                    }
+                sacc += __shfl_xor(sacc, 16);
+                sacc += __shfl_xor(sacc, 32);
+                s[tt] = sacc;
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const bool need = s[tt] > m[tt] + kTau;
+                if (__any(need)) {
+                    const float mn = need ? s[tt] : m[tt];
+                    const float alpha = __builtin_amdgcn_exp2f(m[tt] - mn);
+                    l[tt] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[tt][dt] *= alpha;
+                    m[tt] = mn;
+                }
+                const float p = __builtin_amdgcn_exp2f(s[tt] - m[tt]);
+                l[tt] += p;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[tt][dt][i] = __builtin_fmaf(p, ev[dt][i] * gt[tt][dt][i], o[tt][dt][i]);
+            }
+        }
+        if (bi + 1 < nb) {
+            prod.store(a, t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), E_of(cur ^ 1), D);
+            if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
+        }
+        __syncthreads();
+    }
+
+    // O = ln2 * o / l  (the gate carried a factor log2 e), LSE = ln2 * (m + log2 l).
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int t = t0 + 16 * tt + c16;
+        if (t >= a.L) continue;
+        const bool any = l[tt] > 0.f;
+        const float inv = any ? kLn2 / l[tt] : 0.f;
+        float* orow = a.O + (((int64_t)b * a.H + h) * a.L + t) * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const f32x4 v = o[tt][dt] * inv;
+            *reinterpret_cast<f32x4*>(orow + 16 * dt + 4 * g) = v;
+        }
+        if (g == 0)
+            a.LSE[((int64_t)b * a.H + h) * a.L + t] = any ? (m[tt] + __log2f(l[tt])) * kLn2 : -INFINITY;
+    }
+}
+
+template <int HD, int NS, int SB>
+static size_t fwd_lds_bytes(int D) {
+    return 2 * Stage<32 * NS, SB>::bytes(D) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
+           65 * 32 * NS * 4 + 16;
+}
+
+template <int HD, int NS, int SB>
+static int launch_fwd(const FlashArgs& a, hipStream_t st) {
+    const int D = a.H * HD;
+    const int nthr = 64 * a.H;
+    constexpr int NPAD = 32 * NS;
+    const int mi = (kTB * (NPAD / 4) + nthr - 1) / nthr;
+    const int nvec = SB * 2 * (D / 4);
+    const size_t lds = fwd_lds_bytes<HD, NS, SB>(D);
+    if (lds > 160 * 1024)
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: D=%d, N=%d needs %zu B of LDS", D, a.N, lds);
+    const int ntb = (a.L + kTB - 1) / kTB;
+    dim3 grid(a.B * ntb);
+#define MB_FWD(MI, ME)                                                                      \
+    do {                                                                                    \
+        auto k = flash_ema_fwd_kernel<HD, NS, SB, MI, ME>;                                  \
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+        if (e != hipSuccess) {                                                              \
+            (void)hipGetLastError();                                                        \
+            return fail((int)e, "mb_flash_ema_fwd: LDS attribute: %s", hipGetErrorString(e)); \
+        }                                                                                   \
+        hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, a);                                \
+    } while (0)
+    const int me = (nvec + nthr - 1) / nthr;
+    if (mi > 4 || me > 4)
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: D=%d, N=%d too wide for %d threads", D, a.N, nthr);
+    if (mi <= 1 && me <= 1) MB_FWD(1, 1);
+    else if (mi <= 1 && me <= 2) MB_FWD(1, 2);
+    else if (mi <= 2 && me <= 2) MB_FWD(2, 2);
+    else MB_FWD(4, 4);
+#undef MB_FWD
+    return check_launch("mb_flash_ema_fwd");
+}
+
+// Host-side validation shared with the backward entry point.
+int flash_validate(const char* who, const FlashArgs& a, int hd) {
+    MB_REQUIRE(a.B >= 0 && a.L >= 0 && a.K >= 0, "%s: negative B=%d, L=%d or K=%d", who, a.B, a.L, a.K);
+    MB_REQUIRE(a.H >= 1, "%s: H=%d must be >= 1", who, a.H);
+    MB_REQUIRE(a.N >= 1 && a.Np >= a.N, "%s: need 1 <= N=%d <= Np=%d", who, a.N, a.Np);
+    if (hd != 32 && hd != 64)
+        return fail(MB_ERR_UNSUPPORTED, "%s: head_dim %d (supported: 32, 64)", who, hd);
+    if (a.H < 4 || a.H > 8)
+        return fail(MB_ERR_UNSUPPORTED, "%s: %d heads (supported: 4..8, one wave per head)", who, a.H);
+    if (a.N > 128) return fail(MB_ERR_UNSUPPORTED, "%s: N=%d > 128", who, a.N);
+    MB_REQUIRE(a.Br >= 1, "%s: Br=%d must be >= 1", who, a.Br);
+    if (!(a.Br <= 32 || a.Br == 64))
+        return fail(MB_ERR_UNSUPPORTED, "%s: Br=%d (supported: <= 32 or 64)", who, a.Br);
+    const int nc_need = a.L > 0 ? (a.L + a.Br - 1) / a.Br : 1;
+    MB_REQUIRE(a.nc >= nc_need, "%s: C_bounds has %d chunks, L=%d with Br=%d needs %d", who, a.nc,
+               a.L, a.Br, nc_need);
+    return MB_OK;
+}
+
+}  // namespace mb
+
+using namespace mb;
+
+extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int64_t q_sl,
+                                int64_t q_sd, const int64_t* x, int64_t x_sb, int64_t x_sl,
+                                const float* E_k, const float* E_v, const float* W_pe,
+                                const float* rhos, const int64_t* unique, const float* C_bounds,
+                                int B, int H, int L, int hd, int K, int N, int Np, int nc, int Br,
+                                int64_t V_total, int flags, float* O, float* LSE, void* stream) {
+    FlashArgs a{};
+    a.Q = Q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_sl = q_sl; a.q_sd = q_sd;
+    a.x = x; a.x_sb = x_sb; a.x_sl = x_sl;
+    a.Ek = E_k; a.Ev = E_v; a.W = W_pe; a.rhos = rhos; a.unique = unique; a.Cb = C_bounds;
+    a.B = B; a.H = H; a.L = L; a.hd = hd; a.K = K; a.N = N; a.Np = Np; a.Br = Br; a.nc = nc;
+    a.v_total = (flags & MB_FLASH_ABSENT_MASS) ? (float)V_total : -1.0f;
+    a.silu = (flags & MB_FLASH_SILU) ? 1 : 0;
+    a.O = O; a.LSE = LSE;
+    int rc = flash_validate("mb_flash_ema_fwd", a, hd);
+    if (rc) return rc;
+    if (B == 0 || L == 0) return MB_OK;
+    MB_REQUIRE(Q && x && rhos && unique && O && LSE && W_pe, "mb_flash_ema_fwd: null pointer");
+    MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_fwd: null slot pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const int NS = (N + 31) / 32;
+    if (hd == 64) {
+        if (NS == 1) return launch_fwd<64, 1, 4>(a, st);
+        if (NS == 2) return launch_fwd<64, 2, 4>(a, st);
+        return launch_fwd<64, 4, 2>(a, st);
+    }
+    if (NS == 1) return launch_fwd<32, 1, 4>(a, st);
+    if (NS == 2) return launch_fwd<32, 2, 4>(a, st);
+    return launch_fwd<32, 4, 2>(a, st);
+}

@@ -65,3 +65,56 @@ def _build_unique_index(x, device):
     pad = torch.arange(K_max, device=device).unsqueeze(0) >= counts.unsqueeze(1)
     out.masked_fill_(pad, -1)
     return out, K_max
+
+
+def _flash_flags(use_silu, absent_mass):
+    return (_lib.MB_FLASH_SILU if use_silu else 0) | (_lib.MB_FLASH_ABSENT_MASS if absent_mass else 0)
+
+
+def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
+                      C_bounds, use_silu=True, Br=64, absent_mass=True):
+    """Gated flash-EMA attention forward (triton_flash_ema.py:529-568).
+
+    Q [B, H, L, hd]; x [B, L]; E_k_active / E_v_active [B, K_max, H*hd]; W_pe [N, H*hd]
+    (pe_proj.weight.t()); rhos [N]; unique_tensor [B, K_max] (-1 = padding); C_bounds
+    from ``precompute_boundaries(x, unique_tensor, rhos, Br, c_init)``.  Float inputs are
+    used in fp32, as the reference's ``custom_fwd(cast_inputs=float32)`` does.
+
+    Returns (O [B, H, L, hd] fp32, LSE [B, H, L], C_bounds, E_k, E_v) with E_k/E_v viewed
+    [B, K_max, H, hd], as the reference does.  With ``absent_mass`` (the default) the
+    softmax covers all V_total slots as the dense PyTorch reference
+    (flash_ema_attention.py:76-77) does; ``absent_mass=False`` gives the Triton kernel's
+    softmax over the valid slots only (triton_flash_ema.py:215-229).
+    """
+    dev = _lib.require_gpu(Q, x, E_k_active, E_v_active, W_pe, rhos, unique_tensor, C_bounds,
+                           what="flash_ema_forward")
+    B, H, L, hd = Q.shape
+    K = unique_tensor.shape[1]
+    if K != K_max:
+        raise ValueError(f"unique_tensor has {K} slots but K_max={K_max}")
+    N = rhos.shape[0]
+    D = H * hd
+    Qf = Q.to(torch.float32)
+    Ek = E_k_active.to(torch.float32).contiguous()
+    Ev = E_v_active.to(torch.float32).contiguous()
+    if Ek.shape != (B, K, D) or Ev.shape != (B, K, D):
+        raise ValueError(f"E_k/E_v must be [B, K_max, H*hd] = {(B, K, D)}, got {tuple(Ek.shape)}")
+    W = W_pe.to(torch.float32).contiguous()
+    if W.shape[0] < N or W.shape[1] != D:
+        raise ValueError(f"W_pe must be [N, H*hd] = {(N, D)}, got {tuple(W.shape)}")
+    W = W[:N].contiguous()
+    rh = rhos.detach().to(torch.float32).contiguous()
+    uniq = unique_tensor.to(torch.int64).contiguous()
+    xl = x if x.dtype == torch.int64 else x.long()
+    Cb = C_bounds.to(torch.float32).contiguous()
+    if Cb.dim() != 4 or Cb.shape[0] != B or Cb.shape[2] != K or Cb.shape[3] < N:
+        raise ValueError(f"C_bounds must be [B, nc, K_max, >=N], got {tuple(Cb.shape)}")
+    O = torch.empty(B, H, L, hd, dtype=torch.float32, device=dev)
+    LSE = torch.empty(B, H, L, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("mb_flash_ema_fwd", _lib.ptr(Qf), *Qf.stride(), _lib.ptr(xl), xl.stride(0),
+                  xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W), _lib.ptr(rh),
+                  _lib.ptr(uniq), _lib.ptr(Cb), B, H, L, hd, K, N, Cb.shape[3], Cb.shape[1],
+                  int(Br), int(V_total), _flash_flags(use_silu, absent_mass), _lib.ptr(O),
+                  _lib.ptr(LSE), _lib.stream(dev))
+    return O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd)

@@ -14,8 +14,10 @@ Three forms of the same attention, all in torch on the CPU:
                is SiLU(0) = 0 and their score 0 -- folded into the softmax
                denominator as (V - K_b) * exp(0 - m).  ``absent_mass=False`` gives
                the Triton kernel as executed (triton_flash_ema.py:215-229 wipes the
-               absent mass).  ``gate_bf16=True`` rounds the gate operands to
-               bfloat16 as triton_flash_ema.py:188-190 does.
+               absent mass).  ``gate_round="bf16"`` rounds the gate operands to
+               bfloat16 as triton_flash_ema.py:188-190 does; ``gate_round="log2e"``
+               rounds c_dec and W_pe * log2(e) instead (the HIP kernel feeds the
+               MFMA the weights pre-scaled for its base-2 exponentials).
 ``sparse_backward_formulas``
                the reference's closed-form gradients (triton_flash_ema.py:336-350
                and :446-465), evaluated loop by loop; autograd of ``sparse`` must
@@ -66,8 +68,20 @@ def dense(Q, x, E_k_slots, E_v_slots, rhos, pe_weight, n_heads, use_silu=True, c
     return O.transpose(1, 2).reshape(B, L, D)                       # :84
 
 
+def _round_gate_operands(W, gate_round):
+    """W_pe as the gate GEMM sees it: exact, bf16-rounded, or bf16(W * log2 e) / log2 e."""
+    if gate_round is None:
+        return W
+    if gate_round == "bf16":
+        return W.to(torch.bfloat16).to(W.dtype)
+    if gate_round == "log2e":
+        l2e = 1.0 / math.log(2.0)
+        return (W.float() * l2e).to(torch.bfloat16).to(W.dtype) / l2e
+    raise ValueError(f"gate_round={gate_round!r}")
+
+
 def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=True,
-           absent_mass=True, gate_bf16=False, return_lse=False):
+           absent_mass=True, gate_round=None, return_lse=False):
     """Unique-slot flash-EMA attention.
 
     Q [B, H, L, hd]; x [B, L]; E_k / E_v [B, K, D]; W_pe [N, D] (= pe_proj.weight.T);
@@ -88,16 +102,14 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
     C = torch.zeros(B, K, N, dtype=dt) if c_init is None else c_init[:, :, :N].to(dt)
     C = C * valid.unsqueeze(-1).to(dt)
     rho = rhos.to(dt).reshape(1, 1, N)
-    W = W_pe[:N].to(dt)
-    if gate_bf16:
-        W = W.to(torch.bfloat16).to(dt)
+    W = _round_gate_operands(W_pe[:N].to(dt), gate_round)
     Ek = E_k.reshape(B, K, H, hd).to(dt)
     Ev = E_v.reshape(B, K, H, hd).to(dt)
     log_absent = torch.log((V_total - Kb).clamp(min=0).to(dt))       # -inf if none absent
     outs, lses = [], []
     for t in range(L):
         c_dec = C * rho
-        cg = c_dec.to(torch.bfloat16).to(dt) if gate_bf16 else c_dec
+        cg = c_dec.float().to(torch.bfloat16).to(dt) if gate_round else c_dec
         pre = (cg @ W).reshape(B, K, H, hd)
         g = F.silu(pre) if use_silu else pre
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]

@@ -1,0 +1,203 @@
+"""Pins the CPU oracle of flash-EMA attention (oracle/attention.py).
+
+The reference has no test of attention values (its tests pin only the scans), so the
+oracle is pinned by what the mathematics fixes:
+  * the dense restatement of flash_ema_attention.flash_ema_forward equals the unique-slot
+    form plus the (V - K_b) absent-slot mass, exactly (absent slots have zero counters,
+    hence gate SiLU(0) = 0, score 0 and value 0);
+  * with no decay and no occurrences the gate is constant in time, and the attention is
+    torch's scaled_dot_product_attention on gated keys/values;
+  * all-zero counters give a uniform softmax and a zero output;
+  * a one-slot case evaluated by hand with the math module;
+  * float64 gradcheck of the oracle, and autograd == the reference's closed-form
+    gradients (mathbrain/triton_flash_ema.py:336-350, 446-465).
+"""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as att
+
+
+def _problem(seed, B=2, L=10, V=24, H=2, hd=4, N=3, extra=3, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randint(0, V // 2, (B, L), generator=g)
+    E_k_slots = torch.randn(V, H * hd, generator=g, dtype=dtype) * 0.5
+    E_v_slots = torch.randn(V, H * hd, generator=g, dtype=dtype) * 0.5
+    pe_weight = torch.randn(H * hd, N, generator=g, dtype=dtype) * 0.7
+    rhos = torch.tensor([0.5, 0.9, 0.99][:N], dtype=dtype)
+    Q = torch.randn(B, L, H * hd, generator=g, dtype=dtype)
+    slots = []
+    for b in range(B):
+        s = torch.unique(x[b])
+        hist = torch.arange(V // 2, V // 2 + extra)  # history-only slots
+        slots.append(torch.cat([s, hist]))
+    K = max(s.numel() for s in slots) + 2
+    unique = torch.full((B, K), -1, dtype=torch.int64)
+    c_init = torch.zeros(B, K, N, dtype=dtype)
+    for b, s in enumerate(slots):
+        unique[b, :s.numel()] = s
+        c_init[b, :s.numel()] = torch.rand(s.numel(), N, generator=g, dtype=dtype) * 3
+    E_k = E_k_slots[unique.clamp(min=0)]
+    E_v = E_v_slots[unique.clamp(min=0)]
+    return dict(x=x, E_k_slots=E_k_slots, E_v_slots=E_v_slots, pe_weight=pe_weight, rhos=rhos,
+                Q=Q, unique=unique, c_init=c_init, E_k=E_k, E_v=E_v, V=V, H=H, hd=hd)
+
+
+def _sparse(p, **kw):
+    B, L, D = p["Q"].shape
+    Qh = p["Q"].reshape(B, L, p["H"], p["hd"]).transpose(1, 2)
+    return att.sparse(Qh, p["x"], p["E_k"], p["E_v"], p["pe_weight"].t(), p["rhos"], p["V"],
+                      p["unique"], p["c_init"], **kw)
+
+
+def _to_bld(O):
+    B, H, L, hd = O.shape
+    return O.transpose(1, 2).reshape(B, L, H * hd)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("use_silu", [True, False])
+def test_dense_equals_sparse_plus_absent_mass(seed, use_silu):
+    p = _problem(seed)
+    cg = att.scatter_c_global(p["unique"], p["c_init"], p["V"])
+    dense = att.dense(p["Q"], p["x"], p["E_k_slots"], p["E_v_slots"], p["rhos"], p["pe_weight"],
+                      p["H"], use_silu=use_silu, c_global=cg)
+    sparse = _to_bld(_sparse(p, use_silu=use_silu))
+    assert torch.allclose(dense, sparse, rtol=1e-12, atol=1e-14)
+    # dropping the absent mass (the Triton kernel as executed) is a different function
+    triton_like = _to_bld(_sparse(p, use_silu=use_silu, absent_mass=False))
+    assert not torch.allclose(dense, triton_like, rtol=1e-3)
+
+
+def test_dense_from_zero_state_is_the_reference_as_written():
+    # flash_ema_attention.py:36 starts from C_global = 0; c_global=None must do the same
+    p = _problem(4)
+    a = att.dense(p["Q"], p["x"], p["E_k_slots"], p["E_v_slots"], p["rhos"], p["pe_weight"], p["H"])
+    b = att.dense(p["Q"], p["x"], p["E_k_slots"], p["E_v_slots"], p["rhos"], p["pe_weight"], p["H"],
+                  c_global=torch.zeros(2, p["V"], 3, dtype=torch.float64))
+    assert torch.equal(a, b)
+
+
+def test_no_absent_slots_when_all_tokens_are_slots():
+    p = _problem(5)
+    p["V"] = int(p["unique"].max()) + 1
+    # every id < V is a slot of row 0? not necessarily; use a row whose slots cover 0..V-1
+    V = p["V"]
+    B, K = p["unique"].shape
+    allslots = torch.arange(V)
+    p["unique"] = torch.cat([allslots.expand(B, V), torch.full((B, 1), -1)], 1)
+    g = torch.Generator().manual_seed(7)
+    p["c_init"] = torch.rand(B, V + 1, 3, generator=g, dtype=torch.float64)
+    p["c_init"][:, -1] = 0
+    p["E_k"] = p["E_k_slots"][p["unique"].clamp(min=0)]
+    p["E_v"] = p["E_v_slots"][p["unique"].clamp(min=0)]
+    a = _sparse(p, absent_mass=True)
+    b = _sparse(p, absent_mass=False)
+    assert torch.allclose(a, b, rtol=1e-13)
+
+
+@pytest.mark.parametrize("absent", [True, False])
+def test_constant_gate_reduces_to_sdpa(absent):
+    # rho = 1 and no slot token ever occurs in x: c_dec = c0 for all t, so the gate is
+    # constant in time and the attention is plain softmax attention on gated keys/values.
+    p = _problem(6, N=1)
+    p["rhos"] = torch.ones(1, dtype=torch.float64)
+    p["x"] = torch.full_like(p["x"], p["V"] + 5)  # never a slot
+    B, L, D = p["Q"].shape
+    H, hd = p["H"], p["hd"]
+    O = _sparse(p, absent_mass=absent)
+    valid = p["unique"] >= 0
+    for b in range(B):
+        k = int(valid[b].sum())
+        g = F.silu(p["c_init"][b, :k] @ p["pe_weight"].t())           # [k, D]
+        Kg = (p["E_k"][b, :k] * g).reshape(k, H, hd).transpose(0, 1)  # [H, k, hd]
+        Vg = (p["E_v"][b, :k] * g).reshape(k, H, hd).transpose(0, 1)
+        if absent:
+            n_abs = p["V"] - k
+            Kg = torch.cat([Kg, torch.zeros(H, n_abs, hd, dtype=Kg.dtype)], 1)
+            Vg = torch.cat([Vg, torch.zeros(H, n_abs, hd, dtype=Vg.dtype)], 1)
+        q = p["Q"][b].reshape(L, H, hd).transpose(0, 1)
+        want = F.scaled_dot_product_attention(q, Kg, Vg)                # [H, L, hd]
+        assert torch.allclose(O[b], want, rtol=1e-10, atol=1e-12)
+
+
+def test_zero_counters_give_uniform_softmax_and_zero_output():
+    p = _problem(8)
+    p["c_init"].zero_()
+    p["x"] = torch.full_like(p["x"], p["V"] + 1)
+    O, LSE = _sparse(p, return_lse=True)
+    assert torch.count_nonzero(O) == 0
+    assert torch.allclose(LSE, torch.full_like(LSE, math.log(p["V"])))
+    O2, LSE2 = _sparse(p, absent_mass=False, return_lse=True)
+    kb = (p["unique"] >= 0).sum(1).to(torch.float64)
+    assert torch.allclose(LSE2, torch.log(kb).reshape(-1, 1, 1).expand_as(LSE2))
+
+
+def test_one_slot_by_hand():
+    # B=H=hd=N=1, V=2 (one absent slot), slot u=5 with c0=1, rho=0.5, W=2, e_k=3, e_v=4,
+    # x = [5, 7], q = [1, 2]
+    def silu(z):
+        return z / (1.0 + math.exp(-z))
+    want = []
+    c = 1.0
+    for t, (xt, q) in enumerate([(5, 1.0), (7, 2.0)]):
+        c_dec = c * 0.5
+        g = silu(2.0 * c_dec)
+        s = q * 3.0 * g
+        p = math.exp(s) / (math.exp(s) + 1.0)
+        want.append(p * 4.0 * g)
+        c = c_dec + (1.0 if xt == 5 else 0.0)
+    dt = torch.float64
+    O = att.sparse(torch.tensor([1.0, 2.0], dtype=dt).reshape(1, 1, 2, 1), torch.tensor([[5, 7]]),
+                   torch.tensor([[[3.0]]], dtype=dt), torch.tensor([[[4.0]]], dtype=dt),
+                   torch.tensor([[2.0]], dtype=dt), torch.tensor([0.5], dtype=dt), 2,
+                   torch.tensor([[5]]), torch.tensor([[[1.0]]], dtype=dt))
+    assert torch.allclose(O.flatten(), torch.tensor(want, dtype=dt), rtol=1e-14)
+
+
+def test_gate_rounding_modes_stay_close():
+    p = _problem(9, dtype=torch.float64)
+    exact = _sparse(p)
+    for mode in ("bf16", "log2e"):
+        r = _sparse(p, gate_round=mode)
+        assert (r - exact).abs().max() / exact.abs().max() < 2e-2
+
+
+@pytest.mark.parametrize("use_silu", [True, False])
+@pytest.mark.parametrize("absent", [True, False])
+def test_oracle_gradcheck(use_silu, absent):
+    p = _problem(10, B=1, L=5, V=12, H=2, hd=2, N=2, extra=1)
+    B, L, D = p["Q"].shape
+    Qh = p["Q"].reshape(B, L, 2, 2).transpose(1, 2).contiguous().requires_grad_()
+    Ek = p["E_k"].clone().requires_grad_()
+    Ev = p["E_v"].clone().requires_grad_()
+    W = p["pe_weight"].t().contiguous().requires_grad_()
+
+    def f(q, ek, ev, w):
+        return att.sparse(q, p["x"], ek, ev, w, p["rhos"], p["V"], p["unique"], p["c_init"],
+                          use_silu=use_silu, absent_mass=absent)
+    assert torch.autograd.gradcheck(f, (Qh, Ek, Ev, W), eps=1e-6, atol=1e-8, rtol=1e-6)
+
+
+@pytest.mark.parametrize("seed", [0, 3])
+@pytest.mark.parametrize("absent", [True, False])
+def test_autograd_equals_reference_gradient_formulas(seed, absent):
+    p = _problem(seed)
+    B, L, D = p["Q"].shape
+    H, hd = p["H"], p["hd"]
+    Qh = p["Q"].reshape(B, L, H, hd).transpose(1, 2).contiguous().requires_grad_()
+    Ek = p["E_k"].clone().requires_grad_()
+    Ev = p["E_v"].clone().requires_grad_()
+    W = p["pe_weight"].t().contiguous().requires_grad_()
+    O = att.sparse(Qh, p["x"], Ek, Ev, W, p["rhos"], p["V"], p["unique"], p["c_init"],
+                   absent_mass=absent)
+    dO = torch.randn(O.shape, generator=torch.Generator().manual_seed(seed + 100), dtype=O.dtype)
+    O.backward(dO)
+    dQ, dEk, dEv, dW = att.sparse_backward_formulas(
+        Qh.detach(), p["x"], p["E_k"], p["E_v"], W.detach(), p["rhos"], p["V"], p["unique"], dO,
+        p["c_init"], absent_mass=absent)
+    for got, want in ((Qh.grad, dQ), (Ek.grad, dEk), (Ev.grad, dEv), (W.grad, dW)):
+        assert torch.allclose(got, want, rtol=1e-10, atol=1e-12)
