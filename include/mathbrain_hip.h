@@ -127,6 +127,30 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
                      int K, int N, int Np, int nc, int Br, int64_t V_total, int flags, float *O,
                      float *LSE, void *stream);
 
+/*
+ * Flash-EMA gated cross-attention backward.  Replaces FlashEMAFunction.backward and its
+ * kernels _flash_ema_bwd_dq_de / _flash_ema_bwd_dw (mathbrain/triton_flash_ema.py:586-650,
+ * :250-355, :359-469) with one fused pass.  Arguments as mb_flash_ema_fwd, plus
+ *
+ *   dO        [B, H, L, hd] fp32, same element strides as Q
+ *   O, LSE    the forward's outputs (contiguous)
+ *   dQ        [B, H, L, hd] fp32 contiguous output
+ *   dE_k/dE_v [B, K, H*hd] fp32 contiguous outputs (zero for padding slots)
+ *   dW_pe     [N, H*hd] fp32 contiguous output
+ *
+ * The outputs are cleared by the call (with a fill kernel, no memset) and then
+ * accumulated with fp32 atomics, so the summation order of dE_k, dE_v and dW_pe is not
+ * fixed, as in the reference's tl.atomic_add.  Supported: as mb_flash_ema_fwd with H a
+ * multiple of 4.
+ */
+int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,
+                     const float *dO, const int64_t *x, int64_t x_sb, int64_t x_sl,
+                     const float *E_k, const float *E_v, const float *W_pe, const float *rhos,
+                     const int64_t *unique, const float *C_bounds, const float *O,
+                     const float *LSE, int B, int H, int L, int hd, int K, int N, int Np, int nc,
+                     int Br, int64_t V_total, int flags, float *dQ, float *dE_k, float *dE_v,
+                     float *dW_pe, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,7 @@ DEVICE_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-mcode-object-version=5",
+    "-munsafe-fp-atomics",  # float atomicAdd -> global_atomic_add_f32 / ds_add_f32, not a CAS loop
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]

@@ -1,0 +1,413 @@
+// Flash-EMA gated cross-attention backward on gfx950.
+//
+// Replaces FlashEMAFunction.backward and its kernels _flash_ema_bwd_dq_de and
+// _flash_ema_bwd_dw (mathbrain/triton_flash_ema.py:586-650, :250-355, :359-469) with one
+// fused pass that recomputes the gate once.  With D_t = dO_t . O_t and, per step t and
+// valid slot k,
+//   p = exp(s - LSE_t),  dp = dO_t . (e_v * g),  ds = p (dp - D_t)
+//   dQ_t  += ds e_k * g / sqrt(hd)          dE_k[k] += ds q_t * g / sqrt(hd)
+//   dE_v[k] += p dO_t * g
+//   dpre  = (ds q_t * e_k / sqrt(hd) + p dO_t * e_v) * SiLU'(pre)
+//   dW_pe[:, h] += c_dec^T dpre             (bf16 operands, fp32 accumulate)
+// (the reference's formulas, triton_flash_ema.py:336-350 and :446-465).
+//
+// Layout: one workgroup per (b, 32-step block, group of 4 heads); wave w takes head
+// w % 4 of the group and 16-step half w / 4.  The gate is computed as
+// pre[t, d] = c_dec[t, :] W[:, d], so each lane owns one dim d (lane % 16 of a 16-dim
+// tile, 4 tiles) and steps 4*(lane/16) + i: the sums over t (dE_k, dE_v, and dW through
+// a second MFMA fed straight from the gate tile's registers) stay in registers, dQ
+// accumulates in registers across the slot loop, and only the scores s and dp need a
+// sum over the 16 lanes of a DPP row.  dE_k/dE_v of a batch are combined over the two
+// half-waves in LDS and added to global memory with one atomic per element; dW is added
+// once per wave at the end.
+#include "flash_common.h"
+
+#include <algorithm>
+
+namespace mb {
+
+constexpr int kBwdHeads = 4;  // heads per workgroup
+// Batch slot info ring: batch i-1's info is still read (dE flush) while a fast wave
+// already writes batch i+2's, so four entries.
+constexpr int kMetaRing = 4;
+
+__global__ void zero_fill_kernel(float* p, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.f;
+}
+
+static int zero_fill(float* p, int64_t n, hipStream_t st) {
+    if (n <= 0) return MB_OK;
+    const int blocks = (int)std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, st, p, n);
+    return check_launch("zero fill");
+}
+
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU>
+__global__ void __launch_bounds__(512, 1)
+flash_ema_bwd_kernel(FlashArgs a) {
+    constexpr int NPAD = 32 * NS;
+    constexpr int DT = HD / 16;
+    constexpr int NT = NPAD / 16;
+    constexpr int WID = kBwdHeads * HD;  // embedding columns of this head group
+    using S = Stage<NPAD, SB>;
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int D = a.H * HD;
+    const int ntb = (a.L + kTB - 1) / kTB;
+    const int logical = xcd_major(blockIdx.x, gridDim.x);
+    const int hg = logical % a.head_groups;
+    const int b = logical / (a.head_groups * ntb);
+    const int t0 = ((logical / a.head_groups) % ntb) * kTB;
+    const int cbi = t0 / a.Br;
+    const int cb = cbi * a.Br;
+
+    // LDS: 2 staging buffers | 2 dE accumulators [SB][2][WID] | W fragments | meta ring |
+    // window | power table | slot info
+    const int stage_bytes = (int)S::bytes(WID);
+    const int acc_floats = SB * 2 * WID;
+    float* dEacc = reinterpret_cast<float*>(smem + 2 * stage_bytes);
+    bf16x8* wfr = reinterpret_cast<bf16x8*>(dEacc + 2 * acc_floats);
+    BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + kBwdHeads * DT * NS * 64);
+    int64_t* win = reinterpret_cast<int64_t*>(metas + kMetaRing * SB);
+    float* powt = reinterpret_cast<float*>(win + kMaxWin);
+    int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
+#define cdec_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes)
+#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define meta_of(batch) (metas + ((batch) % kMetaRing) * SB)
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int c16 = lane & 15;
+    const int g = lane >> 4;
+    const int hl = wave & 3;
+    const int th = wave >> 2;
+    const int h = hg * kBwdHeads + hl;
+
+    // Gate weights as the B operand: W[n = 32 ns + 8 g + e][d = 16 dt + c16] * log2 e,
+    // one fragment per (head, dt, ns, lane) in LDS.
+    for (int f = threadIdx.x; f < kBwdHeads * DT * NS * 64; f += blockDim.x) {
+        const int ln = f & 63;
+        const int ns = (f >> 6) % NS;
+        const int dt = ((f >> 6) / NS) % DT;
+        const int hh = (f >> 6) / (NS * DT);
+        bf16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int n = 32 * ns + 8 * (ln >> 4) + e;
+            const float w = n < a.N
+                ? a.W[(int64_t)n * D + (hg * kBwdHeads + hh) * HD + 16 * dt + (ln & 15)] * kLog2e
+                : 0.f;
+            v[e] = (__bf16)w;
+        }
+        wfr[f] = v;
+    }
+    for (int i = threadIdx.x; i < 2 * acc_floats; i += blockDim.x) dEacc[i] = 0.f;
+    flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
+    const int kend = kinfo[1];
+    const int nb = (kend + SB - 1) / SB;
+
+    // Per-lane rows: steps t = t0 + 16 th + 4 g + i, dims d = 16 dt + c16 of head h.
+    const float qscale = 1.0f / sqrtf((float)HD);
+    float qs[DT][4], dov[DT][4], dq[DT][4];
+    float lse2[4], Dv[4];
+    {
+        float dsum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = t0 + 16 * th + 4 * g + i;
+            const bool ok = t < a.L;
+            const int64_t qoff = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)t * a.q_sl;
+            const int64_t ooff = (((int64_t)b * a.H + h) * a.L + t) * HD;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int d = 16 * dt + c16;
+                qs[dt][i] = ok ? a.Q[qoff + (int64_t)d * a.q_sd] * qscale : 0.f;
+                dov[dt][i] = ok ? a.dO[qoff + (int64_t)d * a.q_sd] : 0.f;
+                dq[dt][i] = 0.f;
+                if (ok) dsum[i] = __builtin_fmaf(dov[dt][i], a.Oin[ooff + d], dsum[i]);
+            }
+            lse2[i] = ok ? a.LSEin[((int64_t)b * a.H + h) * a.L + t] * kLog2e : INFINITY;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Dv[i] = row_sum16(dsum[i]);
+    }
+    f32x4 dWacc[DT][NT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) dWacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    Producer<NPAD, SB, MAXI, MAXE> prod;
+    const int col0 = hg * WID;
+    if (nb > 0) {
+        flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
+        prod.load(a, b, cbi, 0, kend, D, col0, WID);
+        __syncthreads();
+        prod.store(a, t0, cb, powt, meta_of(0), cdec_of(0), E_of(0), WID);
+        if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
+        __syncthreads();
+    }
+
+    for (int bi = 0; bi < nb; ++bi) {
+        const int cur = bi & 1;
+        if (bi + 1 < nb) prod.load(a, b, cbi, bi + 1, kend, D, col0, WID);
+        // Flush the previous batch's dE sums (complete after the last barrier).
+        if (bi > 0) {
+            float* acc = dEacc + (cur ^ 1) * acc_floats;
+            for (int i = threadIdx.x; i < acc_floats; i += blockDim.x) {
+                const int j = i / (2 * WID);
+                const int which = (i / WID) & 1;
+                const int c = i % WID;
+                const int k = (bi - 1) * SB + j;
+                if (meta_of(bi - 1)[j].u >= 0) {
+                    float* dst = (which ? a.dEv : a.dEk) + ((int64_t)b * a.K + k) * D + col0 + c;
+                    atomicAdd(dst, acc[i] * kLn2);
+                }
+                acc[i] = 0.f;
+            }
+        }
+        const __bf16* cdec = cdec_of(cur);
+        const float* E = E_of(cur);
+        const BatchMeta* meta = meta_of(bi);
+        float* acc = dEacc + cur * acc_floats;
+        for (int j = 0; j < SB; ++j) {
+            if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
+            const __bf16* crow = cdec + (j * kTB + 16 * th) * S::CROW;
+            bf16x8 cf[NS];
+#pragma unroll
+            for (int ns = 0; ns < NS; ++ns)
+                cf[ns] = *reinterpret_cast<const bf16x8*>(crow + c16 * S::CROW + 32 * ns + 8 * g);
+            float ek[DT], ev[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                ek[dt] = E[(j * 2 + 0) * WID + hl * HD + 16 * dt + c16];
+                ev[dt] = E[(j * 2 + 1) * WID + hl * HD + 16 * dt + c16];
+            }
+            f32x4 g2[DT], sg[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                f32x4 accg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns)
+                    accg = mfma16x16x32(cf[ns], wfr[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
+                g2[dt] = accg;
+            }
+            // Phase 1: gate, score and dO . v partial sums over this lane's dims.
+            float s[4] = {0.f, 0.f, 0.f, 0.f}, dp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float x = g2[dt][i];  // pre * log2 e
+                    float sig = 1.f, gv = x;
+                    if (SILU) {
+                        sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x));
+                        gv = x * sig;
+                    }
+                    g2[dt][i] = gv;  // g * log2 e
+                    sg[dt][i] = sig;
+                    s[i] = __builtin_fmaf(qs[dt][i] * ek[dt], gv, s[i]);
+                    dp[i] = __builtin_fmaf(dov[dt][i] * ev[dt], gv, dp[i]);
+                }
+            float p[4], ds[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s2 = row_sum16(s[i]);               // score * log2 e
+                const float dpt = row_sum16(dp[i]) * kLn2;      // dO . v
+                p[i] = __builtin_amdgcn_exp2f(s2 - lse2[i]);
+                ds[i] = p[i] * (dpt - Dv[i]);
+            }
+            // Phase 2: gradients.
+            float dEk[DT], dEv[DT];
+            bf16x4 dpre[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                dEk[dt] = 0.f;
+                dEv[dt] = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float gv = g2[dt][i];
+                    const float u = ds[i] * gv;
+                    dq[dt][i] = __builtin_fmaf(u, ek[dt], dq[dt][i]);
+                    dEk[dt] = __builtin_fmaf(u, qs[dt][i], dEk[dt]);
+                    const float w = p[i] * gv;
+                    dEv[dt] = __builtin_fmaf(w, dov[dt][i], dEv[dt]);
+                    const float av = __builtin_fmaf(ds[i], qs[dt][i] * ek[dt], p[i] * (dov[dt][i] * ev[dt]));
+                    float dsil = 1.f;
+                    if (SILU) {
+                        const float sig = sg[dt][i];
+                        dsil = __builtin_fmaf(gv * kLn2, 1.0f - sig, sig);
+                    }
+                    dpre[dt][i] = (__bf16)(av * dsil);
+                }
+            }
+            // dE partial sums over this lane's 4 steps -> over the 4 row groups -> LDS.
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                dEk[dt] += __shfl_xor(dEk[dt], 16);
+                dEk[dt] += __shfl_xor(dEk[dt], 32);
+                dEv[dt] += __shfl_xor(dEv[dt], 16);
+                dEv[dt] += __shfl_xor(dEv[dt], 32);
+            }
+            // group g adds dim tile dt == g (DT == 4) or dt == g % DT with g < DT
+            if (g < DT) {
+                float vk = dEk[0], vv = dEv[0];
+#pragma unroll
+                for (int dt = 1; dt < DT; ++dt)
+                    if (g == dt) {
+                        vk = dEk[dt];
+                        vv = dEv[dt];
+                    }
+                atomicAdd(&acc[(j * 2 + 0) * WID + hl * HD + 16 * g + c16], vk);
+                atomicAdd(&acc[(j * 2 + 1) * WID + hl * HD + 16 * g + c16], vv);
+            }
+            // dW^T[d, n] += dpre^T[d, t] c_dec[t, n]: A = dpre (rows d, k = this lane's
+            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16].
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                bf16x4 cb4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) cb4[e] = crow[(4 * g + e) * S::CROW + 16 * nt + c16];
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
+            }
+        }
+        if (bi + 1 < nb) {
+            prod.store(a, t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), E_of(cur ^ 1), WID);
+            if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
+        }
+        __syncthreads();
+    }
+    if (nb > 0) {
+        const int last = nb - 1;
+        float* acc = dEacc + (last & 1) * acc_floats;
+        for (int i = threadIdx.x; i < acc_floats; i += blockDim.x) {
+            const int j = i / (2 * WID);
+            const int which = (i / WID) & 1;
+            const int c = i % WID;
+            const int k = last * SB + j;
+            if (meta_of(last)[j].u >= 0) {
+                float* dst = (which ? a.dEv : a.dEk) + ((int64_t)b * a.K + k) * D + col0 + c;
+                atomicAdd(dst, acc[i] * kLn2);
+            }
+        }
+    }
+
+    // dQ (the gate carried log2 e, the query 1/sqrt(hd)) and dW.
+    const float qf = kLn2 * qscale;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 16 * th + 4 * g + i;
+        if (t >= a.L) continue;
+        float* dst = a.dQ + (((int64_t)b * a.H + h) * a.L + t) * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) dst[16 * dt + c16] = dq[dt][i] * qf;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n = 16 * nt + c16;
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                atomicAdd(&a.dW[(int64_t)n * D + h * HD + 16 * dt + 4 * g + i], dWacc[dt][nt][i]);
+        }
+#undef cdec_of
+#undef E_of
+#undef meta_of
+}
+
+template <int HD, int NS, int SB>
+static size_t bwd_lds_bytes() {
+    constexpr int WID = kBwdHeads * HD;
+    return 2 * Stage<32 * NS, SB>::bytes(WID) + 2 * (size_t)SB * 2 * WID * 4 +
+           (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
+           kMaxWin * 8 + 65 * 32 * NS * 4 + 16;
+}
+
+template <int HD, int NS, int SB>
+static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
+    FlashArgs a = a0;
+    a.head_groups = a.H / kBwdHeads;
+    constexpr int NPAD = 32 * NS;
+    constexpr int WID = kBwdHeads * HD;
+    const int nthr = 64 * 2 * kBwdHeads;
+    const int mi = (kTB * (NPAD / 4) + nthr - 1) / nthr;
+    const int me = (SB * 2 * (WID / 4) + nthr - 1) / nthr;
+    const size_t lds = bwd_lds_bytes<HD, NS, SB>();
+    if (lds > 160 * 1024)
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: hd=%d, N=%d needs %zu B of LDS", HD, a.N, lds);
+    const int ntb = (a.L + kTB - 1) / kTB;
+    dim3 grid(a.B * ntb * a.head_groups);
+#define MB_BWD(MI, ME)                                                                      \
+    do {                                                                                    \
+        auto k = a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true>                   \
+                        : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false>;                 \
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+        if (e != hipSuccess) {                                                              \
+            (void)hipGetLastError();                                                        \
+            return fail((int)e, "mb_flash_ema_bwd: LDS attribute: %s", hipGetErrorString(e)); \
+        }                                                                                   \
+        hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, a);                                \
+    } while (0)
+    if (mi <= 1 && me <= 1) MB_BWD(1, 1);
+    else if (mi <= 2 && me <= 1) MB_BWD(2, 1);
+    else if (mi <= 2 && me <= 2) MB_BWD(2, 2);
+    else return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: N=%d too wide", a.N);
+#undef MB_BWD
+    return check_launch("mb_flash_ema_bwd");
+}
+
+int flash_validate(const char* who, const FlashArgs& a, int hd);
+
+}  // namespace mb
+
+using namespace mb;
+
+extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int64_t q_sl,
+                                int64_t q_sd, const float* dO, const int64_t* x, int64_t x_sb,
+                                int64_t x_sl, const float* E_k, const float* E_v,
+                                const float* W_pe, const float* rhos, const int64_t* unique,
+                                const float* C_bounds, const float* O, const float* LSE, int B,
+                                int H, int L, int hd, int K, int N, int Np, int nc, int Br,
+                                int64_t V_total, int flags, float* dQ, float* dE_k, float* dE_v,
+                                float* dW_pe, void* stream) {
+    FlashArgs a{};
+    a.Q = Q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_sl = q_sl; a.q_sd = q_sd;
+    a.dO = dO; a.x = x; a.x_sb = x_sb; a.x_sl = x_sl;
+    a.Ek = E_k; a.Ev = E_v; a.W = W_pe; a.rhos = rhos; a.unique = unique; a.Cb = C_bounds;
+    a.Oin = O; a.LSEin = LSE;
+    a.B = B; a.H = H; a.L = L; a.hd = hd; a.K = K; a.N = N; a.Np = Np; a.Br = Br; a.nc = nc;
+    a.v_total = (flags & MB_FLASH_ABSENT_MASS) ? (float)V_total : -1.0f;
+    a.silu = (flags & MB_FLASH_SILU) ? 1 : 0;
+    a.dQ = dQ; a.dEk = dE_k; a.dEv = dE_v; a.dW = dW_pe;
+    int rc = flash_validate("mb_flash_ema_bwd", a, hd);
+    if (rc) return rc;
+    if (H % kBwdHeads)
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: H=%d must be a multiple of %d", H, kBwdHeads);
+    if (B == 0 || L == 0) return MB_OK;
+    MB_REQUIRE(Q && dO && x && rhos && unique && O && LSE && W_pe && dQ && dW_pe,
+               "mb_flash_ema_bwd: null pointer");
+    MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds && dE_k && dE_v), "mb_flash_ema_bwd: null slot pointer");
+    hipStream_t st = (hipStream_t)stream;
+    // dE_k, dE_v and dW_pe are accumulated with atomics.
+    const int64_t D = (int64_t)H * hd;
+    if ((rc = zero_fill(dQ, (int64_t)B * H * L * hd, st))) return rc;
+    if ((rc = zero_fill(dW_pe, (int64_t)N * D, st))) return rc;
+    if (K > 0) {
+        if ((rc = zero_fill(dE_k, (int64_t)B * K * D, st))) return rc;
+        if ((rc = zero_fill(dE_v, (int64_t)B * K * D, st))) return rc;
+    }
+    const int NS = (N + 31) / 32;
+    if (hd == 64) {
+        if (NS == 1) return launch_bwd<64, 1, 4>(a, st);
+        if (NS == 2) return launch_bwd<64, 2, 4>(a, st);
+        return launch_bwd<64, 4, 2>(a, st);
+    }
+    if (NS == 1) return launch_bwd<32, 1, 4>(a, st);
+    if (NS == 2) return launch_bwd<32, 2, 4>(a, st);
+    return launch_bwd<32, 4, 2>(a, st);
+}

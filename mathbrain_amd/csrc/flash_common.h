@@ -54,8 +54,25 @@ struct FlashArgs {
     int head_groups;  // backward: workgroups per (b, block) along heads
 };
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
 __device__ inline f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 16x16x16 bf16 MFMA: A[row = lane%16][k = 4*(lane/16) + e], B[k][col = lane%16].
+__device__ inline f32x4 mfma16x16x16(bf16x4 a, bf16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane gets the sum.
+__device__ inline float row_sum16(float v) {
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false);  // row_mirror
+    return v;
 }
 
 // Workgroup id -> logical id so that consecutive logical ids (the blocks of one
@@ -71,8 +88,9 @@ template <int NPAD, int SB>
 struct Stage {
     static constexpr int CROW = NPAD + 8;  // bf16 per cdec row (16 B pad against conflicts)
     static constexpr int CDEC = SB * kTB * CROW;  // bf16 elements per buffer
-    __host__ __device__ static size_t bytes(int D) {
-        return (size_t)CDEC * 2 + (size_t)SB * 2 * D * 4;
+    // width: embedding columns staged per slot
+    __host__ __device__ static size_t bytes(int width) {
+        return (size_t)CDEC * 2 + (size_t)SB * 2 * width * 4;
     }
 };
 
@@ -147,7 +165,9 @@ struct Producer {
     float4 s[MAXI][SB];
     float4 e[MAXE];
 
-    __device__ void load(const FlashArgs& a, int b, int cbi, int bi, int kend, int D) {
+    // D: row length of E_k/E_v; the copy takes columns [col0, col0 + width).
+    __device__ void load(const FlashArgs& a, int b, int cbi, int bi, int kend, int D, int col0,
+                         int width) {
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
         const int nitems = kTB * (NPAD / 4);
@@ -173,19 +193,21 @@ struct Producer {
                 s[ii][j] = v;
             }
         }
-        const int nvec = SB * 2 * (D / 4);
+        const int w4 = width / 4;
+        const int nvec = SB * 2 * w4;
 #pragma unroll
         for (int ie = 0; ie < MAXE; ++ie) {
             const int i = tid + ie * nthr;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < nvec) {
-                const int j = i / (2 * (D / 4));
-                const int r = i % (2 * (D / 4));
-                const int which = r / (D / 4);
-                const int c4 = r % (D / 4);
+                const int j = i / (2 * w4);
+                const int r = i % (2 * w4);
+                const int which = r / w4;
+                const int c4 = r % w4;
                 const int k = bi * SB + j;
                 if (k < kend) {
-                    const float* src = (which ? a.Ev : a.Ek) + ((int64_t)b * a.K + k) * D + c4 * 4;
+                    const float* src =
+                        (which ? a.Ev : a.Ek) + ((int64_t)b * a.K + k) * D + col0 + c4 * 4;
                     v = *reinterpret_cast<const float4*>(src);
                 }
             }
@@ -193,9 +215,9 @@ struct Producer {
         }
     }
 
-    // Builds cdec and E of the batch into the staging buffer.
+    // Builds cdec and E ([SB][2][width]) of the batch into the staging buffer.
     __device__ void store(const FlashArgs& a, int t0, int cb, const float* powt,
-                          const BatchMeta* meta, __bf16* cdec, float* E, int D) {
+                          const BatchMeta* meta, __bf16* cdec, float* E, int width) {
         using S = Stage<NPAD, SB>;
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
@@ -230,7 +252,7 @@ struct Producer {
                 *reinterpret_cast<bf16x4*>(cdec + (j * kTB + tl) * S::CROW + n0) = w;
             }
         }
-        const int nvec = SB * 2 * (D / 4);
+        const int nvec = SB * 2 * (width / 4);
 #pragma unroll
         for (int ie = 0; ie < (MAXE); ++ie) {
             const int i = tid + ie * nthr;

@@ -24,7 +24,7 @@ namespace mb {
 
 constexpr float kTau = 8.0f;
 
-template <int HD, int NS, int SB, int MAXI, int MAXE>
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_fwd_kernel(FlashArgs a) {
     constexpr int NPAD = 32 * NS;
@@ -42,15 +42,14 @@ flash_ema_fwd_kernel(FlashArgs a) {
 
     // LDS: two staging buffers, a 3-deep ring of batch slot info (batch i+2's info is
     // written while batch i is still being read), the window, the power table.
-    const size_t stage_bytes = S::bytes(D);
-    unsigned char* bufs[2] = {smem, smem + stage_bytes};
+    const int stage_bytes = (int)S::bytes(D);
     BatchMeta* metas = reinterpret_cast<BatchMeta*>(smem + 2 * stage_bytes);
     int64_t* win = reinterpret_cast<int64_t*>(metas + 3 * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
-    auto cdec_of = [&](int i) { return reinterpret_cast<__bf16*>(bufs[i]); };
-    auto E_of = [&](int i) { return reinterpret_cast<float*>(bufs[i] + (size_t)S::CDEC * 2); };
-    auto meta_of = [&](int batch) { return metas + (batch % 3) * SB; };
+#define cdec_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes)
+#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define meta_of(batch) (metas + ((batch) % 3) * SB)
 
     flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
     const int kvalid = kinfo[0];
@@ -101,7 +100,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
     Producer<NPAD, SB, MAXI, MAXE> prod;
     if (nb > 0) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
-        prod.load(a, b, cbi, 0, kend, D);
+        prod.load(a, b, cbi, 0, kend, D, 0, D);
         __syncthreads();
         prod.store(a, t0, cb, powt, meta_of(0), cdec_of(0), E_of(0), D);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
@@ -110,7 +109,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
 
     for (int bi = 0; bi < nb; ++bi) {
         const int cur = bi & 1;
-        if (bi + 1 < nb) prod.load(a, b, cbi, bi + 1, kend, D);
+        if (bi + 1 < nb) prod.load(a, b, cbi, bi + 1, kend, D, 0, D);
         const __bf16* cdec = cdec_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
@@ -149,7 +148,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
                     for (int i = 0; i < 4; ++i) {
                         const float x = gt[tt][dt][i];
                         float gv = x;
-                        if (a.silu) {
+                        if (SILU) {
                             const float ex = __builtin_amdgcn_exp2f(-x);
                             gv = x * __builtin_amdgcn_rcpf(1.0f + ex);
                         }
@@ -203,6 +202,9 @@ flash_ema_fwd_kernel(FlashArgs a) {
         if (g == 0)
             a.LSE[((int64_t)b * a.H + h) * a.L + t] = any ? (m[tt] + __log2f(l[tt])) * kLn2 : -INFINITY;
     }
+#undef cdec_of
+#undef E_of
+#undef meta_of
 }
 
 template <int HD, int NS, int SB>
@@ -225,7 +227,8 @@ static int launch_fwd(const FlashArgs& a, hipStream_t st) {
     dim3 grid(a.B * ntb);
 #define MB_FWD(MI, ME)                                                                      \
     do {                                                                                    \
-        auto k = flash_ema_fwd_kernel<HD, NS, SB, MI, ME>;                                  \
+        auto k = a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true>                   \
+                        : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false>;                 \
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
         if (e != hipSuccess) {                                                              \

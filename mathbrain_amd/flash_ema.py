@@ -118,3 +118,76 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
                   int(Br), int(V_total), _flash_flags(use_silu, absent_mass), _lib.ptr(O),
                   _lib.ptr(LSE), _lib.stream(dev))
     return O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd)
+
+
+def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bounds, O, LSE, dO,
+                       use_silu=True, Br=64, absent_mass=True):
+    """Gradients of flash_ema_forward (triton_flash_ema.py:586-650) in one fused HIP pass.
+
+    E_k / E_v are [B, K, H*hd] or [B, K, H, hd]; returns (dQ [B,H,L,hd], dE_k [B,K,H*hd],
+    dE_v [B,K,H*hd], dW_pe [N, H*hd]), all fp32.
+    """
+    dev = _lib.require_gpu(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO,
+                           what="flash_ema_backward")
+    B, H, L, hd = Q.shape
+    K = unique_tensor.shape[1]
+    N = rhos.shape[0]
+    D = H * hd
+    Qf = Q.to(torch.float32)
+    dOf = dO.to(torch.float32)
+    if dOf.stride() != Qf.stride():
+        Qf = Qf.contiguous()
+        dOf = dOf.contiguous()
+    Ek = E_k.to(torch.float32).reshape(B, K, D).contiguous()
+    Ev = E_v.to(torch.float32).reshape(B, K, D).contiguous()
+    W = W_pe.to(torch.float32)[:N].contiguous()
+    rh = rhos.detach().to(torch.float32).contiguous()
+    uniq = unique_tensor.to(torch.int64).contiguous()
+    xl = x if x.dtype == torch.int64 else x.long()
+    Cb = C_bounds.to(torch.float32).contiguous()
+    Of = O.to(torch.float32).contiguous()
+    Lf = LSE.to(torch.float32).contiguous()
+    dQ = torch.empty(B, H, L, hd, dtype=torch.float32, device=dev)
+    dEk = torch.empty(B, K, D, dtype=torch.float32, device=dev)
+    dEv = torch.empty(B, K, D, dtype=torch.float32, device=dev)
+    dW = torch.empty(N, D, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("mb_flash_ema_bwd", _lib.ptr(Qf), *Qf.stride(), _lib.ptr(dOf), _lib.ptr(xl),
+                  xl.stride(0), xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W),
+                  _lib.ptr(rh), _lib.ptr(uniq), _lib.ptr(Cb), _lib.ptr(Of), _lib.ptr(Lf), B, H, L,
+                  hd, K, N, Cb.shape[3], Cb.shape[1], int(Br), int(V_total),
+                  _flash_flags(use_silu, absent_mass), _lib.ptr(dQ), _lib.ptr(dEk),
+                  _lib.ptr(dEv), _lib.ptr(dW), _lib.stream(dev))
+    return dQ, dEk, dEv, dW
+
+
+class FlashEMAFunction(torch.autograd.Function):
+    """Autograd entry point with the reference's 12 arguments (triton_flash_ema.py:571-650):
+    apply(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max, C_bounds,
+    use_silu=True, Br=64) -> O [B, H, L, hd].  Inputs are used in fp32 (the reference's
+    custom_fwd(cast_inputs=float32)); gradients flow to Q, E_k_active, E_v_active, W_pe."""
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float32)
+    def forward(ctx, Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
+                C_bounds, use_silu=True, Br=64):
+        O, LSE, C_bounds, E_k, E_v = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos,
+                                                       V_total, unique_tensor, K_max, C_bounds,
+                                                       use_silu, Br)
+        ctx.save_for_backward(Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE)
+        ctx.V_total = V_total
+        ctx.use_silu = use_silu
+        ctx.Br = Br
+        ctx.W_rows = W_pe.shape[0]
+        return O
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, dO):
+        Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE = ctx.saved_tensors
+        dQ, dEk, dEv, dW = flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, ctx.V_total,
+                                              unique_tensor, C_bounds, O, LSE, dO.contiguous(),
+                                              ctx.use_silu, ctx.Br)
+        if ctx.W_rows > dW.shape[0]:  # W_pe passed with padded rows: their gradient is 0
+            dW = torch.cat([dW, dW.new_zeros(ctx.W_rows - dW.shape[0], dW.shape[1])])
+        return dQ, None, dEk, dEv, dW, None, None, None, None, None, None, None

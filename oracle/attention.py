@@ -133,7 +133,7 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
 
 @torch.no_grad()
 def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_init=None,
-                             use_silu=True, absent_mass=True):
+                             use_silu=True, absent_mass=True, gate_round=None):
     """The reference's closed-form backward, loop by loop (float64 recommended).
 
     D = (dO*O).sum(-1) (triton_flash_ema.py:602); p = exp(s - LSE) (:336);
@@ -142,6 +142,8 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     dpre = (ds q/sqrt(hd)*e_k + p dO*e_v) * SiLU'(pre) (:453-461);
     dW_pe[:, head] = sum c_dec^T dpre (:465).
     Returns dQ [B,H,L,hd], dE_k [B,K,D], dE_v [B,K,D], dW_pe [N,D].
+    With ``gate_round`` the gate operands are rounded as in ``sparse`` and the dW_pe
+    product takes bf16 c_dec and bf16 dpre, as triton_flash_ema.py:463-465 does.
     """
     B, H, L, hd = Q.shape
     K = unique.shape[1]
@@ -149,15 +151,16 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     D = H * hd
     dt = Q.dtype
     O, LSE = sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init, use_silu,
-                    absent_mass, return_lse=True)
+                    absent_mass, gate_round=gate_round, return_lse=True)
     Dv = (dO * O).sum(-1)                                            # [B,H,L]
     valid = unique != -1
     C = torch.zeros(B, K, N, dtype=dt) if c_init is None else c_init[:, :, :N].to(dt)
     C = C * valid.unsqueeze(-1).to(dt)
     rho = rhos.to(dt).reshape(1, 1, N)
-    W = W_pe[:N].to(dt)
+    W = _round_gate_operands(W_pe[:N].to(dt), gate_round)
     Ek = E_k.reshape(B, K, H, hd).to(dt)
     Ev = E_v.reshape(B, K, H, hd).to(dt)
+    bf = (lambda v: v.float().to(torch.bfloat16).to(dt)) if gate_round else (lambda v: v)
     dQ = torch.zeros_like(Q)
     dEk = torch.zeros(B, K, H, hd, dtype=dt)
     dEv = torch.zeros(B, K, H, hd, dtype=dt)
@@ -165,7 +168,7 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     scale = 1.0 / math.sqrt(hd)
     for t in range(L):
         c_dec = C * rho
-        pre = (c_dec @ W).reshape(B, K, H, hd)
+        pre = (bf(c_dec) @ W).reshape(B, K, H, hd)
         g = F.silu(pre) if use_silu else pre
         gp = silu_grad(pre) if use_silu else torch.ones_like(pre)
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
@@ -178,7 +181,7 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
         dEk += ds.unsqueeze(-1) * q_t * g * scale
         dEv += p.unsqueeze(-1) * do_t * g
         dpre = (ds.unsqueeze(-1) * q_t * scale * Ek + p.unsqueeze(-1) * do_t * Ev) * gp
-        dW += torch.einsum("bkn,bkd->nd", c_dec, dpre.reshape(B, K, D))
+        dW += torch.einsum("bkn,bkd->nd", bf(c_dec), bf(dpre.reshape(B, K, D)))
         match = (x[:, t].unsqueeze(1) == unique) & valid
         C = c_dec + match.unsqueeze(-1).to(dt)
     return dQ, dEk.reshape(B, K, D), dEv.reshape(B, K, D), dW

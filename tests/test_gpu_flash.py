@@ -170,3 +170,102 @@ def test_fwd_rejects_unsupported_shapes():
     c["W"] = torch.randn(16, 192)
     with pytest.raises(HipKernelError, match="head_dim 48"):
         gpu_forward(c)
+
+
+# ---- backward ------------------------------------------------------------------------
+
+def gpu_backward(c, dO, use_silu=True, absent_mass=True):
+    from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward
+    cu = lambda t: t.cuda()
+    O, LSE, *_ = flash_ema_forward(cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]), cu(c["W"]),
+                                   cu(c["rhos"]), c["V"], cu(c["unique"]), c["K"], cu(c["Cb"]),
+                                   use_silu=use_silu, Br=c["Br"], absent_mass=absent_mass)
+    grads = flash_ema_backward(cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]), cu(c["W"]),
+                               cu(c["rhos"]), c["V"], cu(c["unique"]), cu(c["Cb"]), O, LSE, cu(dO),
+                               use_silu=use_silu, Br=c["Br"], absent_mass=absent_mass)
+    torch.cuda.synchronize()
+    return [t.cpu() for t in grads]
+
+
+def oracle_backward(c, dO, use_silu=True, absent_mass=True, gate_round=None):
+    dt = torch.float64
+    return att.sparse_backward_formulas(
+        c["Q"].to(dt), c["x"], c["E_k"].to(dt), c["E_v"].to(dt), c["W"].to(dt), c["rhos"].to(dt),
+        c["V"], c["unique"], dO.to(dt), c["c_base"].to(dt), use_silu=use_silu,
+        absent_mass=absent_mass, gate_round=gate_round)
+
+
+def check_backward(c, use_silu=True, absent_mass=True, exact=False, seed=0):
+    g = torch.Generator().manual_seed(seed + 77)
+    dO = torch.randn(c["Q"].shape, generator=g)
+    got = gpu_backward(c, dO, use_silu, absent_mass)
+    want = oracle_backward(c, dO, use_silu, absent_mass, gate_round="log2e")
+    names = ("dQ", "dE_k", "dE_v", "dW_pe")
+    errs = [norm_err(a, b) for a, b in zip(got, want)]
+    msg = ", ".join(f"{n} {e:.2e}" for n, e in zip(names, errs))
+    if exact:
+        ex = [norm_err(a, b) for a, b in zip(got, oracle_backward(c, dO, use_silu, absent_mass))]
+        msg += " | exact: " + ", ".join(f"{n} {e:.2e}" for n, e in zip(names, ex))
+        assert max(ex) < TOL_BF16, msg
+    print(msg)
+    for t in got:
+        assert torch.isfinite(t).all()
+    assert max(errs) < TOL_KERNEL_ROUNDING, msg
+    # padding slots get no gradient
+    pad = c["unique"] < 0
+    assert torch.count_nonzero(got[1][pad]) == 0 and torch.count_nonzero(got[2][pad]) == 0
+
+
+def test_bwd_cfg1():
+    check_backward(make_case(2, 128, 1000, 4, 32, 16, warmup=512, seed=3, min_hl=4, max_hl=1024))
+
+
+def test_bwd_cfg1_exact():
+    check_backward(make_case(2, 128, 1000, 4, 32, 16, uniform=True, min_hl=4, max_hl=1024, **CFG),
+                   exact=True)
+
+
+@pytest.mark.parametrize("N", [16, 64, 128])
+def test_bwd_rates(N):
+    check_backward(make_case(2, 96, 500, 8, 64, N, warmup=256, seed=N))
+
+
+def test_bwd_cfg2_slice_exact():
+    check_backward(make_case(1, 256, 50257, 8, 64, 64, warmup=4096, seed=12, **CFG), exact=True)
+
+
+@pytest.mark.parametrize("L", [1, 33, 77])
+def test_bwd_ragged_lengths(L):
+    check_backward(make_case(2, L, 200, 4, 64, 16, warmup=100, seed=L))
+
+
+@pytest.mark.parametrize("Br", [16, 32])
+def test_bwd_short_chunks(Br):
+    check_backward(make_case(2, 100, 150, 4, 32, 16, warmup=64, seed=Br, Br=Br))
+
+
+def test_bwd_interleaved_padding_slots():
+    check_backward(make_case(2, 70, 120, 8, 64, 16, warmup=80, seed=21, pad_slots=9))
+
+
+@pytest.mark.parametrize("use_silu", [True, False])
+@pytest.mark.parametrize("absent_mass", [True, False])
+def test_bwd_flags(use_silu, absent_mass):
+    check_backward(make_case(2, 64, 90, 4, 32, 16, warmup=50, seed=31), use_silu, absent_mass)
+
+
+def test_autograd_function_matches_direct_calls():
+    from mathbrain_amd.flash_ema import FlashEMAFunction
+    c = make_case(2, 64, 300, 8, 64, 64, warmup=200, seed=5)
+    g = torch.Generator().manual_seed(9)
+    dO = torch.randn(c["Q"].shape, generator=g)
+    want = gpu_backward(c, dO)
+    Q = c["Q"].cuda().requires_grad_()
+    Ek = c["E_k"].cuda().requires_grad_()
+    Ev = c["E_v"].cuda().requires_grad_()
+    W = c["W"].cuda().requires_grad_()
+    O = FlashEMAFunction.apply(Q, c["x"].cuda(), Ek, Ev, W, c["rhos"].cuda(), c["V"],
+                               c["unique"].cuda(), c["K"], c["Cb"].cuda(), True)
+    O.backward(dO.cuda())
+    for got, w in zip((Q.grad, Ek.grad, Ev.grad, W.grad), want):
+        assert norm_err(got, w) < 1e-5
