@@ -8,7 +8,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/mathbrain_hip.h"
+#include "mathbrain_hip.h"
 
 namespace mb {
 

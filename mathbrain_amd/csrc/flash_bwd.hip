@@ -51,6 +51,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
     constexpr int NT = NPAD / 16;
     constexpr int WID = kBwdHeads * HD;  // embedding columns of this head group
     using S = Stage<NPAD, SB>;
+    constexpr int CTROW = kTB + 4;               // bf16 per cdecT row (8 B pad)
+    constexpr int CT = SB * NPAD * CTROW;        // bf16 elements of cdecT per buffer
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int D = a.H * HD;
@@ -62,9 +64,9 @@ flash_ema_bwd_kernel(FlashArgs a) {
     const int cbi = t0 / a.Br;
     const int cb = cbi * a.Br;
 
-    // LDS: 2 staging buffers | 2 dE accumulators [SB][2][WID] | W fragments | meta ring |
-    // window | power table | slot info
-    const int stage_bytes = (int)S::bytes(WID);
+    // LDS: 2 staging buffers (cdec | cdecT | E) | 2 dE accumulators [SB][2][WID] |
+    // W fragments | meta ring | window | power table | slot info
+    const int stage_bytes = (int)S::bytes(WID) + CT * 2;
     const int acc_floats = SB * 2 * WID;
     float* dEacc = reinterpret_cast<float*>(smem + 2 * stage_bytes);
     bf16x8* wfr = reinterpret_cast<bf16x8*>(dEacc + 2 * acc_floats);
@@ -73,7 +75,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
 #define cdec_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes)
-#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2 + CT * 2)
 #define meta_of(batch) (metas + ((batch) % kMetaRing) * SB)
 
     const int wave = threadIdx.x >> 6;
@@ -144,7 +147,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
         prod.load(a, b, cbi, 0, kend, D, col0, WID);
         __syncthreads();
-        prod.store(a, t0, cb, powt, meta_of(0), cdec_of(0), E_of(0), WID);
+        prod.template store<true, S::CROW, CTROW>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0),
+                                                  E_of(0), WID);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -168,6 +172,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
             }
         }
         const __bf16* cdec = cdec_of(cur);
+        const __bf16* cdecT = cdecT_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
         float* acc = dEacc + cur * acc_floats;
@@ -218,7 +223,9 @@ flash_ema_bwd_kernel(FlashArgs a) {
                 p[i] = __builtin_amdgcn_exp2f(s2 - lse2[i]);
                 ds[i] = p[i] * (dpt - Dv[i]);
             }
-            // Phase 2: gradients.
+            // Phase 2: gradients.  With xq = ds q, yd = p dO:
+            //   dE_k += xq g, dE_v += yd g, dQ += ds g e_k,
+            //   dpre = (xq e_k + yd e_v) SiLU'(pre),  SiLU' = sig + g (1 - sig).
             float dEk[DT], dEv[DT];
             bf16x4 dpre[DT];
 #pragma unroll
@@ -228,12 +235,12 @@ flash_ema_bwd_kernel(FlashArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float gv = g2[dt][i];
-                    const float u = ds[i] * gv;
-                    dq[dt][i] = __builtin_fmaf(u, ek[dt], dq[dt][i]);
-                    dEk[dt] = __builtin_fmaf(u, qs[dt][i], dEk[dt]);
-                    const float w = p[i] * gv;
-                    dEv[dt] = __builtin_fmaf(w, dov[dt][i], dEv[dt]);
-                    const float av = __builtin_fmaf(ds[i], qs[dt][i] * ek[dt], p[i] * (dov[dt][i] * ev[dt]));
+                    const float xq = ds[i] * qs[dt][i];
+                    const float yd = p[i] * dov[dt][i];
+                    dEk[dt] = __builtin_fmaf(xq, gv, dEk[dt]);
+                    dEv[dt] = __builtin_fmaf(yd, gv, dEv[dt]);
+                    dq[dt][i] = __builtin_fmaf(ds[i] * gv, ek[dt], dq[dt][i]);
+                    const float av = __builtin_fmaf(xq, ek[dt], yd * ev[dt]);
                     float dsil = 1.f;
                     if (SILU) {
                         const float sig = sg[dt][i];
@@ -242,39 +249,35 @@ flash_ema_bwd_kernel(FlashArgs a) {
                     dpre[dt][i] = (__bf16)(av * dsil);
                 }
             }
-            // dE partial sums over this lane's 4 steps -> over the 4 row groups -> LDS.
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                dEk[dt] += __shfl_xor(dEk[dt], 16);
-                dEk[dt] += __shfl_xor(dEk[dt], 32);
-                dEv[dt] += __shfl_xor(dEv[dt], 16);
-                dEv[dt] += __shfl_xor(dEv[dt], 32);
-            }
-            // group g adds dim tile dt == g (DT == 4) or dt == g % DT with g < DT
-            if (g < DT) {
-                float vk = dEk[0], vv = dEv[0];
-#pragma unroll
-                for (int dt = 1; dt < DT; ++dt)
-                    if (g == dt) {
-                        vk = dEk[dt];
-                        vv = dEv[dt];
-                    }
+            // dE: this lane's 4 steps summed in registers; the 4 row groups (other steps)
+            // are reduce-scattered with v_permlane16/32_swap so that the writing row holds
+            // one dim tile; the two half-waves meet in LDS.
+            if (DT == 4) {
+                const float vk = rows4_reduce_scatter(dEk[0], dEk[1 % DT], dEk[2 % DT], dEk[3 % DT]);
+                const float vv = rows4_reduce_scatter(dEv[0], dEv[1 % DT], dEv[2 % DT], dEv[3 % DT]);
                 atomicAdd(&acc[(j * 2 + 0) * WID + hl * HD + 16 * g + c16], vk);
                 atomicAdd(&acc[(j * 2 + 1) * WID + hl * HD + 16 * g + c16], vv);
+            } else {
+                const float vk = rows4_reduce_scatter2(dEk[0], dEk[1 % DT]);
+                const float vv = rows4_reduce_scatter2(dEv[0], dEv[1 % DT]);
+                if ((g & 1) == 0) {
+                    atomicAdd(&acc[(j * 2 + 0) * WID + hl * HD + 8 * g + c16], vk);
+                    atomicAdd(&acc[(j * 2 + 1) * WID + hl * HD + 8 * g + c16], vv);
+                }
             }
             // dW^T[d, n] += dpre^T[d, t] c_dec[t, n]: A = dpre (rows d, k = this lane's
-            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16].
+            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16] read from cdecT.
+            const __bf16* ctrow = cdecT + (j * NPAD) * CTROW + 16 * th + 4 * g;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                bf16x4 cb4;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) cb4[e] = crow[(4 * g + e) * S::CROW + 16 * nt + c16];
+                const bf16x4 cb4 = *reinterpret_cast<const bf16x4*>(ctrow + (16 * nt + c16) * CTROW);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
             }
         }
         if (bi + 1 < nb) {
-            prod.store(a, t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), E_of(cur ^ 1), WID);
+            prod.template store<true, S::CROW, CTROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1),
+                                                      cdecT_of(cur ^ 1), E_of(cur ^ 1), WID);
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();
@@ -315,6 +318,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
                 atomicAdd(&a.dW[(int64_t)n * D + h * HD + 16 * dt + 4 * g + i], dWacc[dt][nt][i]);
         }
 #undef cdec_of
+#undef cdecT_of
 #undef E_of
 #undef meta_of
 }
@@ -322,7 +326,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
 template <int HD, int NS, int SB>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
-    return 2 * Stage<32 * NS, SB>::bytes(WID) + 2 * (size_t)SB * 2 * WID * 4 +
+    return 2 * (Stage<32 * NS, SB>::bytes(WID) + (size_t)SB * 32 * NS * (kTB + 4) * 2) +
+           2 * (size_t)SB * 2 * WID * 4 +
            (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16;
 }
@@ -334,7 +339,7 @@ static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
     constexpr int NPAD = 32 * NS;
     constexpr int WID = kBwdHeads * HD;
     const int nthr = 64 * 2 * kBwdHeads;
-    const int mi = (kTB * (NPAD / 4) + nthr - 1) / nthr;
+    const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
     const int me = (SB * 2 * (WID / 4) + nthr - 1) / nthr;
     const size_t lds = bwd_lds_bytes<HD, NS, SB>();
     if (lds > 160 * 1024)
@@ -405,7 +410,7 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     if (hd == 64) {
         if (NS == 1) return launch_bwd<64, 1, 4>(a, st);
         if (NS == 2) return launch_bwd<64, 2, 4>(a, st);
-        return launch_bwd<64, 4, 2>(a, st);
+        return launch_bwd<64, 4, 1>(a, st);
     }
     if (NS == 1) return launch_bwd<32, 1, 4>(a, st);
     if (NS == 2) return launch_bwd<32, 2, 4>(a, st);

@@ -66,6 +66,39 @@ __device__ inline f32x4 mfma16x16x16(bf16x4 a, bf16x4 b, f32x4 c) {
                                                      __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
 }
 
+// Exchange helpers on the four 16-lane rows of a wave (gfx950 v_permlane{16,32}_swap).
+// Written as inline asm: in this toolchain the builtins return the first register for
+// both results.  The s_nop pads cover the VALU-write -> permlane-read hazard.
+__device__ inline float2 swap_halves(float a, float b) {
+    // a' = {a.lo, b.lo}, b' = {a.hi, b.hi}
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return make_float2(a, b);
+}
+__device__ inline float2 swap_odd_rows(float a, float b) {
+    // a' = {a.r0, b.r0, a.r2, b.r2}, b' = {a.r1, b.r1, a.r3, b.r3}
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return make_float2(a, b);
+}
+
+// Reduce-scatter over the four rows: v[k] holds per-lane partials of 4 quantities;
+// returns, in row g, the sum over all rows of v[g] (lane l gets sum_r v[g][16 r + l%16]).
+__device__ inline float rows4_reduce_scatter(float v0, float v1, float v2, float v3) {
+    const float2 a = swap_halves(v0, v2);  // lo: v0 halves, hi: v2 halves
+    const float2 b = swap_halves(v1, v3);
+    const float x02 = a.x + a.y;           // rows 0,1: v0 over halves; rows 2,3: v2
+    const float x13 = b.x + b.y;
+    const float2 c = swap_odd_rows(x02, x13);
+    return c.x + c.y;                      // row 0: v0, row 1: v1, row 2: v2, row 3: v3
+}
+
+// Same for two quantities: row 0 gets the sum of v0, row 2 the sum of v1 (rows 1, 3: 0).
+__device__ inline float rows4_reduce_scatter2(float v0, float v1) {
+    const float2 a = swap_halves(v0, v1);
+    const float x = a.x + a.y;             // rows 0,1: v0 over halves; rows 2,3: v1
+    const float2 c = swap_odd_rows(x, 0.0f);
+    return c.x + c.y;
+}
+
 // Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane gets the sum.
 __device__ inline float row_sum16(float v) {
     v += __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
@@ -158,40 +191,39 @@ __device__ void flash_batch_meta(const FlashArgs& a, int b, int bi, int kend, co
     }
 }
 
-// Producer registers: each thread owns up to MAXI items (t, 4 rates) of the cdec tile and
-// up to MAXE float4 of the embedding copy.
+// Producer: each thread owns up to MAXI blocks (slot j, 4 steps, 4 rates) of the batch's
+// cdec tiles and up to MAXE float4 of the embedding copy.  Blocks of 4 steps x 4 rates
+// let the same thread also write the transposed tile cdecT[j][n][t] (TRANS) with 8-byte
+// stores.
 template <int NPAD, int SB, int MAXI, int MAXE>
 struct Producer {
-    float4 s[MAXI][SB];
+    static constexpr int BPS = (kTB / 4) * (NPAD / 4);  // blocks per slot
+    float4 s[MAXI];
     float4 e[MAXE];
 
-    // D: row length of E_k/E_v; the copy takes columns [col0, col0 + width).
     __device__ void load(const FlashArgs& a, int b, int cbi, int bi, int kend, int D, int col0,
                          int width) {
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
-        const int nitems = kTB * (NPAD / 4);
 #pragma unroll
         for (int ii = 0; ii < MAXI; ++ii) {
             const int item = tid + ii * nthr;
+            const int j = item / BPS;
             const int n0 = (item % (NPAD / 4)) * 4;
-#pragma unroll
-            for (int j = 0; j < SB; ++j) {
-                const int k = bi * SB + j;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (item < nitems && k < kend) {
-                    const float* src = a.Cb + (((int64_t)b * a.nc + cbi) * a.K + k) * a.Np + n0;
-                    if (n0 + 3 < a.N && (a.Np & 3) == 0) {
-                        v = *reinterpret_cast<const float4*>(src);
-                    } else {
-                        if (n0 + 0 < a.N) v.x = src[0];
-                        if (n0 + 1 < a.N) v.y = src[1];
-                        if (n0 + 2 < a.N) v.z = src[2];
-                        if (n0 + 3 < a.N) v.w = src[3];
-                    }
+            const int k = bi * SB + j;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (j < SB && k < kend) {
+                const float* src = a.Cb + (((int64_t)b * a.nc + cbi) * a.K + k) * a.Np + n0;
+                if (n0 + 3 < a.N && (a.Np & 3) == 0) {
+                    v = *reinterpret_cast<const float4*>(src);
+                } else {
+                    if (n0 + 0 < a.N) v.x = src[0];
+                    if (n0 + 1 < a.N) v.y = src[1];
+                    if (n0 + 2 < a.N) v.z = src[2];
+                    if (n0 + 3 < a.N) v.w = src[3];
                 }
-                s[ii][j] = v;
             }
+            s[ii] = v;
         }
         const int w4 = width / 4;
         const int nvec = SB * 2 * w4;
@@ -215,26 +247,30 @@ struct Producer {
         }
     }
 
-    // Builds cdec and E ([SB][2][width]) of the batch into the staging buffer.
-    __device__ void store(const FlashArgs& a, int t0, int cb, const float* powt,
-                          const BatchMeta* meta, __bf16* cdec, float* E, int width) {
-        using S = Stage<NPAD, SB>;
+    // Builds cdec ([SB][kTB][CROW]), optionally cdecT ([SB][NPAD][CTROW]), and E
+    // ([SB][2][width]) of the batch into the staging buffer.
+    template <bool TRANS, int CROW, int CTROW>
+    __device__ void store(int t0, int cb, const float* powt, const BatchMeta* meta,
+                          __bf16* cdec, __bf16* cdecT, float* E, int width) {
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
-        const int nitems = kTB * (NPAD / 4);
 #pragma unroll
         for (int ii = 0; ii < MAXI; ++ii) {
             const int item = tid + ii * nthr;
-            if (item >= nitems) continue;
-            const int tl = item / (NPAD / 4);
+            const int j = item / BPS;
+            if (j >= SB) continue;
+            const int tq = (item % BPS) / (NPAD / 4);
             const int n0 = (item % (NPAD / 4)) * 4;
-            const int tr = t0 - cb + tl;  // 0 .. 63
-            const float4 pw = *reinterpret_cast<const float4*>(powt + (tr + 1) * NPAD + n0);
+            const float4 sv = s[ii];
+            const uint64_t mask = meta[j].mask;
+            bf16x4 blk[4];
 #pragma unroll
-            for (int j = 0; j < SB; ++j) {
-                const float4 sv = s[ii][j];
+            for (int r = 0; r < 4; ++r) {
+                const int tl = 4 * tq + r;
+                const int tr = t0 - cb + tl;  // 0 .. 63
+                const float4 pw = *reinterpret_cast<const float4*>(powt + (tr + 1) * NPAD + n0);
                 float c0 = sv.x * pw.x, c1 = sv.y * pw.y, c2 = sv.z * pw.z, c3 = sv.w * pw.w;
-                uint64_t m = meta[j].mask & ((tr >= 64) ? ~0ull : ((1ull << tr) - 1ull));
+                uint64_t m = mask & ((1ull << tr) - 1ull);
                 while (m) {
                     const int p = __builtin_ctzll(m);
                     m &= m - 1;
@@ -249,12 +285,24 @@ struct Producer {
                 w[1] = (__bf16)c1;
                 w[2] = (__bf16)c2;
                 w[3] = (__bf16)c3;
-                *reinterpret_cast<bf16x4*>(cdec + (j * kTB + tl) * S::CROW + n0) = w;
+                blk[r] = w;
+                *reinterpret_cast<bf16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
+            }
+            if (TRANS) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    bf16x4 w;
+                    w[0] = blk[0][q];
+                    w[1] = blk[1][q];
+                    w[2] = blk[2][q];
+                    w[3] = blk[3][q];
+                    *reinterpret_cast<bf16x4*>(cdecT + (j * NPAD + n0 + q) * CTROW + 4 * tq) = w;
+                }
             }
         }
         const int nvec = SB * 2 * (width / 4);
 #pragma unroll
-        for (int ie = 0; ie < (MAXE); ++ie) {
+        for (int ie = 0; ie < MAXE; ++ie) {
             const int i = tid + ie * nthr;
             if (i < nvec) reinterpret_cast<float4*>(E)[i] = e[ie];
         }

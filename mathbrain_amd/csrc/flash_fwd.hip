@@ -102,7 +102,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
         prod.load(a, b, cbi, 0, kend, D, 0, D);
         __syncthreads();
-        prod.store(a, t0, cb, powt, meta_of(0), cdec_of(0), E_of(0), D);
+        prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -180,7 +180,8 @@ flash_ema_fwd_kernel(FlashArgs a) {
             }
         }
         if (bi + 1 < nb) {
-            prod.store(a, t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), E_of(cur ^ 1), D);
+            prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+                                                 E_of(cur ^ 1), D);
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();
@@ -218,7 +219,7 @@ static int launch_fwd(const FlashArgs& a, hipStream_t st) {
     const int D = a.H * HD;
     const int nthr = 64 * a.H;
     constexpr int NPAD = 32 * NS;
-    const int mi = (kTB * (NPAD / 4) + nthr - 1) / nthr;
+    const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
     const int nvec = SB * 2 * (D / 4);
     const size_t lds = fwd_lds_bytes<HD, NS, SB>(D);
     if (lds > 160 * 1024)
