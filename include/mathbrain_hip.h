@@ -117,6 +117,9 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
  *   unique    [B, K] int64 contiguous, -1 = padding slot
  *   C_bounds  [B, nc, K, Np] fp32 contiguous (mb_ema_boundary_states), nc >= ceil(L/Br)
  *   O         [B, H, L, hd] fp32 contiguous output; LSE [B, H, L] fp32 output
+ *   scores    NULL, or [B, H, K, L] fp32 output: s[t,k] * log2(e) for every valid slot
+ *             (rows of padding slots are not written).  Passed to mb_flash_ema_bwd, it
+ *             spares the backward the score recomputation.
  *
  * Supported: hd in {32, 64}, 4 <= H <= 8, N <= 128, Br <= 32 or Br == 64.
  */
@@ -125,7 +128,7 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
                      const float *E_v, const float *W_pe, const float *rhos,
                      const int64_t *unique, const float *C_bounds, int B, int H, int L, int hd,
                      int K, int N, int Np, int nc, int Br, int64_t V_total, int flags, float *O,
-                     float *LSE, void *stream);
+                     float *LSE, float *scores, void *stream);
 
 /*
  * Flash-EMA gated cross-attention backward.  Replaces FlashEMAFunction.backward and its
@@ -134,6 +137,7 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
  *
  *   dO        [B, H, L, hd] fp32, same element strides as Q
  *   O, LSE    the forward's outputs (contiguous)
+ *   scores    NULL (recompute the scores), or the forward's scores output
  *   dQ        [B, H, L, hd] fp32 contiguous output
  *   dE_k/dE_v [B, K, H*hd] fp32 contiguous outputs (zero for padding slots)
  *   dW_pe     [N, H*hd] fp32 contiguous output
@@ -148,8 +152,8 @@ int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
                      const float *E_k, const float *E_v, const float *W_pe, const float *rhos,
                      const int64_t *unique, const float *C_bounds, const float *O,
                      const float *LSE, int B, int H, int L, int hd, int K, int N, int Np, int nc,
-                     int Br, int64_t V_total, int flags, float *dQ, float *dE_k, float *dE_v,
-                     float *dW_pe, void *stream);
+                     int Br, int64_t V_total, int flags, const float *scores, float *dQ,
+                     float *dE_k, float *dE_v, float *dW_pe, void *stream);
 
 #ifdef __cplusplus
 }

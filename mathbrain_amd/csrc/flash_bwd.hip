@@ -43,7 +43,7 @@ static int zero_fill(float* p, int64_t n, hipStream_t st) {
     return check_launch("zero fill");
 }
 
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU>
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_bwd_kernel(FlashArgs a) {
     constexpr int NPAD = 32 * NS;
@@ -64,9 +64,10 @@ flash_ema_bwd_kernel(FlashArgs a) {
     const int cbi = t0 / a.Br;
     const int cb = cbi * a.Br;
 
-    // LDS: 2 staging buffers (cdec | cdecT | E) | 2 dE accumulators [SB][2][WID] |
-    // W fragments | meta ring | window | power table | slot info
-    const int stage_bytes = (int)S::bytes(WID) + CT * 2;
+    // LDS: 2 staging buffers (cdec | cdecT | E | scores [SB][heads][kTB]) | 2 dE
+    // accumulators [SB][2][WID] | W fragments | meta ring | window | power table | slot info
+    constexpr int SCN = HAS_S ? SB * kBwdHeads * kTB : 0;  // staged scores per buffer
+    const int stage_bytes = (int)S::bytes(WID) + CT * 2 + SCN * 4;
     const int acc_floats = SB * 2 * WID;
     float* dEacc = reinterpret_cast<float*>(smem + 2 * stage_bytes);
     bf16x8* wfr = reinterpret_cast<bf16x8*>(dEacc + 2 * acc_floats);
@@ -77,6 +78,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
 #define cdec_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes)
 #define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CDEC * 2)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2 + CT * 2)
+#define S2_of(i) (E_of(i) + SB * 2 * WID)
 #define meta_of(batch) (metas + ((batch) % kMetaRing) * SB)
 
     const int wave = threadIdx.x >> 6;
@@ -143,10 +145,38 @@ flash_ema_bwd_kernel(FlashArgs a) {
 
     Producer<NPAD, SB, MAXI, MAXE> prod;
     const int col0 = hg * WID;
+    // Forward scores of a batch, one float4 (4 steps) per thread < SCN / 4.
+    float4 s2pre = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto load_scores = [&](int batch) {
+        if (!HAS_S || (int)threadIdx.x >= SCN / 4) return;
+        const int j = threadIdx.x / (kBwdHeads * kTB / 4);
+        const int hh = (threadIdx.x / (kTB / 4)) % kBwdHeads;
+        const int tq = threadIdx.x % (kTB / 4);
+        const int k = batch * SB + j;
+        const int t = t0 + 4 * tq;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < kend) {
+            const float* src = a.S2in + (((int64_t)b * a.H + hg * kBwdHeads + hh) * a.K + k) * a.L + t;
+            if ((a.L & 3) == 0 && t + 3 < a.L) {
+                v = *reinterpret_cast<const float4*>(src);
+            } else {
+                if (t + 0 < a.L) v.x = src[0];
+                if (t + 1 < a.L) v.y = src[1];
+                if (t + 2 < a.L) v.z = src[2];
+                if (t + 3 < a.L) v.w = src[3];
+            }
+        }
+        s2pre = v;
+    };
+    auto store_scores = [&](float* dst) {
+        if (HAS_S && (int)threadIdx.x < SCN / 4) reinterpret_cast<float4*>(dst)[threadIdx.x] = s2pre;
+    };
     if (nb > 0) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
         prod.load(a, b, cbi, 0, kend, D, col0, WID);
+        load_scores(0);
         __syncthreads();
+        store_scores(S2_of(0));
         prod.template store<true, S::CROW, CTROW>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0),
                                                   E_of(0), WID);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
@@ -155,7 +185,10 @@ flash_ema_bwd_kernel(FlashArgs a) {
 
     for (int bi = 0; bi < nb; ++bi) {
         const int cur = bi & 1;
-        if (bi + 1 < nb) prod.load(a, b, cbi, bi + 1, kend, D, col0, WID);
+        if (bi + 1 < nb) {
+            prod.load(a, b, cbi, bi + 1, kend, D, col0, WID);
+            load_scores(bi + 1);
+        }
         // Flush the previous batch's dE sums (complete after the last barrier).
         if (bi > 0) {
             float* acc = dEacc + (cur ^ 1) * acc_floats;
@@ -178,6 +211,10 @@ flash_ema_bwd_kernel(FlashArgs a) {
         float* acc = dEacc + cur * acc_floats;
         for (int j = 0; j < SB; ++j) {
             if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
+            // Forward scores of this lane's 4 steps, staged in LDS with the batch.
+            f32x4 s2v = {0.f, 0.f, 0.f, 0.f};
+            if (HAS_S)
+                s2v = *reinterpret_cast<const f32x4*>(S2_of(cur) + (j * kBwdHeads + hl) * kTB + 16 * th + 4 * g);
             const __bf16* crow = cdec + (j * kTB + 16 * th) * S::CROW;
             bf16x8 cf[NS];
 #pragma unroll
@@ -212,14 +249,14 @@ flash_ema_bwd_kernel(FlashArgs a) {
                     }
                     g2[dt][i] = gv;  // g * log2 e
                     sg[dt][i] = sig;
-                    s[i] = __builtin_fmaf(qs[dt][i] * ek[dt], gv, s[i]);
+                    if (!HAS_S) s[i] = __builtin_fmaf(qs[dt][i] * ek[dt], gv, s[i]);
                     dp[i] = __builtin_fmaf(dov[dt][i] * ev[dt], gv, dp[i]);
                 }
             float p[4], ds[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s2 = row_sum16(s[i]);               // score * log2 e
-                const float dpt = row_sum16(dp[i]) * kLn2;      // dO . v
+                const float s2 = HAS_S ? s2v[i] : row_sum16(s[i]);  // score * log2 e
+                const float dpt = row_sum16(dp[i]) * kLn2;          // dO . v
                 p[i] = __builtin_amdgcn_exp2f(s2 - lse2[i]);
                 ds[i] = p[i] * (dpt - Dv[i]);
             }
@@ -242,9 +279,9 @@ flash_ema_bwd_kernel(FlashArgs a) {
                     dq[dt][i] = __builtin_fmaf(ds[i] * gv, ek[dt], dq[dt][i]);
                     const float av = __builtin_fmaf(xq, ek[dt], yd * ev[dt]);
                     float dsil = 1.f;
-                    if (SILU) {
+                    if (SILU) {  // sig + g (1 - sig), with g = gv ln2
                         const float sig = sg[dt][i];
-                        dsil = __builtin_fmaf(gv * kLn2, 1.0f - sig, sig);
+                        dsil = __builtin_fmaf(gv, __builtin_fmaf(-kLn2, sig, kLn2), sig);
                     }
                     dpre[dt][i] = (__bf16)(av * dsil);
                 }
@@ -278,6 +315,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
         if (bi + 1 < nb) {
             prod.template store<true, S::CROW, CTROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1),
                                                       cdecT_of(cur ^ 1), E_of(cur ^ 1), WID);
+            store_scores(S2_of(cur ^ 1));
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();
@@ -320,13 +358,15 @@ flash_ema_bwd_kernel(FlashArgs a) {
 #undef cdec_of
 #undef cdecT_of
 #undef E_of
+#undef S2_of
 #undef meta_of
 }
 
 template <int HD, int NS, int SB>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
-    return 2 * (Stage<32 * NS, SB>::bytes(WID) + (size_t)SB * 32 * NS * (kTB + 4) * 2) +
+    return 2 * (Stage<32 * NS, SB>::bytes(WID) + (size_t)SB * 32 * NS * (kTB + 4) * 2 +
+                (size_t)SB * kBwdHeads * kTB * 4) +
            2 * (size_t)SB * 2 * WID * 4 +
            (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16;
@@ -348,8 +388,10 @@ static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
     dim3 grid(a.B * ntb * a.head_groups);
 #define MB_BWD(MI, ME)                                                                      \
     do {                                                                                    \
-        auto k = a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true>                   \
-                        : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false>;                 \
+        auto k = a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true>   \
+                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true>) \
+                        : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false>  \
+                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false>); \
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
         if (e != hipSuccess) {                                                              \
@@ -378,8 +420,8 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
                                 const float* W_pe, const float* rhos, const int64_t* unique,
                                 const float* C_bounds, const float* O, const float* LSE, int B,
                                 int H, int L, int hd, int K, int N, int Np, int nc, int Br,
-                                int64_t V_total, int flags, float* dQ, float* dE_k, float* dE_v,
-                                float* dW_pe, void* stream) {
+                                int64_t V_total, int flags, const float* scores, float* dQ,
+                                float* dE_k, float* dE_v, float* dW_pe, void* stream) {
     FlashArgs a{};
     a.Q = Q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_sl = q_sl; a.q_sd = q_sd;
     a.dO = dO; a.x = x; a.x_sb = x_sb; a.x_sl = x_sl;
@@ -389,6 +431,7 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     a.v_total = (flags & MB_FLASH_ABSENT_MASS) ? (float)V_total : -1.0f;
     a.silu = (flags & MB_FLASH_SILU) ? 1 : 0;
     a.dQ = dQ; a.dEk = dE_k; a.dEv = dE_v; a.dW = dW_pe;
+    a.S2in = scores;
     int rc = flash_validate("mb_flash_ema_bwd", a, hd);
     if (rc) return rc;
     if (H % kBwdHeads)

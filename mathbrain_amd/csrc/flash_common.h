@@ -43,6 +43,8 @@ struct FlashArgs {
     int silu;
     float* O;    // [B, H, L, hd]
     float* LSE;  // [B, H, L]
+    float* S2out;        // optional [B, H, K, L]: scores * log2 e (forward output)
+    const float* S2in;   // optional, the same, read by the backward
     // backward only
     const float* dO;   // [B, H, L, hd], same strides as Q
     const float* Oin;  // forward output, [B, H, L, hd] contiguous

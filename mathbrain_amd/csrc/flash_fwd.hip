@@ -159,6 +159,14 @@ flash_ema_fwd_kernel(FlashArgs a) {
                 sacc += __shfl_xor(sacc, 32);
                 s[tt] = sacc;
             }
+            if (a.S2out && g == 0) {
+                float* srow = a.S2out + (((int64_t)b * a.H + h) * a.K + bi * SB + j) * a.L;
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int t = t0 + 16 * tt + c16;
+                    if (t < a.L) srow[t] = s[tt];
+                }
+            }
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 const bool need = s[tt] > m[tt] + kTau;
@@ -277,7 +285,8 @@ extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
                                 const float* E_k, const float* E_v, const float* W_pe,
                                 const float* rhos, const int64_t* unique, const float* C_bounds,
                                 int B, int H, int L, int hd, int K, int N, int Np, int nc, int Br,
-                                int64_t V_total, int flags, float* O, float* LSE, void* stream) {
+                                int64_t V_total, int flags, float* O, float* LSE, float* scores,
+                                void* stream) {
     FlashArgs a{};
     a.Q = Q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_sl = q_sl; a.q_sd = q_sd;
     a.x = x; a.x_sb = x_sb; a.x_sl = x_sl;
@@ -286,6 +295,7 @@ extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     a.v_total = (flags & MB_FLASH_ABSENT_MASS) ? (float)V_total : -1.0f;
     a.silu = (flags & MB_FLASH_SILU) ? 1 : 0;
     a.O = O; a.LSE = LSE;
+    a.S2out = scores;
     int rc = flash_validate("mb_flash_ema_fwd", a, hd);
     if (rc) return rc;
     if (B == 0 || L == 0) return MB_OK;

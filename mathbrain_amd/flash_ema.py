@@ -72,7 +72,7 @@ def _flash_flags(use_silu, absent_mass):
 
 
 def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
-                      C_bounds, use_silu=True, Br=64, absent_mass=True):
+                      C_bounds, use_silu=True, Br=64, absent_mass=True, return_scores=False):
     """Gated flash-EMA attention forward (triton_flash_ema.py:529-568).
 
     Q [B, H, L, hd]; x [B, L]; E_k_active / E_v_active [B, K_max, H*hd]; W_pe [N, H*hd]
@@ -84,7 +84,9 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
     [B, K_max, H, hd], as the reference does.  With ``absent_mass`` (the default) the
     softmax covers all V_total slots as the dense PyTorch reference
     (flash_ema_attention.py:76-77) does; ``absent_mass=False`` gives the Triton kernel's
-    softmax over the valid slots only (triton_flash_ema.py:215-229).
+    softmax over the valid slots only (triton_flash_ema.py:215-229).  With
+    ``return_scores`` a sixth element holds the scores * log2(e) as [B, H, K_max, L]
+    (what ``flash_ema_backward(scores=...)`` consumes instead of recomputing them).
     """
     dev = _lib.require_gpu(Q, x, E_k_active, E_v_active, W_pe, rhos, unique_tensor, C_bounds,
                            what="flash_ema_forward")
@@ -111,20 +113,23 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
         raise ValueError(f"C_bounds must be [B, nc, K_max, >=N], got {tuple(Cb.shape)}")
     O = torch.empty(B, H, L, hd, dtype=torch.float32, device=dev)
     LSE = torch.empty(B, H, L, dtype=torch.float32, device=dev)
+    S2 = torch.empty(B, H, K, L, dtype=torch.float32, device=dev) if return_scores else None
     with torch.cuda.device(dev):
         _lib.call("mb_flash_ema_fwd", _lib.ptr(Qf), *Qf.stride(), _lib.ptr(xl), xl.stride(0),
                   xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W), _lib.ptr(rh),
                   _lib.ptr(uniq), _lib.ptr(Cb), B, H, L, hd, K, N, Cb.shape[3], Cb.shape[1],
                   int(Br), int(V_total), _flash_flags(use_silu, absent_mass), _lib.ptr(O),
-                  _lib.ptr(LSE), _lib.stream(dev))
-    return O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd)
+                  _lib.ptr(LSE), _lib.ptr(S2), _lib.stream(dev))
+    out = (O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd))
+    return out + (S2,) if return_scores else out
 
 
 def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bounds, O, LSE, dO,
-                       use_silu=True, Br=64, absent_mass=True):
+                       use_silu=True, Br=64, absent_mass=True, scores=None):
     """Gradients of flash_ema_forward (triton_flash_ema.py:586-650) in one fused HIP pass.
 
-    E_k / E_v are [B, K, H*hd] or [B, K, H, hd]; returns (dQ [B,H,L,hd], dE_k [B,K,H*hd],
+    E_k / E_v are [B, K, H*hd] or [B, K, H, hd]; ``scores`` is the forward's optional
+    scores output (recomputed when None).  Returns (dQ [B,H,L,hd], dE_k [B,K,H*hd],
     dE_v [B,K,H*hd], dW_pe [N, H*hd]), all fp32.
     """
     dev = _lib.require_gpu(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO,
@@ -151,14 +156,24 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
     dEk = torch.empty(B, K, D, dtype=torch.float32, device=dev)
     dEv = torch.empty(B, K, D, dtype=torch.float32, device=dev)
     dW = torch.empty(N, D, dtype=torch.float32, device=dev)
+    if scores is not None and (scores.shape != (B, H, K, L) or scores.dtype != torch.float32
+                               or not scores.is_contiguous()):
+        raise ValueError(f"scores must be contiguous fp32 [B, H, K_max, L], got {tuple(scores.shape)}")
     with torch.cuda.device(dev):
         _lib.call("mb_flash_ema_bwd", _lib.ptr(Qf), *Qf.stride(), _lib.ptr(dOf), _lib.ptr(xl),
                   xl.stride(0), xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W),
                   _lib.ptr(rh), _lib.ptr(uniq), _lib.ptr(Cb), _lib.ptr(Of), _lib.ptr(Lf), B, H, L,
                   hd, K, N, Cb.shape[3], Cb.shape[1], int(Br), int(V_total),
-                  _flash_flags(use_silu, absent_mass), _lib.ptr(dQ), _lib.ptr(dEk),
-                  _lib.ptr(dEv), _lib.ptr(dW), _lib.stream(dev))
+                  _flash_flags(use_silu, absent_mass), _lib.ptr(scores), _lib.ptr(dQ),
+                  _lib.ptr(dEk), _lib.ptr(dEv), _lib.ptr(dW), _lib.stream(dev))
     return dQ, dEk, dEv, dW
+
+
+# With SAVE_SCORES, FlashEMAFunction keeps the forward's scores ([B, H, K_max, L] fp32,
+# 1.4 GB at B=56, T=512, H=8, K_max=1638) and the backward skips recomputing them.  Off by
+# default: on gfx950 the extra live registers of that variant cost more than the skipped
+# score arithmetic (30.1 ms recomputing vs 33.3 ms reading them, configuration 2).
+SAVE_SCORES = False
 
 
 class FlashEMAFunction(torch.autograd.Function):
@@ -171,10 +186,11 @@ class FlashEMAFunction(torch.autograd.Function):
     @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float32)
     def forward(ctx, Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
                 C_bounds, use_silu=True, Br=64):
-        O, LSE, C_bounds, E_k, E_v = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos,
-                                                       V_total, unique_tensor, K_max, C_bounds,
-                                                       use_silu, Br)
-        ctx.save_for_backward(Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE)
+        res = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
+                                K_max, C_bounds, use_silu, Br, return_scores=SAVE_SCORES)
+        O, LSE, C_bounds, E_k, E_v = res[:5]
+        ctx.save_for_backward(Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE,
+                              res[5] if SAVE_SCORES else None)
         ctx.V_total = V_total
         ctx.use_silu = use_silu
         ctx.Br = Br
@@ -184,10 +200,10 @@ class FlashEMAFunction(torch.autograd.Function):
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, dO):
-        Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE = ctx.saved_tensors
+        Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE, S2 = ctx.saved_tensors
         dQ, dEk, dEv, dW = flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, ctx.V_total,
                                               unique_tensor, C_bounds, O, LSE, dO.contiguous(),
-                                              ctx.use_silu, ctx.Br)
+                                              ctx.use_silu, ctx.Br, scores=S2)
         if ctx.W_rows > dW.shape[0]:  # W_pe passed with padded rows: their gradient is 0
             dW = torch.cat([dW, dW.new_zeros(ctx.W_rows - dW.shape[0], dW.shape[1])])
         return dQ, None, dEk, dEv, dW, None, None, None, None, None, None, None

@@ -174,15 +174,18 @@ def test_fwd_rejects_unsupported_shapes():
 
 # ---- backward ------------------------------------------------------------------------
 
-def gpu_backward(c, dO, use_silu=True, absent_mass=True):
+def gpu_backward(c, dO, use_silu=True, absent_mass=True, stored_scores=True):
+    """Backward through the C ABI, with the forward's stored scores or recomputing them."""
     from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward
     cu = lambda t: t.cuda()
-    O, LSE, *_ = flash_ema_forward(cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]), cu(c["W"]),
-                                   cu(c["rhos"]), c["V"], cu(c["unique"]), c["K"], cu(c["Cb"]),
-                                   use_silu=use_silu, Br=c["Br"], absent_mass=absent_mass)
+    O, LSE, _, _, _, S2 = flash_ema_forward(
+        cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]), cu(c["W"]), cu(c["rhos"]), c["V"],
+        cu(c["unique"]), c["K"], cu(c["Cb"]), use_silu=use_silu, Br=c["Br"],
+        absent_mass=absent_mass, return_scores=True)
     grads = flash_ema_backward(cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]), cu(c["W"]),
                                cu(c["rhos"]), c["V"], cu(c["unique"]), cu(c["Cb"]), O, LSE, cu(dO),
-                               use_silu=use_silu, Br=c["Br"], absent_mass=absent_mass)
+                               use_silu=use_silu, Br=c["Br"], absent_mass=absent_mass,
+                               scores=S2 if stored_scores else None)
     torch.cuda.synchronize()
     return [t.cpu() for t in grads]
 
@@ -195,10 +198,10 @@ def oracle_backward(c, dO, use_silu=True, absent_mass=True, gate_round=None):
         absent_mass=absent_mass, gate_round=gate_round)
 
 
-def check_backward(c, use_silu=True, absent_mass=True, exact=False, seed=0):
+def check_backward(c, use_silu=True, absent_mass=True, exact=False, seed=0, stored_scores=True):
     g = torch.Generator().manual_seed(seed + 77)
     dO = torch.randn(c["Q"].shape, generator=g)
-    got = gpu_backward(c, dO, use_silu, absent_mass)
+    got = gpu_backward(c, dO, use_silu, absent_mass, stored_scores)
     want = oracle_backward(c, dO, use_silu, absent_mass, gate_round="log2e")
     names = ("dQ", "dE_k", "dE_v", "dW_pe")
     errs = [norm_err(a, b) for a, b in zip(got, want)]
@@ -226,8 +229,9 @@ def test_bwd_cfg1_exact():
 
 
 @pytest.mark.parametrize("N", [16, 64, 128])
-def test_bwd_rates(N):
-    check_backward(make_case(2, 96, 500, 8, 64, N, warmup=256, seed=N))
+@pytest.mark.parametrize("stored_scores", [True, False])
+def test_bwd_rates(N, stored_scores):
+    check_backward(make_case(2, 96, 500, 8, 64, N, warmup=256, seed=N), stored_scores=stored_scores)
 
 
 def test_bwd_cfg2_slice_exact():
@@ -235,8 +239,9 @@ def test_bwd_cfg2_slice_exact():
 
 
 @pytest.mark.parametrize("L", [1, 33, 77])
-def test_bwd_ragged_lengths(L):
-    check_backward(make_case(2, L, 200, 4, 64, 16, warmup=100, seed=L))
+@pytest.mark.parametrize("stored_scores", [True, False])
+def test_bwd_ragged_lengths(L, stored_scores):
+    check_backward(make_case(2, L, 200, 4, 64, 16, warmup=100, seed=L), stored_scores=stored_scores)
 
 
 @pytest.mark.parametrize("Br", [16, 32])
@@ -250,8 +255,27 @@ def test_bwd_interleaved_padding_slots():
 
 @pytest.mark.parametrize("use_silu", [True, False])
 @pytest.mark.parametrize("absent_mass", [True, False])
-def test_bwd_flags(use_silu, absent_mass):
-    check_backward(make_case(2, 64, 90, 4, 32, 16, warmup=50, seed=31), use_silu, absent_mass)
+@pytest.mark.parametrize("stored_scores", [True, False])
+def test_bwd_flags(use_silu, absent_mass, stored_scores):
+    check_backward(make_case(2, 64, 90, 4, 32, 16, warmup=50, seed=31), use_silu, absent_mass,
+                   stored_scores=stored_scores)
+
+
+def test_fwd_scores_output():
+    """The optional scores output is s * log2(e) = LSE-consistent log-softmax numerators."""
+    from mathbrain_amd.flash_ema import flash_ema_forward
+    c = make_case(2, 50, 120, 4, 32, 16, warmup=40, seed=8, pad_slots=3)
+    cu = lambda t: t.cuda()
+    O, LSE, _, _, _, S2 = flash_ema_forward(cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]),
+                                            cu(c["W"]), cu(c["rhos"]), c["V"], cu(c["unique"]),
+                                            c["K"], cu(c["Cb"]), return_scores=True)
+    S2 = S2.cpu().double() * np.log(2.0)               # natural-log scores [B, H, K, L]
+    valid = (c["unique"] >= 0)
+    kb = valid.sum(1).double()
+    for b in range(2):
+        s = S2[b][:, valid[b]]                         # [H, K_b, L]
+        lse = torch.logsumexp(torch.cat([s, torch.log(c["V"] - kb[b]).expand(s.shape[0], 1, s.shape[2])], 1), 1)
+        assert torch.allclose(lse, LSE[b].cpu().double(), rtol=1e-5, atol=1e-5)
 
 
 def test_autograd_function_matches_direct_calls():
