@@ -17,6 +17,11 @@ of the reference's PyTorch path) on a bounded slice of the same workload on this
 
 `--workload scan` measures the EMA query scan of configuration 3 instead (B=56, T=2048,
 N=128, c_base from an 8192-token warm-up) in GB/s of algorithmic traffic.
+`--workload gating` measures the query gating forward + backward (mb_gating_fwd/bwd with
+pe_proj folded in) at configuration 2's rows (B=56, T=512, D=512, N=64) in GB/s.
+`--workload model` runs configuration 5: a full SlotTransformerLM training step (6 layers,
+d_model 512, 8 heads, N=64, V=50257, B=56, T=512, bf16 autocast, AdamW, gradient
+clipping) on chunks of synthetic lognormal-length Zipf documents with carried c_base.
 `--workload copy` runs a plain 1 GiB device-to-device copy: the reference dispatch that
 scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes.
 """
@@ -87,40 +92,38 @@ def attention_step(c, timers=None):
     return grads
 
 
-def cpu_baseline_attention(c, seconds=15.0):
+def cpu_baseline_attention(c, seconds=12.0):
     """The oracle's fp32 restatement of the reference attention (sparse form with the
     absent-slot mass, which equals the dense flash_ema_attention.py path), forward and
-    reference backward formulas, on a slice of sequence 0 of the same batch: as many
-    leading steps as fit in about `seconds` (at least 16)."""
+    reference backward formulas, on whole sequences of the same batch (all L steps,
+    each with its own K_b slots), one after another until about `seconds` have passed."""
     from oracle import attention as att
-    from oracle import scan as oscan
     d = c["cpu"]
-    H, hd, N, V = c["H"], c["hd"], c["N"], c["V"]
+    H, hd, N, V, L = c["H"], c["hd"], c["N"], c["V"], c["L"]
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(123)
-    K = int(d["counts"][0])
-    uniq = d["unique"][:1, :K]
-    cb = d["c_base"][:1, :K]
-    Ek = torch.randn(1, K, H * hd, generator=g) * 0.02
-    Ev = torch.randn(1, K, H * hd, generator=g) * 0.02
     W = torch.randn(N, H * hd, generator=g) * 0.02
-    steps, done_steps, elapsed = 16, 0, 0.0
-    while True:
-        x = d["x"][:1, :steps]
-        Q = torch.randn(1, H, steps, hd, generator=g) * 0.02
-        dO = torch.randn(1, H, steps, hd, generator=g)
+    done, elapsed, slots = 0, 0.0, []
+    for b in range(c["B"]):
+        K = int(d["counts"][b])
+        uniq = d["unique"][b:b + 1, :K]
+        cb = d["c_base"][b:b + 1, :K]
+        Ek = torch.randn(1, K, H * hd, generator=g) * 0.02
+        Ev = torch.randn(1, K, H * hd, generator=g) * 0.02
+        Q = torch.randn(1, H, L, hd, generator=g) * 0.02
+        dO = torch.randn(1, H, L, hd, generator=g)
         t = time.perf_counter()
-        att.sparse_backward_formulas(Q, x, Ek, Ev, W, d["rhos"], V, uniq, dO, cb)
-        elapsed = time.perf_counter() - t
-        done_steps = steps
-        if elapsed > seconds / 4 or steps >= c["L"]:
+        att.sparse_backward_formulas(Q, d["x"][b:b + 1], Ek, Ev, W, d["rhos"], V, uniq, dO, cb)
+        elapsed += time.perf_counter() - t
+        done += L
+        slots.append(K)
+        if elapsed > seconds:
             break
-        steps = min(c["L"], steps * 2)
-    return {"value": done_steps / elapsed, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": (f"sequence 0 of the batch (K_b={K} slots), first {done_steps} steps, "
-                       f"forward + reference backward formulas in torch fp32 on {cores} threads; "
-                       f"{elapsed:.1f} s")}
+    return {"value": done / elapsed, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"sequences 0..{len(slots) - 1} of the batch (K_b = {min(slots)}..{max(slots)} "
+                       f"slots), all {L} steps each, forward + reference backward formulas in "
+                       f"torch fp32 on {cores} threads; {elapsed:.1f} s")}
 
 
 def run_attention(args):
@@ -177,24 +180,49 @@ def run_attention(args):
 
 
 def run_scan(args):
+    from mathbrain_amd import _lib
     from mathbrain_amd.ema_query import compute_query_ema_history
     from mathbrain_amd.synthetic import make_batch
     B, T, N, V = 56, 2048, 128, 50257
     d = make_batch(B, T, V, N, 8192, seed=3)
     dev = torch.device("cuda", torch.cuda.current_device())
-    x, rh, cb, u = (d[k].to(dev) for k in ("x", "rhos", "c_base", "unique"))
-    # rotate 4 input copies so consecutive calls do not hit the previous call's lines
-    xs = [x.clone() for _ in range(4)]
+    K = d["unique"].shape[1]
+    rh = d["rhos"].to(dev)
+    u = d["unique"].to(dev)
+    # four input/output sets, rotated, so consecutive calls miss the 256 MB MALL
+    sets = []
+    for _ in range(4):
+        cb = d["c_base"].to(dev)
+        sets.append(dict(x=d["x"].to(dev), cb=cb, out=torch.empty(B, T, N, device=dev),
+                         state=cb.clone(), stamps=torch.empty(B, K, dtype=torch.int32, device=dev)))
+    st = _lib.stream(dev)
+
+    def call(s):
+        _lib.call("mb_ema_query_scan", _lib.ptr(s["x"]), T, 1, B, T, _lib.ptr(rh), N, V,
+                  _lib.ptr(s["cb"]), _lib.ptr(u), K, None, _lib.ptr(s["out"]), _lib.ptr(s["state"]),
+                  _lib.ptr(s["stamps"]), st)
+
     for i in range(args.warmup):
-        compute_query_ema_history(xs[i % 4], rh, V, cb, u, return_state=True)
+        call(sets[i % 4])
     torch.cuda.synchronize()
     t0, t1 = _events()
     t0.record()
     for i in range(args.steps):
-        compute_query_ema_history(xs[i % 4], rh, V, cb, u, return_state=True)
+        call(sets[i % 4])
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
+    # the Python entry point on top (allocations, and a copy of c_init for the state)
+    for i in range(2):
+        compute_query_ema_history(sets[i]["x"], rh, V, sets[i]["cb"], u, return_state=True)
+    torch.cuda.synchronize()
+    w0, w1 = _events()
+    w0.record()
+    for i in range(args.steps):
+        compute_query_ema_history(sets[i % 4]["x"], rh, V, sets[i % 4]["cb"], u, return_state=True)
+    w1.record()
+    torch.cuda.synchronize()
+    wrapper_ms = w0.elapsed_time(w1) / args.steps
     # x + C_seq + touched c_base rows read + lazy state written + stamps
     touched = 0
     for b in range(B):
@@ -206,12 +234,119 @@ def run_scan(args):
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-        "config": {"workload": "cfg3 EMA query scan with final lazy state", "B": B, "T": T,
-                   "N": N, "V": V, "bytes_per_call": nbytes},
+        "config": {"workload": "cfg3 EMA query scan with final lazy state (C-ABI call, outputs "
+                               "preallocated)", "B": B, "T": T, "N": N, "V": V,
+                   "bytes_per_call": nbytes, "python_entry_ms": round(wrapper_ms, 4)},
         "roofline": {"bound": "hbm", "kernel": "ema_query_scan_kernel", "achieved": round(gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "traffic": None},
     }
+
+
+def run_gating(args):
+    from mathbrain_amd import _lib
+    B, L, D, N = 56, 512, 512, 64
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = torch.Generator().manual_seed(0)
+    rows = B * L
+    x_q = torch.randn(rows, D, generator=g).to(dev)
+    C = (torch.rand(rows, N, generator=g) * 50).to(dev)
+    W = (torch.randn(N, D, generator=g) * 0.02).to(dev)
+    ln_w = torch.ones(D, device=dev)
+    ln_b = torch.zeros(D, device=dev)
+    dy = torch.randn(rows, D, generator=g).to(dev)
+    y, dxq, dpre = (torch.empty(rows, D, device=dev) for _ in range(3))
+    mu, rstd = torch.empty(rows, device=dev), torch.empty(rows, device=dev)
+    col = [torch.empty(D, device=dev) for _ in range(3)]
+    st = _lib.stream(dev)
+
+    def fwd():
+        _lib.call("mb_gating_fwd", _lib.ptr(x_q), D, None, 0, None, _lib.ptr(C), N, _lib.ptr(W), N,
+                  _lib.ptr(ln_w), _lib.ptr(ln_b), rows, D, 1, 1e-5, _lib.ptr(y), _lib.ptr(mu),
+                  _lib.ptr(rstd), st)
+
+    def bwd():
+        _lib.call("mb_gating_bwd", _lib.ptr(dy), _lib.ptr(x_q), D, None, 0, None, _lib.ptr(C), N,
+                  _lib.ptr(W), N, _lib.ptr(ln_w), _lib.ptr(mu), _lib.ptr(rstd), rows, D, 1,
+                  _lib.ptr(dxq), _lib.ptr(dpre), *(_lib.ptr(t) for t in col), st)
+
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    ev = [_events() for _ in range(2)]
+    f_ms = b_ms = 0.0
+    for _ in range(args.steps):
+        ev[0][0].record(); fwd(); ev[0][1].record()
+        ev[1][0].record(); bwd(); ev[1][1].record()
+        torch.cuda.synchronize()
+        f_ms += ev[0][0].elapsed_time(ev[0][1])
+        b_ms += ev[1][0].elapsed_time(ev[1][1])
+    f_ms /= args.steps
+    b_ms /= args.steps
+    # algorithmic bytes: fwd reads x_q, C, writes y, mu, rstd; bwd reads dy, x_q, C, mu,
+    # rstd, writes dx_q and dpre
+    fb = rows * (D * 4 * 2 + N * 4 + 8)
+    bb = rows * (D * 4 * 4 + N * 4 + 8)
+    gbs = (fb + bb) / ((f_ms + b_ms) * 1e-3) / 1e9
+    return {"metric": "query gating fwd+bwd GB/s (cfg2 rows: B56 T512 D512 N64)", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(f_ms + b_ms, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "gating fwd+bwd, pe_proj folded in", "rows": rows, "D": D, "N": N,
+                       "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4)},
+            "roofline": {"bound": "hbm", "kernel": "gating_fwd_kernel + gating_bwd_kernel",
+                         "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}
+
+
+def run_model(args):
+    import torch.nn.functional as F
+    from mathbrain_amd.model import SlotTransformerLM
+    from mathbrain_amd.synthetic import make_doc_batch
+    B, T, V, N, D, n_layers, H = 56, 512, 50257, 64, 512, 6, 8
+    dev = torch.device("cuda", torch.cuda.current_device())
+    torch.set_float32_matmul_precision("high")   # train.py:94-95
+    d = make_doc_batch(B, T, V, N, min_hl=1.0, max_hl=2048.0, seed=0)
+    torch.manual_seed(1)
+    model = SlotTransformerLM(V, D, n_layers, H, N=N, dropout=0.1).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
+    x, uniq, cb, tgt = (d[k].to(dev) for k in ("x", "unique", "c_base", "targets"))
+    pm = uniq >= 0
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = model(x, unique_slots=uniq, c_base=cb, pad_mask=pm)
+            loss = F.cross_entropy(logits.view(-1, V), tgt.view(-1), ignore_index=-1)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = _events()
+    t0.record()
+    for _ in range(args.steps):
+        loss = step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    n_params = sum(p.numel() for p in model.parameters())
+    real = int((tgt >= 0).sum())
+    return {"metric": "SlotTransformerLM training step tokens/s (cfg5)", "value": round(B * T / (ms * 1e-3), 1),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 autocast (attention fp32 state, bf16 gate MFMA)",
+            "data": "synthetic lognormal(median 1500) Zipf(1.1) documents, chunked, random init",
+            "config": {"workload": "cfg5 full training step", "layers": n_layers, "d_model": D,
+                       "heads": H, "N": N, "V": V, "B": B, "T": T, "params": n_params,
+                       "K_max": int(uniq.shape[1]), "unpadded_tokens": real,
+                       "steps_per_s": round(1e3 / ms, 3),
+                       "unpadded_tokens_per_s": round(real / (ms * 1e-3), 1),
+                       "loss": round(float(loss), 4)}}
 
 
 def run_copy(args):
@@ -242,17 +377,19 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("attention", "scan", "copy"), default="attention")
+    ap.add_argument("--workload", choices=("attention", "scan", "gating", "model", "copy"),
+                    default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(sharding across GPUs is described in DESIGN.md, not run)", file=sys.stderr)
+              "(how the path would shard is documented, not run)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         sys.exit(1)
-    run = {"attention": run_attention, "scan": run_scan, "copy": run_copy}[args.workload]
+    run = {"attention": run_attention, "scan": run_scan, "gating": run_gating, "model": run_model,
+           "copy": run_copy}[args.workload]
     line = run(args)
     print(json.dumps(line), flush=True)
 

@@ -155,6 +155,54 @@ int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
                      int Br, int64_t V_total, int flags, const float *scores, float *dQ,
                      float *dE_k, float *dE_v, float *dW_pe, void *stream);
 
+/*
+ * Fused symmetric query gating, forward.  Replaces _fused_gating_fwd and the forward of
+ * FusedGatingFunction (mathbrain/triton_fused_gating.py:12-57, :122-148); with the
+ * projection folded in, also the pe_proj GEMM and bias of
+ * fused_apply_symmetric_query_gating (:179-186).  Per row r and column d:
+ *
+ *   pre[r,d] = p_pre[r,d] + bias[d]                    when p_pre != NULL
+ *            = sum_n (C_seq[r,n] + 1) W_pe[n,d]         when p_pre == NULL
+ *   y[r,:]   = LayerNorm_eps(x_q[r,:] * SiLU(pre[r,:])) * ln_w + ln_b
+ *
+ * (the linear gate pre instead of SiLU(pre) when use_silu == 0).
+ *
+ *   x_q     [rows, D] fp32, row stride xq_row_stride (columns contiguous)
+ *   p_pre   [rows, D] fp32, row stride pp_row_stride, or NULL; bias [D] with p_pre
+ *   C_seq   [rows, N] fp32, row stride c_row_stride, and W_pe [N, D] contiguous
+ *           (pe_proj.weight transposed): used when p_pre is NULL
+ *   y       [rows, D] contiguous output; mu, rstd [rows] outputs (LayerNorm statistics,
+ *           consumed by mb_gating_bwd)
+ *
+ * Supported: D <= 1024, N <= 1024.
+ */
+int mb_gating_fwd(const float *x_q, int64_t xq_row_stride, const float *p_pre,
+                  int64_t pp_row_stride, const float *bias, const float *C_seq,
+                  int64_t c_row_stride, const float *W_pe, int N, const float *ln_w,
+                  const float *ln_b, int64_t rows, int D, int use_silu, float eps, float *y,
+                  float *mu, float *rstd, void *stream);
+
+/*
+ * Fused symmetric query gating, backward.  Replaces _fused_gating_bwd and the backward of
+ * FusedGatingFunction (mathbrain/triton_fused_gating.py:61-119, :150-177).  Inputs as
+ * mb_gating_fwd (the same p_pre / C_seq choice), plus dy [rows, D] contiguous and the
+ * forward's mu, rstd.  Outputs, all contiguous:
+ *
+ *   dx_q   [rows, D]   dx_emb * g
+ *   dp_pre [rows, D]   dx_emb * x_q * SiLU'(pre): the gradient of p_pre, or, with the
+ *                      folded projection, of pre (then dW_pe = dp_pre^T (C_seq + 1))
+ *   dbias, dln_w, dln_b [D]  column sums of dp_pre, dy * x_hat and dy
+ *
+ * The column sums are cleared by the call (fill kernel) and accumulated with fp32
+ * atomics, one per column and workgroup: their summation order is not fixed.
+ */
+int mb_gating_bwd(const float *dy, const float *x_q, int64_t xq_row_stride, const float *p_pre,
+                  int64_t pp_row_stride, const float *bias, const float *C_seq,
+                  int64_t c_row_stride, const float *W_pe, int N, const float *ln_w,
+                  const float *mu, const float *rstd, int64_t rows, int D, int use_silu,
+                  float *dx_q, float *dp_pre, float *dbias, float *dln_w, float *dln_b,
+                  void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,370 @@
+// Fused symmetric query gating on gfx950: forward and backward row kernels.
+//
+// Replaces _fused_gating_fwd / _fused_gating_bwd and FusedGatingFunction
+// (mathbrain/triton_fused_gating.py:12-57, :61-119, :122-177).  Per row r (one (b, t)
+// position) and column d:
+//   pre[r,d]  = p_pre[r,d] + bias[d]                         (FusedGatingFunction form)
+//             = sum_n (C_seq[r,n] + 1) W_pe[n,d]             (projection folded in; this is
+//               pe_proj(C_seq) + pe_proj.weight.sum(1), triton_fused_gating.py:180-183)
+//   g         = SiLU(pre)  (or pre for the linear gate)
+//   x_emb     = x_q * g
+//   y         = LayerNorm_eps(x_emb) * ln_w + ln_b
+// The backward is the reference's closed form (:95-118): with x_hat = (x_emb - mu) rstd,
+//   dx_hat = dy ln_w,  dx_emb = (dx_hat - mean(dx_hat) - x_hat mean(dx_hat x_hat)) rstd
+//   dx_q = dx_emb g,   dp_pre = dx_emb x_q SiLU'(pre)
+// and the column sums dln_w = sum_r dy x_hat, dln_b = sum_r dy, dbias = sum_r dp_pre
+// (the reference writes [rows, D] partials and reduces them with torch, :159-160,
+// :173-175; here each workgroup reduces its rows in registers and adds once).
+//
+// Layout: a workgroup of 256 threads owns a tile of kRows rows; thread i owns columns
+// i, i + 256, ... (coalesced row reads and writes).  The per-element work runs
+// column-parallel, the LayerNorm row statistics one wave per row over a copy of the
+// tile in LDS.  x_emb and the gate are recomputed in the backward instead of being
+// stored (the reference saves x_emb and p_gate, two more [rows, D] tensors).
+#include "common.h"
+
+#include <algorithm>
+
+namespace mb {
+
+constexpr int kGateThreads = 256;
+constexpr int kGateRows = 8;
+
+struct GateArgs {
+    const float* xq;
+    int64_t xq_sr;  // row stride of x_q (elements); columns contiguous
+    const float* pp;
+    int64_t pp_sr;
+    const float* bias;
+    const float* C;
+    int64_t c_sr;
+    const float* W;  // [N, D]
+    int N;
+    const float* lnw;
+    const float* lnb;
+    int64_t rows;
+    int D;
+    float eps;
+    float* y;
+    float* mu;
+    float* rstd;
+    // backward
+    const float* dy;
+    float* dxq;
+    float* dpp;
+    float* dbias;
+    float* dlnw;
+    float* dlnb;
+};
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Gate pre-activation of rows r0 .. r0 + kGateRows - 1 at column col.  `cst` holds
+// (C_seq + 1) transposed, [N][kGateRows], for the folded projection.
+template <bool FUSED>
+__device__ inline void gate_pre(const GateArgs& a, int64_t r0, int nr, int col, const float* cst,
+                                float (&pre)[kGateRows]) {
+    if (FUSED) {
+#pragma unroll
+        for (int r = 0; r < kGateRows; ++r) pre[r] = 0.f;
+        for (int n = 0; n < a.N; ++n) {
+            const float w = a.W[(int64_t)n * a.D + col];
+            const float4 c0 = *reinterpret_cast<const float4*>(cst + n * kGateRows);
+            const float4 c1 = *reinterpret_cast<const float4*>(cst + n * kGateRows + 4);
+            pre[0] = __builtin_fmaf(c0.x, w, pre[0]);
+            pre[1] = __builtin_fmaf(c0.y, w, pre[1]);
+            pre[2] = __builtin_fmaf(c0.z, w, pre[2]);
+            pre[3] = __builtin_fmaf(c0.w, w, pre[3]);
+            pre[4] = __builtin_fmaf(c1.x, w, pre[4]);
+            pre[5] = __builtin_fmaf(c1.y, w, pre[5]);
+            pre[6] = __builtin_fmaf(c1.z, w, pre[6]);
+            pre[7] = __builtin_fmaf(c1.w, w, pre[7]);
+        }
+    } else {
+        const float bv = a.bias[col];
+#pragma unroll
+        for (int r = 0; r < kGateRows; ++r)
+            pre[r] = r < nr ? a.pp[(r0 + r) * a.pp_sr + col] + bv : 0.f;
+    }
+}
+
+__device__ inline float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Stages (C_seq + 1)^T of the tile: cst[n][r].
+__device__ inline void stage_counts(const GateArgs& a, int64_t r0, int nr, float* cst) {
+    for (int i = threadIdx.x; i < kGateRows * a.N; i += blockDim.x) {
+        const int r = i / a.N;
+        const int n = i % a.N;
+        cst[n * kGateRows + r] = r < nr ? a.C[(r0 + r) * a.c_sr + n] + 1.0f : 0.f;
+    }
+}
+
+template <int CPT, bool FUSED, bool SILU>
+__global__ void __launch_bounds__(kGateThreads)
+gating_fwd_kernel(GateArgs a) {
+    extern __shared__ __align__(16) float gsm[];
+    float* xe = gsm;                          // [kGateRows][D]
+    float* stats = xe + kGateRows * a.D;      // [kGateRows][2]
+    float* cst = stats + 2 * kGateRows;       // [N][kGateRows]
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int64_t ntiles = (a.rows + kGateRows - 1) / kGateRows;
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t r0 = tile * kGateRows;
+        const int nr = (int)std::min<int64_t>(kGateRows, a.rows - r0);
+        if (FUSED) {
+            stage_counts(a, r0, nr, cst);
+            __syncthreads();
+        }
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int col = tid + j * kGateThreads;
+            if (col >= a.D) break;
+            float pre[kGateRows];
+            gate_pre<FUSED>(a, r0, nr, col, cst, pre);
+#pragma unroll
+            for (int r = 0; r < kGateRows; ++r) {
+                if (r >= nr) break;
+                const float g = SILU ? pre[r] * sigmoidf_(pre[r]) : pre[r];
+                xe[r * a.D + col] = a.xq[(r0 + r) * a.xq_sr + col] * g;
+            }
+        }
+        __syncthreads();
+        for (int r = wave; r < nr; r += kGateThreads / 64) {
+            float s = 0.f;
+            for (int c = lane; c < a.D; c += 64) s += xe[r * a.D + c];
+            const float mean = wave_sum(s) / (float)a.D;
+            float v = 0.f;
+            for (int c = lane; c < a.D; c += 64) {
+                const float dd = xe[r * a.D + c] - mean;
+                v = __builtin_fmaf(dd, dd, v);
+            }
+            const float var = wave_sum(v) / (float)a.D;
+            const float rs = 1.0f / sqrtf(var + a.eps);
+            if (lane == 0) {
+                stats[2 * r] = mean;
+                stats[2 * r + 1] = rs;
+                a.mu[r0 + r] = mean;
+                a.rstd[r0 + r] = rs;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int col = tid + j * kGateThreads;
+            if (col >= a.D) break;
+            const float w = a.lnw[col];
+            const float bb = a.lnb[col];
+            for (int r = 0; r < nr; ++r)
+                a.y[(r0 + r) * a.D + col] = (xe[r * a.D + col] - stats[2 * r]) * stats[2 * r + 1] * w + bb;
+        }
+        __syncthreads();
+    }
+}
+
+template <int CPT, bool FUSED, bool SILU>
+__global__ void __launch_bounds__(kGateThreads)
+gating_bwd_kernel(GateArgs a) {
+    extern __shared__ __align__(16) float gsm[];
+    float* xh = gsm;                           // [kGateRows][D]  x_hat
+    float* dxh = xh + kGateRows * a.D;         // [kGateRows][D]  dy * ln_w
+    float* stats = dxh + kGateRows * a.D;      // [kGateRows][2]  c1, c2
+    float* cst = stats + 2 * kGateRows;        // [N][kGateRows]
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    float acc_w[CPT], acc_b[CPT], acc_p[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) acc_w[j] = acc_b[j] = acc_p[j] = 0.f;
+    const int64_t ntiles = (a.rows + kGateRows - 1) / kGateRows;
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t r0 = tile * kGateRows;
+        const int nr = (int)std::min<int64_t>(kGateRows, a.rows - r0);
+        if (FUSED) {
+            stage_counts(a, r0, nr, cst);
+            __syncthreads();
+        }
+        float gv[CPT][kGateRows], ds[CPT][kGateRows];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int col = tid + j * kGateThreads;
+            if (col >= a.D) break;
+            float pre[kGateRows];
+            gate_pre<FUSED>(a, r0, nr, col, cst, pre);
+            const float w = a.lnw[col];
+#pragma unroll
+            for (int r = 0; r < kGateRows; ++r) {
+                if (r >= nr) break;
+                float g = pre[r], dsil = 1.f;
+                if (SILU) {
+                    const float sg = sigmoidf_(pre[r]);
+                    g = pre[r] * sg;
+                    dsil = g + sg * (1.0f - g);  // SiLU' (triton_fused_gating.py:113-114)
+                }
+                gv[j][r] = g;
+                ds[j][r] = dsil;
+                const float x = a.xq[(r0 + r) * a.xq_sr + col];
+                const float dyv = a.dy[(r0 + r) * a.D + col];
+                const float xhat = (x * g - a.mu[r0 + r]) * a.rstd[r0 + r];
+                xh[r * a.D + col] = xhat;
+                dxh[r * a.D + col] = dyv * w;
+                acc_w[j] = __builtin_fmaf(dyv, xhat, acc_w[j]);
+                acc_b[j] += dyv;
+            }
+        }
+        __syncthreads();
+        for (int r = wave; r < nr; r += kGateThreads / 64) {
+            float s1 = 0.f, s2 = 0.f;
+            for (int c = lane; c < a.D; c += 64) {
+                const float v = dxh[r * a.D + c];
+                s1 += v;
+                s2 = __builtin_fmaf(v, xh[r * a.D + c], s2);
+            }
+            s1 = wave_sum(s1);
+            s2 = wave_sum(s2);
+            if (lane == 0) {
+                stats[2 * r] = s1 / (float)a.D;
+                stats[2 * r + 1] = s2 / (float)a.D;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int col = tid + j * kGateThreads;
+            if (col >= a.D) break;
+#pragma unroll
+            for (int r = 0; r < kGateRows; ++r) {
+                if (r >= nr) break;
+                const float dxe = (dxh[r * a.D + col] - stats[2 * r] - xh[r * a.D + col] * stats[2 * r + 1]) *
+                                  a.rstd[r0 + r];
+                const float x = a.xq[(r0 + r) * a.xq_sr + col];
+                a.dxq[(r0 + r) * a.D + col] = dxe * gv[j][r];
+                const float dp = dxe * x * ds[j][r];
+                a.dpp[(r0 + r) * a.D + col] = dp;
+                acc_p[j] += dp;
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int col = tid + j * kGateThreads;
+        if (col >= a.D) break;
+        atomicAdd(&a.dlnw[col], acc_w[j]);
+        atomicAdd(&a.dlnb[col], acc_b[j]);
+        atomicAdd(&a.dbias[col], acc_p[j]);
+    }
+}
+
+__global__ void gate_zero_kernel(float* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0.f;
+}
+
+static int gate_grid(int64_t rows) {
+    const int64_t ntiles = (rows + kGateRows - 1) / kGateRows;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(ntiles, 256 * 8));
+}
+
+template <bool BWD>
+static int gate_launch(const GateArgs& a, bool fused, bool silu, hipStream_t st) {
+    const int cpt = (a.D + kGateThreads - 1) / kGateThreads;
+    const size_t lds = ((BWD ? 2 : 1) * (size_t)kGateRows * a.D + 2 * kGateRows +
+                        (fused ? (size_t)kGateRows * a.N : 0)) * sizeof(float);
+    const dim3 grid(gate_grid(a.rows));
+#define MB_GATE_K(C, F, S) (BWD ? gating_bwd_kernel<C, F, S> : gating_fwd_kernel<C, F, S>)
+#define MB_GATE_CPT(C)                                                                          \
+    do {                                                                                        \
+        auto k = fused ? (silu ? MB_GATE_K(C, true, true) : MB_GATE_K(C, true, false))          \
+                       : (silu ? MB_GATE_K(C, false, true) : MB_GATE_K(C, false, false));       \
+        if (lds > 64 * 1024) {                                                                  \
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            if (e != hipSuccess) {                                                              \
+                (void)hipGetLastError();                                                        \
+                return fail((int)e, "gating: LDS attribute: %s", hipGetErrorString(e));         \
+            }                                                                                   \
+        }                                                                                       \
+        hipLaunchKernelGGL(k, grid, dim3(kGateThreads), lds, st, a);                            \
+    } while (0)
+    switch (cpt) {
+        case 1: MB_GATE_CPT(1); break;
+        case 2: MB_GATE_CPT(2); break;
+        case 3: MB_GATE_CPT(3); break;
+        case 4: MB_GATE_CPT(4); break;
+        default: return fail(MB_ERR_UNSUPPORTED, "gating: D=%d > %d", a.D, 4 * kGateThreads);
+    }
+#undef MB_GATE_CPT
+#undef MB_GATE_K
+    return check_launch(BWD ? "mb_gating_bwd" : "mb_gating_fwd");
+}
+
+static int gate_validate(const char* who, const GateArgs& a, bool fused) {
+    MB_REQUIRE(a.rows >= 0, "%s: negative rows %lld", who, (long long)a.rows);
+    MB_REQUIRE(a.D >= 1, "%s: D=%d must be >= 1", who, a.D);
+    if (a.D > 4 * kGateThreads) return fail(MB_ERR_UNSUPPORTED, "%s: D=%d > %d", who, a.D, 4 * kGateThreads);
+    MB_REQUIRE(a.xq_sr >= a.D, "%s: x_q row stride %lld < D=%d", who, (long long)a.xq_sr, a.D);
+    if (fused) {
+        MB_REQUIRE(a.N >= 1 && a.N <= 1024, "%s: N=%d out of range 1..1024", who, a.N);
+        MB_REQUIRE(a.c_sr >= a.N, "%s: C_seq row stride %lld < N=%d", who, (long long)a.c_sr, a.N);
+    } else {
+        MB_REQUIRE(a.pp_sr >= a.D, "%s: p_pre row stride %lld < D=%d", who, (long long)a.pp_sr, a.D);
+    }
+    return MB_OK;
+}
+
+}  // namespace mb
+
+using namespace mb;
+
+extern "C" int mb_gating_fwd(const float* x_q, int64_t xq_row_stride, const float* p_pre,
+                             int64_t pp_row_stride, const float* bias, const float* C_seq,
+                             int64_t c_row_stride, const float* W_pe, int N, const float* ln_w,
+                             const float* ln_b, int64_t rows, int D, int use_silu, float eps,
+                             float* y, float* mu, float* rstd, void* stream) {
+    GateArgs a{};
+    a.xq = x_q; a.xq_sr = xq_row_stride; a.pp = p_pre; a.pp_sr = pp_row_stride; a.bias = bias;
+    a.C = C_seq; a.c_sr = c_row_stride; a.W = W_pe; a.N = N; a.lnw = ln_w; a.lnb = ln_b;
+    a.rows = rows; a.D = D; a.eps = eps; a.y = y; a.mu = mu; a.rstd = rstd;
+    const bool fused = p_pre == nullptr;
+    int rc = gate_validate("mb_gating_fwd", a, fused);
+    if (rc) return rc;
+    if (rows == 0) return MB_OK;
+    MB_REQUIRE(x_q && ln_w && ln_b && y && mu && rstd, "mb_gating_fwd: null pointer");
+    MB_REQUIRE(fused ? (C_seq && W_pe) : (bias != nullptr),
+               "mb_gating_fwd: need p_pre and bias, or C_seq and W_pe");
+    return gate_launch<false>(a, fused, use_silu != 0, (hipStream_t)stream);
+}
+
+extern "C" int mb_gating_bwd(const float* dy, const float* x_q, int64_t xq_row_stride,
+                             const float* p_pre, int64_t pp_row_stride, const float* bias,
+                             const float* C_seq, int64_t c_row_stride, const float* W_pe, int N,
+                             const float* ln_w, const float* mu, const float* rstd, int64_t rows,
+                             int D, int use_silu, float* dx_q, float* dp_pre, float* dbias,
+                             float* dln_w, float* dln_b, void* stream) {
+    GateArgs a{};
+    a.dy = dy; a.xq = x_q; a.xq_sr = xq_row_stride; a.pp = p_pre; a.pp_sr = pp_row_stride;
+    a.bias = bias; a.C = C_seq; a.c_sr = c_row_stride; a.W = W_pe; a.N = N; a.lnw = ln_w;
+    a.mu = const_cast<float*>(mu); a.rstd = const_cast<float*>(rstd);
+    a.rows = rows; a.D = D;
+    a.dxq = dx_q; a.dpp = dp_pre; a.dbias = dbias; a.dlnw = dln_w; a.dlnb = dln_b;
+    const bool fused = p_pre == nullptr;
+    int rc = gate_validate("mb_gating_bwd", a, fused);
+    if (rc) return rc;
+    MB_REQUIRE(dbias && dln_w && dln_b, "mb_gating_bwd: null column-sum output");
+    hipStream_t st = (hipStream_t)stream;
+    // The column sums are accumulated with atomics: clear them first (fill kernel).
+    hipLaunchKernelGGL(gate_zero_kernel, dim3(1), dim3(256), 0, st, dbias, D);
+    hipLaunchKernelGGL(gate_zero_kernel, dim3(1), dim3(256), 0, st, dln_w, D);
+    hipLaunchKernelGGL(gate_zero_kernel, dim3(1), dim3(256), 0, st, dln_b, D);
+    if ((rc = check_launch("mb_gating_bwd: clear"))) return rc;
+    if (rows == 0) return MB_OK;
+    MB_REQUIRE(dy && x_q && ln_w && mu && rstd && dx_q && dp_pre, "mb_gating_bwd: null pointer");
+    MB_REQUIRE(fused ? (C_seq && W_pe) : (bias != nullptr),
+               "mb_gating_bwd: need p_pre and bias, or C_seq and W_pe");
+    return gate_launch<true>(a, fused, use_silu != 0, st);
+}

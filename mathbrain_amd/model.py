@@ -1,0 +1,175 @@
+"""SlotTransformerLM over the gfx950 hot path.
+
+Drop-in for mathbrain/model.py (:11-186): the same modules, parameter names, constructor
+arguments and forward signatures, so checkpoints and train.py's calls carry over.  The
+hot path runs in the HIP kernels: the query scan (``compute_query_ema_history``), the
+key-side chunk states (``precompute_boundaries``), the gating with pe_proj folded in
+(``fused_apply_symmetric_query_gating``) and flash-EMA attention (``FlashEMAFunction``).
+RMSNorm, SwiGLU, the slot K/V projections and the tied lm_head stay torch modules, as in
+the reference.  The reference's CPU branch (dense attention over the whole vocabulary,
+model.py:88-99) is not a product path here: CPU tensors raise NotImplementedError.
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .ema_query import compute_query_ema_history
+from .flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
+from .fused_gating import fused_apply_symmetric_query_gating
+
+
+class RMSNorm(nn.Module):
+    """model.py:11-19."""
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x):
+        variance = x.pow(2).mean(-1, keepdim=True)
+        return self.weight * (x * torch.rsqrt(variance + self.eps))
+
+
+class SwiGLU(nn.Module):
+    """model.py:21-29."""
+
+    def __init__(self, dim: int, hidden_dim: int):
+        super().__init__()
+        self.w1 = nn.Linear(dim, hidden_dim, bias=False)
+        self.w2 = nn.Linear(hidden_dim, dim, bias=False)
+        self.w3 = nn.Linear(dim, hidden_dim, bias=False)
+
+    def forward(self, x):
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+
+class SlotAttentionLayer(nn.Module):
+    """Multiplicative EMA cross-attention over the sequence's unique slots
+    (model.py:32-102): memory = ln_kv(E[slots]), K = k_proj(memory), V = v_proj(memory),
+    keys and values gated by SiLU(pe_proj(C)) inside the flash-EMA kernel."""
+
+    def __init__(self, d_model: int, n_heads: int, dropout: float, n_scales: int, use_silu: bool = True):
+        super().__init__()
+        assert d_model % n_heads == 0
+        self.n_heads = n_heads
+        self.head_dim = d_model // n_heads
+        self.q_proj = nn.Linear(d_model, d_model, bias=False)
+        self.k_proj = nn.Linear(d_model, d_model, bias=False)
+        self.v_proj = nn.Linear(d_model, d_model, bias=False)
+        self.o_proj = nn.Linear(d_model, d_model, bias=False)
+        self.pe_proj = nn.Linear(n_scales, d_model, bias=False)
+        self.ln_kv = nn.LayerNorm(d_model)
+        self.ln_q = nn.LayerNorm(d_model)
+        self.resid_dropout = nn.Dropout(dropout)
+        self.use_silu = use_silu
+
+    def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None):
+        B, L, D = x_q.shape
+        if unique_tensor is None or C_bounds is None:
+            # model.py:88-99 runs the dense all-vocabulary reference here; it is the CPU
+            # reference's path, not this implementation's.
+            raise NotImplementedError(
+                "SlotAttentionLayer: needs unique_tensor and C_bounds (the dense all-vocabulary "
+                "path is the reference's CPU fallback, not part of this implementation)")
+        # 1. slot K/V projections (model.py:63-68)
+        E_active = F.embedding(torch.clamp(unique_tensor, min=0), E_slots)
+        memory_base = self.ln_kv(E_active)
+        E_k_active = self.k_proj(memory_base)
+        E_v_active = self.v_proj(memory_base)
+        # 2. query gating (model.py:75)
+        Q_t = fused_apply_symmetric_query_gating(x_q, C_seq, self.pe_proj, self.ln_q, self.q_proj,
+                                                 self.use_silu)
+        # 3. gated cross-attention (model.py:79-87)
+        H = self.n_heads
+        hd = D // H
+        Q_mha = Q_t.view(B, L, H, hd).transpose(1, 2)
+        W_pe_t = self.pe_proj.weight.t()
+        out_mha = FlashEMAFunction.apply(Q_mha, x, E_k_active, E_v_active, W_pe_t, rhos,
+                                         E_slots.shape[0], unique_tensor, K_max, C_bounds, self.use_silu)
+        out = out_mha.transpose(1, 2).reshape(B, L, D)
+        out = self.o_proj(out)
+        return self.resid_dropout(out)
+
+
+class SlotTransformerBlock(nn.Module):
+    """model.py:105-116."""
+
+    def __init__(self, d_model, n_heads, d_ff, dropout, n_scales, use_silu=True):
+        super().__init__()
+        self.attn_norm = RMSNorm(d_model)
+        self.attn = SlotAttentionLayer(d_model, n_heads, dropout, n_scales, use_silu)
+        self.ffn_norm = RMSNorm(d_model)
+        self.ffn = SwiGLU(d_model, d_ff)
+
+    def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None):
+        h = x_q + self.attn(self.attn_norm(x_q), x, E_slots, rhos, C_seq, unique_tensor, K_max, C_bounds)
+        h = h + self.ffn(self.ffn_norm(h))
+        return h
+
+
+class SlotTransformerLM(nn.Module):
+    """model.py:119-186.  forward(x, unique_slots=None, inverse_indices=None, c_base=None,
+    doc_ids=None, pad_mask=None) -> logits [B, L, vocab_size].
+
+    With ``unique_slots`` and ``pad_mask`` (the data loader's history-expanded slots) the
+    slots are those, padded with -1 where pad_mask is False; otherwise the sorted unique
+    tokens of each row (``_build_unique_index``) with no carried state.  As in the
+    reference, ``inverse_indices`` and ``doc_ids`` are accepted and unused (a chunk is one
+    document).
+    """
+
+    def __init__(self, vocab_size, d_model, n_layers, n_heads, N=16, dropout=0.1, use_silu=True,
+                 ema_dropout=0.0, min_hl=1.0, max_hl=2048.0):
+        super().__init__()
+        self.vocab_size = vocab_size
+        self.d_model = d_model
+        self.n_scales = N
+        self.ema_dropout = ema_dropout
+        half_lives = torch.logspace(math.log10(min_hl), math.log10(max_hl), self.n_scales)
+        rhos = torch.exp(-torch.log(torch.tensor(2.0)) / half_lives)
+        self.register_buffer("ema_rhos", rhos)
+        self.embed = nn.Embedding(vocab_size, d_model)
+        d_ff = 256 * ((int(8 * d_model / 3) + 255) // 256)
+        self.layers = nn.ModuleList([
+            SlotTransformerBlock(d_model, n_heads, d_ff, dropout, self.n_scales, use_silu)
+            for _ in range(n_layers)
+        ])
+        self.final_norm = RMSNorm(d_model)
+        self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
+        self.lm_head.weight = self.embed.weight
+
+    def forward(self, x, unique_slots=None, inverse_indices=None, c_base=None, doc_ids=None, pad_mask=None):
+        device = x.device
+        if device.type != "cuda":
+            raise NotImplementedError(
+                "SlotTransformerLM: this implementation runs on an MI355X GPU only "
+                "(the reference's CPU path is its dense PyTorch fallback)")
+        E_slots = self.embed.weight
+        x_q = self.embed(x)
+        # scans hoisted once for all layers (model.py:157, 162-180)
+        C_seq = compute_query_ema_history(x, self.ema_rhos, self.vocab_size, c_base, unique_slots)
+        if self.ema_dropout > 0 and self.training:
+            C_seq = F.dropout(C_seq, p=self.ema_dropout, training=True)
+        if unique_slots is not None and pad_mask is not None:
+            unique_tensor = unique_slots.masked_fill(~pad_mask, -1)
+            K_max = max(int(pad_mask.sum(dim=1).max().item()), 16)
+            unique_tensor = unique_tensor[:, :K_max]
+            c_base_kv = c_base[:, :K_max, :] if c_base is not None else None
+            if unique_tensor.shape[1] < K_max:
+                # fewer than 16 slots in every row: pad the slot list to the 16 the
+                # reference's K_max floor asks for (model.py:170), with -1
+                pad = K_max - unique_tensor.shape[1]
+                unique_tensor = F.pad(unique_tensor, (0, pad), value=-1)
+                if c_base_kv is not None:
+                    c_base_kv = F.pad(c_base_kv, (0, 0, 0, pad))
+        else:
+            unique_tensor, K_max = _build_unique_index(x, device)
+            c_base_kv = None
+        C_bounds = precompute_boundaries(x, unique_tensor, self.ema_rhos, 64, c_init=c_base_kv)
+        for layer in self.layers:
+            x_q = layer(x_q, x, E_slots, self.ema_rhos, C_seq, unique_tensor, K_max, C_bounds)
+        x_q = self.final_norm(x_q)
+        return self.lm_head(x_q)

@@ -80,3 +80,62 @@ def make_batch(B, T, V, N, warmup, alpha=1.1, min_hl=1.0, max_hl=4096.0, seed=0,
         c_base[b, :counts[b]] = cbs[b]
     return dict(x=x, unique=unique, c_base=c_base, counts=counts, rhos=rhos, pad_len=pad_len,
                 history=hist)
+
+
+def make_doc_batch(B, T, V, N, alpha=1.1, median_len=1500, sigma=1.0, min_hl=1.0, max_hl=4096.0,
+                   seed=0, max_history=8192):
+    """Chunks of synthetic documents, shaped like the reference's training batches
+    (mathbrain/data.py:95-148, collate :211-235).  Each row is one chunk of a document
+    whose length is lognormal (median ``median_len``); the chunk starts at a random
+    multiple of T inside the document, the tokens before it (at most ``max_history``)
+    are its history, and a chunk that runs past the document end is padded with token 0
+    and masked (``targets`` = -1, as train.py:320-323 masks padding).  Returns the
+    make_batch dict plus ``targets`` [B, T] (next token or -1) and ``lengths`` [B]."""
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(V, generator=gen)
+    rhos = rhos_from_half_lives(N, min_hl, max_hl)
+    xs, hists, lens = [], [], []
+    for b in range(B):
+        Ld = int(math.exp(math.log(median_len) + sigma * float(torch.randn(1, generator=gen))))
+        Ld = max(2, min(Ld, max_history + T))
+        n_chunks = (Ld + T - 1) // T
+        start = T * int(torch.randint(0, n_chunks, (1,), generator=gen))
+        doc = zipf_tokens((Ld + 1,), V, alpha, gen, perm)
+        chunk = doc[start:min(start + T + 1, Ld + 1)]
+        hists.append(doc[max(0, start - max_history):start])
+        xs.append(chunk)
+        lens.append(min(T, chunk.numel() - 1))
+    x = torch.zeros(B, T, dtype=torch.int64)
+    targets = torch.full((B, T), -1, dtype=torch.int64)
+    for b in range(B):
+        n = lens[b]
+        x[b, :n] = xs[b][:n]
+        targets[b, :n] = xs[b][1:n + 1]
+    slots, cbs = [], []
+    for b in range(B):
+        cu = torch.unique(x[b, :lens[b]])
+        h = hists[b]
+        W = h.numel()
+        if W:
+            w = rhos.double().unsqueeze(0).pow(torch.arange(W, 0, -1, dtype=torch.float64).unsqueeze(1))
+            hu, inv = torch.unique(h, return_inverse=True)
+            state_h = torch.zeros(hu.numel(), N, dtype=torch.float64).index_add_(0, inv, w)
+            s = torch.cat([cu, hu[~torch.isin(hu, cu)]])
+            cb = torch.zeros(s.numel(), N, dtype=torch.float64)
+            idx = torch.searchsorted(hu, s).clamp(max=hu.numel() - 1)
+            hit = hu[idx] == s
+            cb[hit] = state_h[idx[hit]]
+        else:
+            s = cu
+            cb = torch.zeros(s.numel(), N, dtype=torch.float64)
+        slots.append(s)
+        cbs.append(cb.to(torch.float32))
+    counts = torch.tensor([s.numel() for s in slots], dtype=torch.int64)
+    K_max = int(counts.max())
+    unique = torch.full((B, K_max), -1, dtype=torch.int64)
+    c_base = torch.zeros(B, K_max, N, dtype=torch.float32)
+    for b in range(B):
+        unique[b, :counts[b]] = slots[b]
+        c_base[b, :counts[b]] = cbs[b]
+    return dict(x=x, unique=unique, c_base=c_base, counts=counts, rhos=rhos, targets=targets,
+                lengths=torch.tensor(lens, dtype=torch.int64))

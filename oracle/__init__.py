@@ -18,8 +18,8 @@ attention  Dense flash-EMA attention (mathbrain/flash_ema_attention.py:19-85,
            update so autograd can differentiate it) and the sparse unique-slot
            form with the absent-slot softmax mass.
 gating     Fused symmetric query gating (mathbrain/triton_fused_gating.py:
-           264-282, CPU branch) and its closed-form backward
-           (triton_fused_gating.py:145-204).
+           179-197, CPU branch :187-195) and its closed-form backward
+           (triton_fused_gating.py:61-119, :173-175).
 
 Pinning status (every function is checked in tests/test_oracle_*.py):
   scan.query_scan          pinned: reference KATs + closed form + chunk invariance

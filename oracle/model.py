@@ -1,0 +1,99 @@
+"""TEST INFRASTRUCTURE ONLY: CPU restatement of SlotTransformerLM's forward (the checker).
+
+``lm_forward`` evaluates mathbrain/model.py:144-186 from a parameter dict keyed like the
+module's state_dict, in whatever dtype the parameters have (float64 in the tests), with
+autograd intact so parameter gradients can be compared.  It composes the other oracle
+pieces: the query scan (``scan.query_scan``), the gating (``gating.forward``) and the
+attention, either
+
+* ``attention="sparse"``: the device path of model.py:63-87 -- slot K/V projections of
+  the sequence's unique slots and unique-slot attention with the absent-slot mass and the
+  key-side c_base (``attention.sparse``), or
+* ``attention="dense"``: the reference's CPU path of model.py:88-99 -- K/V projections of
+  the whole vocabulary and the dense all-slot attention (``attention.dense``), which
+  starts every key counter at zero.
+
+Pinning: with no carried state (c_base None) the two must agree (dense == sparse + absent
+mass at model level), which tests/test_oracle_model.py checks in float64.
+"""
+import torch
+import torch.nn.functional as F
+
+from . import attention as att
+from . import gating
+from . import scan
+
+
+def rmsnorm(x, w, eps=1e-6):
+    """model.py:17-19."""
+    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+
+
+def swiglu(x, w1, w2, w3):
+    """model.py:28-29 (nn.Linear weights are [out, in])."""
+    return (F.silu(x @ w1.t()) * (x @ w3.t())) @ w2.t()
+
+
+def unique_index(x):
+    """_build_unique_index (triton_flash_ema.py:475-507): sorted unique ids per row,
+    -1 padded to K_max = max(max count, 16)."""
+    rows = [torch.unique(r) for r in x]
+    K = max(max(r.numel() for r in rows), 16)
+    out = torch.full((x.shape[0], K), -1, dtype=torch.int64)
+    for b, r in enumerate(rows):
+        out[b, : r.numel()] = r
+    return out
+
+
+def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_base=None,
+               pad_mask=None, use_silu=True, attention="sparse", gate_round=None):
+    """Logits [B, L, V] of SlotTransformerLM.forward (model.py:144-186)."""
+    B, L = x.shape
+    E = p["embed.weight"]
+    dt = E.dtype
+    D = E.shape[1]
+    H = n_heads
+    hd = D // H
+    x_q = E[x]                                                          # :149
+    C_seq = torch.from_numpy(scan.query_scan(x, rhos, vocab_size, c_base, unique_slots)).to(dt)  # :157
+    if unique_slots is not None and pad_mask is not None:               # :163-174
+        unique = unique_slots.masked_fill(~pad_mask, -1)
+        K_max = max(int(pad_mask.sum(1).max()), 16)
+        unique = unique[:, :K_max]
+        cb = c_base[:, :K_max].to(dt) if c_base is not None else None
+        if unique.shape[1] < K_max:
+            pad = K_max - unique.shape[1]
+            unique = F.pad(unique, (0, pad), value=-1)
+            cb = F.pad(cb, (0, 0, 0, pad)) if cb is not None else None
+    else:
+        unique = unique_index(x)                                        # :177
+        cb = None
+    for l in range(n_layers):
+        pre = f"layers.{l}."
+        g = lambda name: p[pre + name]
+        a = rmsnorm(x_q, g("attn_norm.weight"))                         # :114
+        Q_t = gating.forward(a, C_seq, g("attn.pe_proj.weight"), g("attn.ln_q.weight"),
+                             g("attn.ln_q.bias"), g("attn.q_proj.weight"), use_silu)   # :75
+        if attention == "sparse":
+            E_active = E[unique.clamp(min=0)]                           # :64-65
+            mem = F.layer_norm(E_active, (D,), g("attn.ln_kv.weight"), g("attn.ln_kv.bias"))
+            Ek = mem @ g("attn.k_proj.weight").t()                      # :67
+            Ev = mem @ g("attn.v_proj.weight").t()                      # :68
+            Q_mha = Q_t.reshape(B, L, H, hd).transpose(1, 2)            # :81
+            O = att.sparse(Q_mha, x, Ek, Ev, g("attn.pe_proj.weight").t(), rhos.to(dt), vocab_size,
+                           unique, cb, use_silu=use_silu, absent_mass=True, gate_round=gate_round)
+            out = O.transpose(1, 2).reshape(B, L, D)                    # :87
+        elif attention == "dense":
+            mem = F.layer_norm(E, (D,), g("attn.ln_kv.weight"), g("attn.ln_kv.bias"))   # :92
+            Eks = mem @ g("attn.k_proj.weight").t()                     # :93
+            Evs = mem @ g("attn.v_proj.weight").t()                     # :94
+            out = att.dense(Q_t, x, Eks, Evs, rhos.to(dt), g("attn.pe_proj.weight"), H, use_silu)
+        else:
+            raise ValueError(attention)
+        out = out @ g("attn.o_proj.weight").t()                         # :101
+        h = x_q + out                                                   # :114
+        h = h + swiglu(rmsnorm(h, g("ffn_norm.weight")), g("ffn.w1.weight"), g("ffn.w2.weight"),
+                       g("ffn.w3.weight"))                              # :115
+        x_q = h
+    x_q = rmsnorm(x_q, p["final_norm.weight"])                          # :185
+    return x_q @ E.t()                                                  # :186, tied lm_head
