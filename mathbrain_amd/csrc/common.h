@@ -95,26 +95,118 @@ __device__ inline int block_exclusive_scan(int v, int* scratch, int& total) {
     return res;
 }
 
-// In-place ascending bitonic sort of n (power of two) keys in LDS by the whole block.
+// In-place ascending bitonic sort of n (power of two) keys in LDS by the whole block
+// (blockDim.x a multiple of 64).  Thread t of wave w handles the compare-exchange pairs
+// p = w * 64 * ppt + r * 64 + lane (r < ppt, ppt = pairs per thread), so a stage whose
+// pairs span at most 2 * 64 * ppt elements stays inside one wave's chunk and needs no
+// block barrier: only the stages with a stride above that, and the first stage after
+// them, synchronise the block.  LDS operations of one wave execute in order.
 template <typename T>
 __device__ inline void block_bitonic_sort(T* s, int n) {
     const int half = n >> 1;
+    const int nthr = blockDim.x;
+    const int ppt = half > nthr ? half / nthr : 1;
+    const int wave_pairs = 64 * ppt;
+    const int base = (threadIdx.x >> 6) * wave_pairs + (threadIdx.x & 63);
+    bool prev_cross = true;
     for (int k = 2; k <= n; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < half; i += blockDim.x) {
-                const int lo = 2 * j * (i / j) + (i % j);
-                const int hi = lo + j;
-                const bool up = (lo & k) == 0;
-                const T a = s[lo];
-                const T b = s[hi];
-                if ((a > b) == up) {
-                    s[lo] = b;
-                    s[hi] = a;
+            const bool cross = j > wave_pairs;
+            if (cross || prev_cross) {
+                __syncthreads();
+            } else {
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+            prev_cross = cross;
+            const int lj = __builtin_ctz(j);
+            for (int r = 0; r < ppt; ++r) {
+                const int p = base + r * 64;
+                if (p < half) {
+                    const int lo = ((p >> lj) << (lj + 1)) | (p & (j - 1));
+                    const int hi = lo + j;
+                    const bool up = (lo & k) == 0;
+                    const T a = s[lo];
+                    const T b = s[hi];
+                    if ((a > b) == up) {
+                        s[lo] = b;
+                        s[hi] = a;
+                    }
                 }
             }
-            __syncthreads();
         }
     }
+    __syncthreads();
+}
+
+// Stable LSD radix sort, by 8-bit digits of bits [sh0, sh0 + nbits), of the L keys in
+// a[0:L) (the block's LDS), using b[0:L) and cnt[4 * blockDim.x] ints of LDS as scratch.
+// blockDim.x is a multiple of 64 and L <= 64 * MAXR * (blockDim.x / 64).  Wave w owns a
+// contiguous run of the input; a lane's rank among the equal digits of its 64-key round
+// comes from eight ballots, the wave's running count per digit lives in cnt[digit][w],
+// and one block scan over cnt (digit-major) turns the counts into stable offsets.
+// Returns the buffer that holds the sorted keys (a or b).
+template <int MAXR, typename T>
+__device__ T* block_radix_sort(T* a, T* b, int* cnt, int L, int sh0, int nbits) {
+    const int nw = blockDim.x >> 6;
+    const int w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int C = ((L + nw - 1) / nw + 63) & ~63;  // keys per wave
+    const int rounds = C >> 6;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int sh = sh0; sh < sh0 + nbits; sh += 8) {
+        for (int d = lane; d < 256; d += 64) cnt[d * nw + w] = 0;
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        T kk[MAXR];
+        int rk[MAXR], dg[MAXR];
+#pragma unroll
+        for (int r = 0; r < MAXR; ++r) {
+            if (r >= rounds) break;
+            const int e = w * C + r * 64 + lane;
+            const bool valid = e < L;
+            const T key = valid ? a[e] : T(0);
+            const int dig = (int)((key >> sh) & T(255));
+            uint64_t m = __ballot(valid);
+#pragma unroll
+            for (int bit = 0; bit < 8; ++bit) {
+                const bool on = (dig >> bit) & 1;
+                const uint64_t bl = __ballot(valid && on);
+                m &= on ? bl : ~bl;
+            }
+            const int base = valid ? cnt[dig * nw + w] : 0;
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            if (valid && (m & below) == 0) cnt[dig * nw + w] = base + __popcll(m);
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            kk[r] = key;
+            rk[r] = base + __popcll(m & below);
+            dg[r] = dig;
+        }
+        __syncthreads();
+        // exclusive scan of cnt in (digit, wave) order: 4 entries per thread
+        int* c4 = cnt + 4 * threadIdx.x;
+        const int v0 = c4[0], v1 = c4[1], v2 = c4[2], v3 = c4[3];
+        int total;
+        const int off = block_exclusive_scan(v0 + v1 + v2 + v3, cnt + 4 * blockDim.x, total);
+        c4[0] = off;
+        c4[1] = off + v0;
+        c4[2] = off + v0 + v1;
+        c4[3] = off + v0 + v1 + v2;
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < MAXR; ++r) {
+            if (r >= rounds) break;
+            const int e = w * C + r * 64 + lane;
+            if (e < L) b[cnt[dg[r] * nw + w] + rk[r]] = kk[r];
+        }
+        __syncthreads();
+        T* t = a;
+        a = b;
+        b = t;
+    }
+    return a;
 }
 
 }  // namespace mb
