@@ -3,8 +3,8 @@
  *
  * Every entry point takes device pointers, plain sizes and strides, and a HIP stream
  * (hipStream_t passed as void*; NULL = the null stream).  Nothing here allocates:
- * callers pass every output buffer and, where a call needs one, a workspace whose size
- * the matching *_workspace_size() call returns.  Calls are asynchronous on the stream.
+ * callers pass every output buffer, and no call needs a workspace.  Calls are
+ * asynchronous on the stream.
  *
  * Return value: MB_OK (0) on success; a negative MB_ERR_* code for an argument the call
  * rejects before launching anything; a positive hipError_t code when the HIP runtime
@@ -142,10 +142,10 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
  *   dE_k/dE_v [B, K, H*hd] fp32 contiguous outputs (zero for padding slots)
  *   dW_pe     [N, H*hd] fp32 contiguous output
  *
- * The outputs are cleared by the call (with a fill kernel, no memset) and then
- * accumulated with fp32 atomics, so the summation order of dE_k, dE_v and dW_pe is not
- * fixed, as in the reference's tl.atomic_add.  Supported: as mb_flash_ema_fwd with H a
- * multiple of 4.
+ * dQ is written once per element.  dE_k, dE_v and dW_pe are cleared by the call (with a
+ * fill kernel, no memset) and then accumulated with fp32 atomics, so their summation
+ * order is not fixed, as in the reference's tl.atomic_add.  Supported: as
+ * mb_flash_ema_fwd with H a multiple of 4.
  */
 int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,
                      const float *dO, const int64_t *x, int64_t x_sb, int64_t x_sl,

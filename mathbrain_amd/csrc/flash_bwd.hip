@@ -91,19 +91,23 @@ flash_ema_bwd_kernel(FlashArgs a) {
 
     // Gate weights as the B operand: W[n = 32 ns + 8 g + e][d = 16 dt + c16] * log2 e,
     // one fragment per (head, dt, ns, lane) in LDS.
+    // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
     for (int f = threadIdx.x; f < kBwdHeads * DT * NS * 64; f += blockDim.x) {
         const int ln = f & 63;
         const int ns = (f >> 6) % NS;
         const int dt = ((f >> 6) / NS) % DT;
         const int hh = (f >> 6) / (NS * DT);
+        float w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int n = min(32 * ns + 8 * (ln >> 4) + e, a.N - 1);
+            w[e] = a.W[(int64_t)n * D + (hg * kBwdHeads + hh) * HD + 16 * dt + (ln & 15)];
+        }
         bf16x8 v;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int n = 32 * ns + 8 * (ln >> 4) + e;
-            const float w = n < a.N
-                ? a.W[(int64_t)n * D + (hg * kBwdHeads + hh) * HD + 16 * dt + (ln & 15)] * kLog2e
-                : 0.f;
-            v[e] = (__bf16)w;
+            v[e] = (__bf16)(n < a.N ? w[e] * kLog2e : 0.f);
         }
         wfr[f] = v;
     }
@@ -441,9 +445,8 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
                "mb_flash_ema_bwd: null pointer");
     MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds && dE_k && dE_v), "mb_flash_ema_bwd: null slot pointer");
     hipStream_t st = (hipStream_t)stream;
-    // dE_k, dE_v and dW_pe are accumulated with atomics.
+    // dE_k, dE_v and dW_pe are accumulated with atomics; every dQ element is written once.
     const int64_t D = (int64_t)H * hd;
-    if ((rc = zero_fill(dQ, (int64_t)B * H * L * hd, st))) return rc;
     if ((rc = zero_fill(dW_pe, (int64_t)N * D, st))) return rc;
     if (K > 0) {
         if ((rc = zero_fill(dE_k, (int64_t)B * K * D, st))) return rc;

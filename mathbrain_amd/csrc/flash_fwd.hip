@@ -63,17 +63,29 @@ flash_ema_fwd_kernel(FlashArgs a) {
     const int h = wave;
 
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
+    // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
     bf16x8 wf[DT][NS];
+    {
+        float wraw[DT][NS][8];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int ns = 0; ns < NS; ++ns)
+            for (int ns = 0; ns < NS; ++ns)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int n = 32 * ns + 8 * g + e;
-                const float w = n < a.N ? a.W[(int64_t)n * D + h * HD + 16 * dt + c16] * kLog2e : 0.f;
-                wf[dt][ns][e] = (__bf16)w;
-            }
+                for (int e = 0; e < 8; ++e) {
+                    const int n = min(32 * ns + 8 * g + e, a.N - 1);
+                    wraw[dt][ns][e] = a.W[(int64_t)n * D + h * HD + 16 * dt + c16];
+                }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ns = 0; ns < NS; ++ns)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int n = 32 * ns + 8 * g + e;
+                    wf[dt][ns][e] = (__bf16)(n < a.N ? wraw[dt][ns][e] * kLog2e : 0.f);
+                }
+    }
 
     // Queries of this lane's steps, pre-scaled by 1/sqrt(hd).
     const float qscale = 1.0f / sqrtf((float)HD);
