@@ -95,50 +95,6 @@ __device__ inline int block_exclusive_scan(int v, int* scratch, int& total) {
     return res;
 }
 
-// In-place ascending bitonic sort of n (power of two) keys in LDS by the whole block
-// (blockDim.x a multiple of 64).  Thread t of wave w handles the compare-exchange pairs
-// p = w * 64 * ppt + r * 64 + lane (r < ppt, ppt = pairs per thread), so a stage whose
-// pairs span at most 2 * 64 * ppt elements stays inside one wave's chunk and needs no
-// block barrier: only the stages with a stride above that, and the first stage after
-// them, synchronise the block.  LDS operations of one wave execute in order.
-template <typename T>
-__device__ inline void block_bitonic_sort(T* s, int n) {
-    const int half = n >> 1;
-    const int nthr = blockDim.x;
-    const int ppt = half > nthr ? half / nthr : 1;
-    const int wave_pairs = 64 * ppt;
-    const int base = (threadIdx.x >> 6) * wave_pairs + (threadIdx.x & 63);
-    bool prev_cross = true;
-    for (int k = 2; k <= n; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const bool cross = j > wave_pairs;
-            if (cross || prev_cross) {
-                __syncthreads();
-            } else {
-                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-            }
-            prev_cross = cross;
-            const int lj = __builtin_ctz(j);
-            for (int r = 0; r < ppt; ++r) {
-                const int p = base + r * 64;
-                if (p < half) {
-                    const int lo = ((p >> lj) << (lj + 1)) | (p & (j - 1));
-                    const int hi = lo + j;
-                    const bool up = (lo & k) == 0;
-                    const T a = s[lo];
-                    const T b = s[hi];
-                    if ((a > b) == up) {
-                        s[lo] = b;
-                        s[hi] = a;
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
-}
-
 // Stable LSD radix sort, by 8-bit digits of bits [sh0, sh0 + nbits), of the L keys in
 // a[0:L) (the block's LDS), using b[0:L) and cnt[4 * blockDim.x] ints of LDS as scratch.
 // blockDim.x is a multiple of 64 and L <= 64 * MAXR * (blockDim.x / 64).  Wave w owns a

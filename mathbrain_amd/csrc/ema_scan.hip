@@ -1,14 +1,13 @@
 // EMA counter scans on gfx950: the query-side scan (C_seq) and the key-side chunk-start
 // states (C_bounds).
 //
-// Both rest on one per-sequence index built in LDS: the positions of the sequence sorted
-// by (token, position), so that every token's occurrences form a contiguous "chain".
-// The recurrence C <- C*rho^dt (+1 per occurrence) only ever couples positions of the
-// same chain, so chains are independent and all chains of all sequences run in parallel:
-// a group of lanes owns one chain and one slice of the N decay rates, keeps the counter
-// in registers and walks the chain, writing each output row with one vector store.
-// Nothing of size V (vocabulary) is ever touched, unlike the reference, which zero-fills a
-// [B, V+1, N] state every call (mathbrain/triton_ema_query.py:141-142).
+// The query scan sorts each sequence's positions by (token, position) in LDS, so that
+// every token's occurrences form a contiguous "chain": the recurrence
+// C <- C*rho^dt (+1 per occurrence) only couples positions of one chain, so lane groups
+// walk chains in parallel, writing each output row with one vector store.  The key-side
+// states need no sort: a wave follows one slot and finds its occurrences in each window
+// with a ballot.  Nothing of size V (vocabulary) is ever touched, unlike the reference,
+// which zero-fills a [B, V+1, N] state every call (mathbrain/triton_ema_query.py:141-142).
 #include "common.h"
 
 #include <algorithm>
@@ -17,39 +16,7 @@ namespace mb {
 
 constexpr int kScanThreads = 1024;
 constexpr int kMaxScanL = 8192;
-constexpr int kBoundSlotsPerBlock = 64;
 constexpr size_t kMaxLds = 160 * 1024;
-
-// ---- per-sequence sorted index ---------------------------------------------------------------
-
-// Loads x[b, 0:L) into `keys` as (token << pb | position), pads to n (power of two) with the
-// all-ones key, and sorts ascending.
-template <typename KeyT>
-__device__ void build_sorted_positions(const int64_t* __restrict__ x, int64_t sb, int64_t sl,
-                                       int b, int L, int n, int pb, KeyT* keys) {
-    const KeyT tokmask = (pb == 0) ? ~KeyT(0) : ((~KeyT(0)) >> pb);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        KeyT k = ~KeyT(0);
-        if (i < L) {
-            const uint64_t tok = (uint64_t)x[(int64_t)b * sb + (int64_t)i * sl];
-            k = ((KeyT)tok & tokmask) << pb | (KeyT)i;
-        }
-        keys[i] = k;
-    }
-    __syncthreads();
-    block_bitonic_sort(keys, n);
-}
-
-// First index in sorted keys[0:L) whose token is >= tok (tok given unshifted).
-template <typename KeyT>
-__device__ inline int lower_bound_token(const KeyT* keys, int L, int pb, uint64_t tok) {
-    int lo = 0, hi = L;
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if ((uint64_t)(keys[mid] >> pb) < tok) lo = mid + 1; else hi = mid;
-    }
-    return lo;
-}
 
 // ---- query scan ---------------------------------------------------------------------------
 //
@@ -441,82 +408,111 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
 }
 
 // ---- key-side chunk-start states -----------------------------------------------------------
+//
+// One workgroup per (sequence b, block of kBoundSlots slots); wave w takes slots w,
+// w + nwaves, ... and its lanes the decay rates (lane, lane + 64, ...).  The sequence's
+// tokens sit in LDS.  Between two chunk starts the window [(j-1) Br, j Br) is walked in
+// pieces of at most 64 steps: one ballot of (token == slot id) gives the piece's
+// occurrence mask and the state advances as
+//   C <- C rho^len + sum_{p in mask} rho^(len - 1 - p)
+// (an occurrence adds 1 after its step's decay: triton_flash_ema.py:56-78).  A document
+// change at r zeroes the state before step r (:69-75): the piece drops the carried state
+// and the occurrences before its last change.  No sort is needed.
 
-template <typename KeyT>
-__global__ void __launch_bounds__(kScanThreads)
+constexpr int kBoundThreads = 512;
+constexpr int kBoundSlots = 32;
+
+// 64 bits of the bitmask `bits` starting at bit `pos` (bits beyond the array read as 0:
+// the array carries one spare word).
+__device__ inline uint64_t bits64_at(const uint64_t* bits, int pos) {
+    const int w = pos >> 6;
+    const int off = pos & 63;
+    uint64_t v = bits[w] >> off;
+    if (off) v |= bits[w + 1] << (64 - off);
+    return v;
+}
+
+template <int RPL>
+__global__ void __launch_bounds__(kBoundThreads)
 ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L,
                     const int64_t* __restrict__ unique, int K, const float* __restrict__ rhos,
                     int N, int Br, int nc, const float* __restrict__ c_init, int64_t cis,
-                    const int64_t* __restrict__ doc_ids, float* __restrict__ out, int Np,
-                    int pb) {
+                    const int64_t* __restrict__ doc_ids, float* __restrict__ out, int Np) {
     extern __shared__ __align__(16) unsigned char smem[];
+    const int nwords = (L >> 6) + 2;
+    int64_t* tok = reinterpret_cast<int64_t*>(smem);                 // [L]
+    uint64_t* rbits = reinterpret_cast<uint64_t*>(tok + L);          // [nwords] document changes
     const int b = blockIdx.x;
-    const int k0 = blockIdx.y * kBoundSlotsPerBlock;
-    const int n = next_pow2(L);
-    KeyT* keys = reinterpret_cast<KeyT*>(smem);
-    int* resets = reinterpret_cast<int*>(keys + n);  // [L] positions where the document changes
-    int* scratch = resets + L;                       // [64]
+    const int k0 = blockIdx.y * kBoundSlots;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int nw = blockDim.x >> 6;
 
-    build_sorted_positions<KeyT>(x, sb, sl, b, L, n, pb, keys);
-
-    int n_resets = 0;
-    if (doc_ids) {
-        const int per = (L + blockDim.x - 1) / blockDim.x;
-        const int i0 = threadIdx.x * per;
-        const int i1 = min(i0 + per, L);
-        const int64_t* d = doc_ids + (int64_t)b * L;
-        int cnt = 0;
-        for (int i = max(i0, 1); i < i1; ++i) cnt += d[i] != d[i - 1];
-        int c = block_exclusive_scan(cnt, scratch, n_resets);
-        for (int i = max(i0, 1); i < i1; ++i)
-            if (d[i] != d[i - 1]) resets[c++] = i;
-        __syncthreads();
+    for (int i = threadIdx.x; i < L; i += blockDim.x) tok[i] = x[(int64_t)b * sb + (int64_t)i * sl];
+    // bit p: the document changes at step p (doc[p] != doc[p - 1], p >= 1)
+    for (int w = wave; w < nwords; w += nw) {
+        const int p = 64 * w + lane;
+        bool chg = false;
+        if (doc_ids && p >= 1 && p < L)
+            chg = doc_ids[(int64_t)b * L + p] != doc_ids[(int64_t)b * L + p - 1];
+        const uint64_t m = __ballot(chg);
+        if (lane == 0) rbits[w] = m;
     }
+    float hi[RPL], lo[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+        hi[r] = 0.f;
+        lo[r] = 0.f;
+        const int n = lane + 64 * r;
+        if (n < N) log2_split(rhos[n], hi[r], lo[r]);
+    }
+    __syncthreads();
 
-    const KeyT posmask = (pb == 0) ? KeyT(0) : ((KeyT(1) << pb) - 1);
-    const int kcount = min(kBoundSlotsPerBlock, K - k0);
-    for (int idx = threadIdx.x; idx < kcount * Np; idx += blockDim.x) {
-        const int k = k0 + idx / Np;
-        const int col = idx % Np;
-        float* o = out + ((int64_t)b * nc * K + k) * Np + col;
-        const int64_t cstride = (int64_t)K * Np;
-        if (col >= N) {
-            for (int j = 0; j < nc; ++j) o[j * cstride] = 0.0f;
-            continue;
-        }
-        float hi, lo;
-        log2_split(rhos[col], hi, lo);
-        float c = c_init ? c_init[((int64_t)b * K + k) * cis + col] : 0.0f;
+    const int64_t cstride = (int64_t)K * Np;
+    for (int kk = wave; kk < kBoundSlots; kk += nw) {
+        const int k = k0 + kk;
+        if (k >= K) break;
         const int64_t u = unique[(int64_t)b * K + k];
-        int mi = 0, me = 0;  // this slot's chain in the sorted positions
-        if (u >= 0) {
-            mi = lower_bound_token(keys, L, pb, (uint64_t)u);
-            me = lower_bound_token(keys, L, pb, (uint64_t)u + 1);
+        float c[RPL];
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) {
+            const int n = lane + 64 * r;
+            c[r] = (c_init && n < N) ? c_init[((int64_t)b * K + k) * cis + n] : 0.f;
         }
-        int ri = 0;
-        int t_cur = 0;  // c is the state before step t_cur
-        for (int j = 0; j < nc; ++j) {
-            const int tb = j * Br;
-            // Events before the chunk start, in time order: a document reset at r zeroes the
-            // state before step r; an occurrence at s adds 1 after step s's decay.
-            while (true) {
-                const int s = (mi < me) ? (int)(keys[mi] & posmask) : INT32_MAX;
-                const int r = (ri < n_resets) ? resets[ri] : INT32_MAX;
-                if (r <= s && r < tb) {
-                    c = 0.0f;
-                    t_cur = r;
-                    ++ri;
-                } else if (s < tb) {
-                    c = c * pow_steps(hi, lo, s + 1 - t_cur) + 1.0f;
-                    t_cur = s + 1;
-                    ++mi;
-                } else {
-                    break;
+        float* o = out + ((int64_t)b * nc * K + k) * Np;
+        auto store = [&](float* dst) {
+#pragma unroll
+            for (int r = 0; r < RPL; ++r) {
+                const int n = lane + 64 * r;
+                if (n < Np) dst[n] = n < N ? c[r] : 0.f;
+            }
+        };
+        store(o);
+        for (int j = 1; j < nc; ++j) {
+            for (int ps = (j - 1) * Br; ps < j * Br; ps += 64) {
+                const int len = min(64, j * Br - ps);
+                const bool hit = lane < len && u >= 0 && tok[ps + lane] == u;
+                uint64_t m = __ballot(hit);
+                bool drop = false;
+                if (doc_ids) {
+                    uint64_t rb = bits64_at(rbits, ps);
+                    if (len < 64) rb &= (1ull << len) - 1;
+                    if (rb) {
+                        const int rl = 63 - __builtin_clzll(rb);  // last change in the piece
+                        drop = true;
+                        m &= ~((1ull << rl) - 1);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < RPL; ++r) c[r] = drop ? 0.f : c[r] * pow_steps(hi[r], lo[r], len);
+                while (m) {  // uniform across the wave
+                    const int p = __builtin_ctzll(m);
+                    m &= m - 1;
+#pragma unroll
+                    for (int r = 0; r < RPL; ++r) c[r] += pow_steps(hi[r], lo[r], len - 1 - p);
                 }
             }
-            c = c * pow_steps(hi, lo, tb - t_cur);
-            t_cur = tb;
-            o[j * cstride] = c;
+            store(o + j * cstride);
         }
     }
 }
@@ -620,20 +616,26 @@ extern "C" int mb_ema_boundary_states(const int64_t* x, int64_t x_stride_b, int6
     if (L > kMaxScanL)
         return fail(MB_ERR_UNSUPPORTED, "mb_ema_boundary_states: L=%d exceeds the on-chip limit %d",
                     L, kMaxScanL);
-    const int nc = L > 0 ? (L + Br - 1) / Br : 1;
-    const int Lk = L > 0 ? L : 1;  // an empty sequence still stores c0 once
-    const int pb = ceil_log2(Lk);
-    const int n = next_pow2(Lk);
-    const size_t key_bytes = 8;  // slot ids are int64 and unbounded by any vocab size here
-    const size_t lds = n * key_bytes + (size_t)Lk * 4 + 64 * 4;
+    const int nc = L > 0 ? (L + Br - 1) / Br : 1;  // an empty sequence still stores c0 once
+    const size_t lds = (size_t)L * 8 + (size_t)((L >> 6) + 2) * 8;
     if (lds > kMaxLds)
         return fail(MB_ERR_UNSUPPORTED, "mb_ema_boundary_states: L=%d needs %zu B of LDS", L, lds);
-    dim3 grid(B, (K + kBoundSlotsPerBlock - 1) / kBoundSlotsPerBlock);
-    auto kfn = ema_boundary_kernel<uint64_t>;
-    int rc = set_lds(kfn, lds);
-    if (rc) return rc;
-    hipLaunchKernelGGL(kfn, grid, dim3(kScanThreads), lds, (hipStream_t)stream, x, x_stride_b,
-                       x_stride_l, L, unique, K, rhos, N, Br, nc, c_init, c_init_stride_k, doc_ids,
-                       C_bounds, Np, pb);
+    if (Np > 256)
+        return fail(MB_ERR_UNSUPPORTED, "mb_ema_boundary_states: Np=%d > 256", Np);
+    dim3 grid(B, (K + kBoundSlots - 1) / kBoundSlots);
+    hipStream_t st = (hipStream_t)stream;
+#define MB_LAUNCH_BOUND(RPL)                                                                   \
+    do {                                                                                       \
+        auto kfn = ema_boundary_kernel<RPL>;                                                   \
+        int rc = set_lds(kfn, lds);                                                            \
+        if (rc) return rc;                                                                     \
+        hipLaunchKernelGGL(kfn, grid, dim3(kBoundThreads), lds, st, x, x_stride_b, x_stride_l, \
+                           L, unique, K, rhos, N, Br, nc, c_init, c_init_stride_k, doc_ids,    \
+                           C_bounds, Np);                                                      \
+    } while (0)
+    if (Np <= 64) MB_LAUNCH_BOUND(1);
+    else if (Np <= 128) MB_LAUNCH_BOUND(2);
+    else MB_LAUNCH_BOUND(4);
+#undef MB_LAUNCH_BOUND
     return check_launch("mb_ema_boundary_states");
 }
