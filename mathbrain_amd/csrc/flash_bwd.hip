@@ -17,9 +17,10 @@
 // tile, 4 tiles) and steps 4*(lane/16) + i: the sums over t (dE_k, dE_v, and dW through
 // a second MFMA fed straight from the gate tile's registers) stay in registers, dQ
 // accumulates in registers across the slot loop, and only the scores s and dp need a
-// sum over the 16 lanes of a DPP row.  dE_k/dE_v of a batch are combined over the two
-// half-waves in LDS and added to global memory with one atomic per element; dW is added
-// once per wave at the end.
+// sum over the 16 lanes of a DPP row.  Each half-wave stores its dE_k/dE_v partials of a
+// batch in its own LDS region (plain stores: LDS float atomics between the two halves
+// cost a fifth of the kernel's time); the flush adds the two halves and makes one
+// global atomic per element.  dW is added once per wave at the end.
 #include "flash_common.h"
 
 #include <algorithm>
@@ -51,8 +52,6 @@ flash_ema_bwd_kernel(FlashArgs a) {
     constexpr int NT = NPAD / 16;
     constexpr int WID = kBwdHeads * HD;  // embedding columns of this head group
     using S = Stage<NPAD, SB>;
-    constexpr int CTROW = kTB + 4;               // bf16 per cdecT row (8 B pad)
-    constexpr int CT = SB * NPAD * CTROW;        // bf16 elements of cdecT per buffer
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int D = a.H * HD;
@@ -64,20 +63,20 @@ flash_ema_bwd_kernel(FlashArgs a) {
     const int cbi = t0 / a.Br;
     const int cb = cbi * a.Br;
 
-    // LDS: 2 staging buffers (cdec | cdecT | E | scores [SB][heads][kTB]) | 2 dE
-    // accumulators [SB][2][WID] | W fragments | meta ring | window | power table | slot info
+    // LDS: 2 staging buffers (cdec | E | scores [SB][heads][kTB]) | 2 x 2 dE partials
+    // [buffer][half-wave][SB][2][WID] | W fragments | meta ring | window | power table |
+    // slot info
     constexpr int SCN = HAS_S ? SB * kBwdHeads * kTB : 0;  // staged scores per buffer
-    const int stage_bytes = (int)S::bytes(WID) + CT * 2 + SCN * 4;
+    const int stage_bytes = (int)S::bytes(WID) + SCN * 4;
     const int acc_floats = SB * 2 * WID;
     float* dEacc = reinterpret_cast<float*>(smem + 2 * stage_bytes);
-    bf16x8* wfr = reinterpret_cast<bf16x8*>(dEacc + 2 * acc_floats);
+    bf16x8* wfr = reinterpret_cast<bf16x8*>(dEacc + 4 * acc_floats);
     BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + kBwdHeads * DT * NS * 64);
     int64_t* win = reinterpret_cast<int64_t*>(metas + kMetaRing * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
 #define cdec_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes)
-#define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CDEC * 2)
-#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2 + CT * 2)
+#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
 #define S2_of(i) (E_of(i) + SB * 2 * WID)
 #define meta_of(batch) (metas + ((batch) % kMetaRing) * SB)
 
@@ -111,7 +110,6 @@ flash_ema_bwd_kernel(FlashArgs a) {
         }
         wfr[f] = v;
     }
-    for (int i = threadIdx.x; i < 2 * acc_floats; i += blockDim.x) dEacc[i] = 0.f;
     flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
     const int kend = kinfo[1];
     const int nb = (kend + SB - 1) / SB;
@@ -149,6 +147,20 @@ flash_ema_bwd_kernel(FlashArgs a) {
 
     Producer<NPAD, SB, MAXI, MAXE> prod;
     const int col0 = hg * WID;
+    // Adds a batch's dE partials (both half-waves) to global memory, one atomic per
+    // element; padding slots' entries (never written) are skipped.
+    auto flush_dE = [&](int batch, const float* acc2) {
+        const BatchMeta* mb = meta_of(batch);
+        for (int i = threadIdx.x; i < acc_floats; i += blockDim.x) {
+            const int j = i / (2 * WID);
+            if (mb[j].u < 0) continue;
+            const int which = (i / WID) & 1;
+            const int c = i % WID;
+            const int k = batch * SB + j;
+            float* dst = (which ? a.dEv : a.dEk) + ((int64_t)b * a.K + k) * D + col0 + c;
+            atomicAdd(dst, (acc2[i] + acc2[acc_floats + i]) * kLn2);
+        }
+    };
     // Forward scores of a batch, one float4 (4 steps) per thread < SCN / 4.
     float4 s2pre = make_float4(0.f, 0.f, 0.f, 0.f);
     auto load_scores = [&](int batch) {
@@ -181,8 +193,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
         load_scores(0);
         __syncthreads();
         store_scores(S2_of(0));
-        prod.template store<true, S::CROW, CTROW>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0),
-                                                  E_of(0), WID);
+        prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), WID);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -194,25 +205,11 @@ flash_ema_bwd_kernel(FlashArgs a) {
             load_scores(bi + 1);
         }
         // Flush the previous batch's dE sums (complete after the last barrier).
-        if (bi > 0) {
-            float* acc = dEacc + (cur ^ 1) * acc_floats;
-            for (int i = threadIdx.x; i < acc_floats; i += blockDim.x) {
-                const int j = i / (2 * WID);
-                const int which = (i / WID) & 1;
-                const int c = i % WID;
-                const int k = (bi - 1) * SB + j;
-                if (meta_of(bi - 1)[j].u >= 0) {
-                    float* dst = (which ? a.dEv : a.dEk) + ((int64_t)b * a.K + k) * D + col0 + c;
-                    atomicAdd(dst, acc[i] * kLn2);
-                }
-                acc[i] = 0.f;
-            }
-        }
+        if (bi > 0) flush_dE(bi - 1, dEacc + (cur ^ 1) * 2 * acc_floats);
         const __bf16* cdec = cdec_of(cur);
-        const __bf16* cdecT = cdecT_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
-        float* acc = dEacc + cur * acc_floats;
+        float* acc = dEacc + (cur * 2 + th) * acc_floats;  // this half-wave's partials
         for (int j = 0; j < SB; ++j) {
             if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
             // Forward scores of this lane's 4 steps, staged in LDS with the batch.
@@ -296,48 +293,38 @@ flash_ema_bwd_kernel(FlashArgs a) {
             if (DT == 4) {
                 const float vk = rows4_reduce_scatter(dEk[0], dEk[1 % DT], dEk[2 % DT], dEk[3 % DT]);
                 const float vv = rows4_reduce_scatter(dEv[0], dEv[1 % DT], dEv[2 % DT], dEv[3 % DT]);
-                atomicAdd(&acc[(j * 2 + 0) * WID + hl * HD + 16 * g + c16], vk);
-                atomicAdd(&acc[(j * 2 + 1) * WID + hl * HD + 16 * g + c16], vv);
+                acc[(j * 2 + 0) * WID + hl * HD + 16 * g + c16] = vk;
+                acc[(j * 2 + 1) * WID + hl * HD + 16 * g + c16] = vv;
             } else {
                 const float vk = rows4_reduce_scatter2(dEk[0], dEk[1 % DT]);
                 const float vv = rows4_reduce_scatter2(dEv[0], dEv[1 % DT]);
                 if ((g & 1) == 0) {
-                    atomicAdd(&acc[(j * 2 + 0) * WID + hl * HD + 8 * g + c16], vk);
-                    atomicAdd(&acc[(j * 2 + 1) * WID + hl * HD + 8 * g + c16], vv);
+                    acc[(j * 2 + 0) * WID + hl * HD + 8 * g + c16] = vk;
+                    acc[(j * 2 + 1) * WID + hl * HD + 8 * g + c16] = vv;
                 }
             }
             // dW^T[d, n] += dpre^T[d, t] c_dec[t, n]: A = dpre (rows d, k = this lane's
-            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16] read from cdecT.
-            const __bf16* ctrow = cdecT + (j * NPAD) * CTROW + 16 * th + 4 * g;
+            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16]: four 16-bit reads of
+            // one column of the c_dec tile.
+            const __bf16* ccol = cdec + (j * kTB + 16 * th + 4 * g) * S::CROW + c16;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                const bf16x4 cb4 = *reinterpret_cast<const bf16x4*>(ctrow + (16 * nt + c16) * CTROW);
+                bf16x4 cb4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) cb4[e] = ccol[e * S::CROW + 16 * nt];
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<true, S::CROW, CTROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1),
-                                                      cdecT_of(cur ^ 1), E_of(cur ^ 1), WID);
+            prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+                                                   E_of(cur ^ 1), WID);
             store_scores(S2_of(cur ^ 1));
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();
     }
-    if (nb > 0) {
-        const int last = nb - 1;
-        float* acc = dEacc + (last & 1) * acc_floats;
-        for (int i = threadIdx.x; i < acc_floats; i += blockDim.x) {
-            const int j = i / (2 * WID);
-            const int which = (i / WID) & 1;
-            const int c = i % WID;
-            const int k = last * SB + j;
-            if (meta_of(last)[j].u >= 0) {
-                float* dst = (which ? a.dEv : a.dEk) + ((int64_t)b * a.K + k) * D + col0 + c;
-                atomicAdd(dst, acc[i] * kLn2);
-            }
-        }
-    }
+    if (nb > 0) flush_dE(nb - 1, dEacc + ((nb - 1) & 1) * 2 * acc_floats);
 
     // dQ (the gate carried log2 e, the query 1/sqrt(hd)) and dW.
     const float qf = kLn2 * qscale;
@@ -360,7 +347,6 @@ flash_ema_bwd_kernel(FlashArgs a) {
                 atomicAdd(&a.dW[(int64_t)n * D + h * HD + 16 * dt + 4 * g + i], dWacc[dt][nt][i]);
         }
 #undef cdec_of
-#undef cdecT_of
 #undef E_of
 #undef S2_of
 #undef meta_of
@@ -369,9 +355,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
 template <int HD, int NS, int SB>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
-    return 2 * (Stage<32 * NS, SB>::bytes(WID) + (size_t)SB * 32 * NS * (kTB + 4) * 2 +
-                (size_t)SB * kBwdHeads * kTB * 4) +
-           2 * (size_t)SB * 2 * WID * 4 +
+    return 2 * (Stage<32 * NS, SB>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
+           4 * (size_t)SB * 2 * WID * 4 +
            (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16;
 }
