@@ -44,12 +44,15 @@ static int zero_fill(float* p, int64_t n, hipStream_t st) {
     return check_launch("zero fill");
 }
 
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S>
+// NT0, NTW: the 16-rate tiles [NT0, NT0 + NTW) of dW_pe this launch accumulates (a 64 x 64
+// fp32 accumulator per wave is 64 registers, so N > 64 takes two launches); DWO: the
+// second such launch, which recomputes the gate and the gradients but adds only its dW_pe
+// tiles (no dQ, no dE).
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NT0, int NTW, bool DWO>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_bwd_kernel(FlashArgs a) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
-    constexpr int NT = NPAD / 16;
     constexpr int WID = kBwdHeads * HD;  // embedding columns of this head group
     using S = Stage<NPAD, SB>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -139,11 +142,11 @@ flash_ema_bwd_kernel(FlashArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) Dv[i] = row_sum16(dsum[i]);
     }
-    f32x4 dWacc[DT][NT];
+    f32x4 dWacc[DT][NTW];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) dWacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NTW; ++nt) dWacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     Producer<NPAD, SB, MAXI, MAXE> prod;
     const int col0 = hg * WID;
@@ -205,7 +208,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
             load_scores(bi + 1);
         }
         // Flush the previous batch's dE sums (complete after the last barrier).
-        if (bi > 0) flush_dE(bi - 1, dEacc + (cur ^ 1) * 2 * acc_floats);
+        if (!DWO && bi > 0) flush_dE(bi - 1, dEacc + (cur ^ 1) * 2 * acc_floats);
         const __bf16* cdec = cdec_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
@@ -277,7 +280,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
                     const float yd = p[i] * dov[dt][i];
                     dEk[dt] = __builtin_fmaf(xq, gv, dEk[dt]);
                     dEv[dt] = __builtin_fmaf(yd, gv, dEv[dt]);
-                    dq[dt][i] = __builtin_fmaf(ds[i] * gv, ek[dt], dq[dt][i]);
+                    if (!DWO) dq[dt][i] = __builtin_fmaf(ds[i] * gv, ek[dt], dq[dt][i]);
                     const float av = __builtin_fmaf(xq, ek[dt], yd * ev[dt]);
                     float dsil = 1.f;
                     if (SILU) {  // sig + g (1 - sig), with g = gv ln2
@@ -290,7 +293,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
             // dE: this lane's 4 steps summed in registers; the 4 row groups (other steps)
             // are reduce-scattered with v_permlane16/32_swap so that the writing row holds
             // one dim tile; the two half-waves meet in LDS.
-            if (DT == 4) {
+            if (DWO) {
+            } else if (DT == 4) {
                 const float vk = rows4_reduce_scatter(dEk[0], dEk[1 % DT], dEk[2 % DT], dEk[3 % DT]);
                 const float vv = rows4_reduce_scatter(dEv[0], dEv[1 % DT], dEv[2 % DT], dEv[3 % DT]);
                 acc[(j * 2 + 0) * WID + hl * HD + 16 * g + c16] = vk;
@@ -308,10 +312,10 @@ flash_ema_bwd_kernel(FlashArgs a) {
             // one column of the c_dec tile.
             const __bf16* ccol = cdec + (j * kTB + 16 * th + 4 * g) * S::CROW + c16;
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
+            for (int nt = 0; nt < NTW; ++nt) {
                 bf16x4 cb4;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) cb4[e] = ccol[e * S::CROW + 16 * nt];
+                for (int e = 0; e < 4; ++e) cb4[e] = ccol[e * S::CROW + 16 * (NT0 + nt)];
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
             }
@@ -324,14 +328,14 @@ flash_ema_bwd_kernel(FlashArgs a) {
         }
         __syncthreads();
     }
-    if (nb > 0) flush_dE(nb - 1, dEacc + ((nb - 1) & 1) * 2 * acc_floats);
+    if (!DWO && nb > 0) flush_dE(nb - 1, dEacc + ((nb - 1) & 1) * 2 * acc_floats);
 
     // dQ (the gate carried log2 e, the query 1/sqrt(hd)) and dW.
     const float qf = kLn2 * qscale;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int t = t0 + 16 * th + 4 * g + i;
-        if (t >= a.L) continue;
+        if (DWO || t >= a.L) continue;
         float* dst = a.dQ + (((int64_t)b * a.H + h) * a.L + t) * HD;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) dst[16 * dt + c16] = dq[dt][i] * qf;
@@ -339,8 +343,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int n = 16 * nt + c16;
+        for (int nt = 0; nt < NTW; ++nt) {
+            const int n = 16 * (NT0 + nt) + c16;
             if (n >= a.N) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -375,12 +379,17 @@ static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: hd=%d, N=%d needs %zu B of LDS", HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
     dim3 grid(a.B * ntb * a.head_groups);
-#define MB_BWD(MI, ME)                                                                      \
+    // dW_pe tiles per launch: a DT x NTW block of 16x16 fp32 accumulators stays at 64
+    // registers; wider N takes a second, dW-only launch for the remaining tiles.
+    constexpr int NT = NPAD / 16;
+    constexpr int NTW = NT < 256 / HD ? NT : 256 / HD;
+    static_assert(NT == NTW || NT == 2 * NTW, "at most two dW launches");
+#define MB_BWD_ONE(MI, ME, NT0, DWO)                                                        \
     do {                                                                                    \
-        auto k = a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true>   \
-                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true>) \
-                        : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false>  \
-                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false>); \
+        auto k = a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NT0, NTW, DWO>   \
+                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NT0, NTW, DWO>) \
+                        : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NT0, NTW, DWO>  \
+                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NT0, NTW, DWO>); \
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
         if (e != hipSuccess) {                                                              \
@@ -389,11 +398,17 @@ static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
         }                                                                                   \
         hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, a);                                \
     } while (0)
+#define MB_BWD(MI, ME)                                  \
+    do {                                                \
+        MB_BWD_ONE(MI, ME, 0, false);                   \
+        if constexpr (NT > NTW) MB_BWD_ONE(MI, ME, NTW, true); \
+    } while (0)
     if (mi <= 1 && me <= 1) MB_BWD(1, 1);
     else if (mi <= 2 && me <= 1) MB_BWD(2, 1);
     else if (mi <= 2 && me <= 2) MB_BWD(2, 2);
     else return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: N=%d too wide", a.N);
 #undef MB_BWD
+#undef MB_BWD_ONE
     return check_launch("mb_flash_ema_bwd");
 }
 
