@@ -11,7 +11,7 @@ dO N(0, 1) (synthetic, seeded).  One step = key-side chunk states (mb_ema_bounda
 Prints one JSON line.  `roofline` is for the dominant kernel (the backward): algorithmic
 flops per launch, sum_b L*K_b*(4*N*D + 10*D) (gate recompute, dW_pe and the five
 per-element products; only valid (t, k) pairs count), over its mean launch time measured
-with HIP events on the launch stream, against the dense bf16 MFMA peak of 2516.6 TFLOP/s.
+with HIP events on the launch stream, against the dense bf16/fp16 MFMA peak of 2516.6 TFLOP/s.
 `cpu_baseline` times the CPU restatement of the reference algorithm (the oracle, a port
 of the reference's PyTorch path) on a bounded slice of the same workload on this host.
 
@@ -161,7 +161,7 @@ def run_attention(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 gate MFMA, fp32 state/softmax/accumulate",
+        "dtype": "fp16 gate MFMA (bf16 dW_pe MFMA), fp32 state/softmax/accumulate",
         "data": "synthetic Zipf(1.1) tokens, seeded; random N(0,0.02) weights",
         "config": {"workload": "cfg2: one flash-EMA layer fwd+bwd (boundary states + fwd + bwd)",
                    "B": c["B"], "T": L, "d_model": D, "heads": c["H"], "head_dim": c["hd"],
@@ -339,7 +339,7 @@ def run_model(args):
     return {"metric": "SlotTransformerLM training step tokens/s (cfg5)", "value": round(B * T / (ms * 1e-3), 1),
             "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "bf16 autocast (attention fp32 state, bf16 gate MFMA)",
+            "vs_baseline": None, "dtype": "bf16 autocast (attention fp32 state, fp16 gate MFMA)",
             "data": "synthetic lognormal(median 1500) Zipf(1.1) documents, chunked, random init",
             "config": {"workload": "cfg5 full training step", "layers": n_layers, "d_model": D,
                        "heads": H, "N": N, "V": V, "B": B, "T": T, "params": n_params,

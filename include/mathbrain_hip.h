@@ -100,7 +100,7 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
  *
  *   c_dec[t,k,:] = C_bounds[b, t/Br, k, :N] rho^(t - Br*(t/Br) + 1)
  *                  + sum_{Br*(t/Br) <= s < t, x_s = unique[b,k]} rho^(t-s)
- *   g[t,k,:]     = SiLU(c_dec[t,k,:] . W_pe[:, h*hd:(h+1)*hd])   (bf16 operands)
+ *   g[t,k,:]     = SiLU(c_dec[t,k,:] . W_pe[:, h*hd:(h+1)*hd])   (fp16 operands)
  *   s[t,k]       = Q[b,h,t] . (E_k[b,k,h] * g[t,k]) / sqrt(hd)
  *   O[b,h,t]     = sum_k softmax_k(s) E_v[b,k,h] * g[t,k]
  *   LSE[b,h,t]   = log(sum_k exp s[t,k] (+ V_total - K_b with MB_FLASH_ABSENT_MASS))
@@ -120,6 +120,10 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
  *   scores    NULL, or [B, H, K, L] fp32 output: s[t,k] * log2(e) for every valid slot
  *             (rows of padding slots are not written).  Passed to mb_flash_ema_bwd, it
  *             spares the backward the score recomputation.
+ *
+ * The gate operands are fp16: c_dec (chunk-start states above 65440 saturate there;
+ * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to
+ * ~45,000 steps) and W_pe * log2(e), with fp32 accumulation.
  *
  * Supported: hd in {32, 64}, 4 <= H <= 8, N <= 128, Br <= 32 or Br == 64.
  */
@@ -144,7 +148,9 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
  *
  * dQ is written once per element.  dE_k, dE_v and dW_pe are cleared by the call (with a
  * fill kernel, no memset) and then accumulated with fp32 atomics, so their summation
- * order is not fixed, as in the reference's tl.atomic_add.  Supported: as
+ * order is not fixed, as in the reference's tl.atomic_add.  The gate is recomputed as
+ * in the forward; the dW_pe product takes bf16 c_dec and bf16 dpre (as the reference's
+ * triton_flash_ema.py:463-465 does) with fp32 accumulation.  Supported: as
  * mb_flash_ema_fwd with H a multiple of 4.
  */
 int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,

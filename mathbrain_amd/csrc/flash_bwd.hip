@@ -15,12 +15,11 @@
 // w % 4 of the group and 16-step half w / 4.  The gate is computed as
 // pre[t, d] = c_dec[t, :] W[:, d], so each lane owns one dim d (lane % 16 of a 16-dim
 // tile, 4 tiles) and steps 4*(lane/16) + i: the sums over t (dE_k, dE_v, and dW through
-// a second MFMA fed straight from the gate tile's registers) stay in registers, dQ
-// accumulates in registers across the slot loop, and only the scores s and dp need a
-// sum over the 16 lanes of a DPP row.  Each half-wave stores its dE_k/dE_v partials of a
-// batch in its own LDS region (plain stores: LDS float atomics between the two halves
-// cost a fifth of the kernel's time); the flush adds the two halves and makes one
-// global atomic per element.  dW is added once per wave at the end.
+// a second MFMA fed from the c_dec tile) stay in registers, dQ accumulates in registers
+// across the slot loop, and only the scores s and dp need a sum over the 16 lanes of a
+// DPP row.  Each wave adds its 16 steps' dE_k/dE_v of a slot to global memory with one
+// coalesced atomic per lane (cheaper, measured, than summing the two half-waves in LDS
+// first and flushing once).  dW is added once per wave at the end.
 #include "flash_common.h"
 
 #include <algorithm>
@@ -28,8 +27,8 @@
 namespace mb {
 
 constexpr int kBwdHeads = 4;  // heads per workgroup
-// Batch slot info ring: batch i-1's info is still read (dE flush) while a fast wave
-// already writes batch i+2's, so four entries.
+// Batch slot info ring: a fast wave writes batch i+2's info while slow waves still read
+// batch i's, so at least three entries; four makes the ring index a mask.
 constexpr int kMetaRing = 4;
 
 __global__ void zero_fill_kernel(float* p, int64_t n) {
@@ -66,19 +65,16 @@ flash_ema_bwd_kernel(FlashArgs a) {
     const int cbi = t0 / a.Br;
     const int cb = cbi * a.Br;
 
-    // LDS: 2 staging buffers (cdec | E | scores [SB][heads][kTB]) | 2 x 2 dE partials
-    // [buffer][half-wave][SB][2][WID] | W fragments | meta ring | window | power table |
-    // slot info
+    // LDS: 2 staging buffers (cdec | E | scores [SB][heads][kTB]) | W fragments |
+    // meta ring | window | power table | slot info
     constexpr int SCN = HAS_S ? SB * kBwdHeads * kTB : 0;  // staged scores per buffer
     const int stage_bytes = (int)S::bytes(WID) + SCN * 4;
-    const int acc_floats = SB * 2 * WID;
-    float* dEacc = reinterpret_cast<float*>(smem + 2 * stage_bytes);
-    bf16x8* wfr = reinterpret_cast<bf16x8*>(dEacc + 4 * acc_floats);
+    f16x8* wfr = reinterpret_cast<f16x8*>(smem + 2 * stage_bytes);
     BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + kBwdHeads * DT * NS * 64);
     int64_t* win = reinterpret_cast<int64_t*>(metas + kMetaRing * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
-#define cdec_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes)
+#define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
 #define S2_of(i) (E_of(i) + SB * 2 * WID)
 #define meta_of(batch) (metas + ((batch) % kMetaRing) * SB)
@@ -105,11 +101,11 @@ flash_ema_bwd_kernel(FlashArgs a) {
             const int n = min(32 * ns + 8 * (ln >> 4) + e, a.N - 1);
             w[e] = a.W[(int64_t)n * D + (hg * kBwdHeads + hh) * HD + 16 * dt + (ln & 15)];
         }
-        bf16x8 v;
+        f16x8 v;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int n = 32 * ns + 8 * (ln >> 4) + e;
-            v[e] = (__bf16)(n < a.N ? w[e] * kLog2e : 0.f);
+            v[e] = (_Float16)(n < a.N ? w[e] * kLog2e : 0.f);
         }
         wfr[f] = v;
     }
@@ -150,20 +146,6 @@ flash_ema_bwd_kernel(FlashArgs a) {
 
     Producer<NPAD, SB, MAXI, MAXE> prod;
     const int col0 = hg * WID;
-    // Adds a batch's dE partials (both half-waves) to global memory, one atomic per
-    // element; padding slots' entries (never written) are skipped.
-    auto flush_dE = [&](int batch, const float* acc2) {
-        const BatchMeta* mb = meta_of(batch);
-        for (int i = threadIdx.x; i < acc_floats; i += blockDim.x) {
-            const int j = i / (2 * WID);
-            if (mb[j].u < 0) continue;
-            const int which = (i / WID) & 1;
-            const int c = i % WID;
-            const int k = batch * SB + j;
-            float* dst = (which ? a.dEv : a.dEk) + ((int64_t)b * a.K + k) * D + col0 + c;
-            atomicAdd(dst, (acc2[i] + acc2[acc_floats + i]) * kLn2);
-        }
-    };
     // Forward scores of a batch, one float4 (4 steps) per thread < SCN / 4.
     float4 s2pre = make_float4(0.f, 0.f, 0.f, 0.f);
     auto load_scores = [&](int batch) {
@@ -196,7 +178,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
         load_scores(0);
         __syncthreads();
         store_scores(S2_of(0));
-        prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), WID);
+        prod.template store<false, S::CROW>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), WID);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -207,23 +189,20 @@ flash_ema_bwd_kernel(FlashArgs a) {
             prod.load(a, b, cbi, bi + 1, kend, D, col0, WID);
             load_scores(bi + 1);
         }
-        // Flush the previous batch's dE sums (complete after the last barrier).
-        if (!DWO && bi > 0) flush_dE(bi - 1, dEacc + (cur ^ 1) * 2 * acc_floats);
-        const __bf16* cdec = cdec_of(cur);
+        const _Float16* cdec = cdec_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
-        float* acc = dEacc + (cur * 2 + th) * acc_floats;  // this half-wave's partials
         for (int j = 0; j < SB; ++j) {
             if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
             // Forward scores of this lane's 4 steps, staged in LDS with the batch.
             f32x4 s2v = {0.f, 0.f, 0.f, 0.f};
             if (HAS_S)
                 s2v = *reinterpret_cast<const f32x4*>(S2_of(cur) + (j * kBwdHeads + hl) * kTB + 16 * th + 4 * g);
-            const __bf16* crow = cdec + (j * kTB + 16 * th) * S::CROW;
-            bf16x8 cf[NS];
+            const _Float16* crow = cdec + (j * kTB + 16 * th) * S::CROW;
+            f16x8 cf[NS];
 #pragma unroll
             for (int ns = 0; ns < NS; ++ns)
-                cf[ns] = *reinterpret_cast<const bf16x8*>(crow + c16 * S::CROW + 32 * ns + 8 * g);
+                cf[ns] = *reinterpret_cast<const f16x8*>(crow + c16 * S::CROW + 32 * ns + 8 * g);
             float ek[DT], ev[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
@@ -291,44 +270,44 @@ flash_ema_bwd_kernel(FlashArgs a) {
                 }
             }
             // dE: this lane's 4 steps summed in registers; the 4 row groups (other steps)
-            // are reduce-scattered with v_permlane16/32_swap so that the writing row holds
-            // one dim tile; the two half-waves meet in LDS.
+            // are reduce-scattered with v_permlane16/32_swap so that row g holds dim tile g
+            // (DT = 4) or rows 0 and 2 hold tiles 0 and 1 (DT = 2); one atomic per lane.
+            const int64_t erow = ((int64_t)b * a.K + bi * SB + j) * D + col0 + hl * HD;
             if (DWO) {
             } else if (DT == 4) {
                 const float vk = rows4_reduce_scatter(dEk[0], dEk[1 % DT], dEk[2 % DT], dEk[3 % DT]);
                 const float vv = rows4_reduce_scatter(dEv[0], dEv[1 % DT], dEv[2 % DT], dEv[3 % DT]);
-                acc[(j * 2 + 0) * WID + hl * HD + 16 * g + c16] = vk;
-                acc[(j * 2 + 1) * WID + hl * HD + 16 * g + c16] = vv;
+                atomicAdd(a.dEk + erow + 16 * g + c16, vk * kLn2);
+                atomicAdd(a.dEv + erow + 16 * g + c16, vv * kLn2);
             } else {
                 const float vk = rows4_reduce_scatter2(dEk[0], dEk[1 % DT]);
                 const float vv = rows4_reduce_scatter2(dEv[0], dEv[1 % DT]);
                 if ((g & 1) == 0) {
-                    acc[(j * 2 + 0) * WID + hl * HD + 8 * g + c16] = vk;
-                    acc[(j * 2 + 1) * WID + hl * HD + 8 * g + c16] = vv;
+                    atomicAdd(a.dEk + erow + 8 * g + c16, vk * kLn2);
+                    atomicAdd(a.dEv + erow + 8 * g + c16, vv * kLn2);
                 }
             }
             // dW^T[d, n] += dpre^T[d, t] c_dec[t, n]: A = dpre (rows d, k = this lane's
             // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16]: four 16-bit reads of
-            // one column of the c_dec tile.
-            const __bf16* ccol = cdec + (j * kTB + 16 * th + 4 * g) * S::CROW + c16;
+            // one column of the c_dec tile, fp16 -> bf16 (dpre needs bf16's range).
+            const _Float16* ccol = cdec + (j * kTB + 16 * th + 4 * g) * S::CROW + c16;
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt) {
                 bf16x4 cb4;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) cb4[e] = ccol[e * S::CROW + 16 * (NT0 + nt)];
+                for (int e = 0; e < 4; ++e) cb4[e] = (__bf16)(float)ccol[e * S::CROW + 16 * (NT0 + nt)];
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
-                                                   E_of(cur ^ 1), WID);
+            prod.template store<false, S::CROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+                                                E_of(cur ^ 1), WID);
             store_scores(S2_of(cur ^ 1));
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();
     }
-    if (!DWO && nb > 0) flush_dE(nb - 1, dEacc + ((nb - 1) & 1) * 2 * acc_floats);
 
     // dQ (the gate carried log2 e, the query 1/sqrt(hd)) and dW.
     const float qf = kLn2 * qscale;
@@ -360,7 +339,6 @@ template <int HD, int NS, int SB>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
     return 2 * (Stage<32 * NS, SB>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
-           4 * (size_t)SB * 2 * WID * 4 +
            (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16;
 }

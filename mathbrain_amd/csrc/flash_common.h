@@ -2,7 +2,8 @@
 //
 // Both kernels work on one (sequence b, 32-step block) per workgroup and walk the valid
 // slots of b in batches of SB.  For every batch the whole workgroup first builds, in LDS,
-//   cdec[j][t][n]  (bf16)  the decayed key-side counter c_dec[t, u_j, n] that gates step t,
+//   cdec[j][t][n]  (fp16)  the decayed key-side counter c_dec[t, u_j, n] that gates step t,
+//   cdecb[j][t][n] (bf16)  the same counter for the backward's dW_pe product (backward only),
 //   E[j][0|1][D]   (fp32)  the slot's key and value embeddings,
 // and every wave then consumes the batch for its head(s).  The counter comes from the
 // chunk-start state S = C_bounds[b, t0 / Br, k] and the slot's occurrences inside the
@@ -10,6 +11,14 @@
 //   c_dec[t] = S rho^(t-cb+1) + sum_{cb <= s < t, x_s = u} rho^(t-s)
 // which is the reference's per-step  c_dec = C * rho ; C = c_dec + match
 // (mathbrain/triton_flash_ema.py:150-153, 175, 185, 241) unrolled from the chunk start.
+//
+// Gate operands are fp16 (c_dec and W_pe * log2 e, round to nearest even), not bf16: the
+// gate pre-activation sum_n c_n W_n cancels, and the dW_pe sums over thousands of steps
+// cancel further, so bf16's 8-bit significand moved dW_pe by ~2.5e-2 (norm-wise, against
+// float64) at T = 4096 with long half-lives; fp16's 11 bits bring that to ~4e-3.  The
+// counter stays in fp16 range: the chunk-start state is clamped to kCMax at load, the
+// window adds at most kMaxWin, and rho <= 1.  dpre, whose scale is unbounded, keeps bf16
+// for the dW_pe product, so that product takes the bf16 copy of the tile.
 #pragma once
 
 #include <hip/hip_bf16.h>
@@ -20,12 +29,15 @@ namespace mb {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr int kTB = 32;      // time steps per workgroup
 constexpr int kMaxWin = 64;  // positions [cb, t0 + 32) of the match window
+constexpr float kCMax = 65504.0f - kMaxWin;  // chunk-start counters saturate here (fp16)
 
 struct FlashArgs {
     const float* Q;
@@ -58,8 +70,8 @@ struct FlashArgs {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-__device__ inline f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+__device__ inline f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // 16x16x16 bf16 MFMA: A[row = lane%16][k = 4*(lane/16) + e], B[k][col = lane%16].
@@ -118,14 +130,16 @@ __device__ inline int xcd_major(int bid, int G) {
     return (bid % 8) * (G / 8) + bid / 8;
 }
 
-// LDS carve-up of the per-batch staging buffers.
-template <int NPAD, int SB>
+// LDS carve-up of the per-batch staging buffers: cdec (fp16), with BF the bf16 copy
+// cdecb, then E.
+template <int NPAD, int SB, bool BF = false>
 struct Stage {
-    static constexpr int CROW = NPAD + 8;  // bf16 per cdec row (16 B pad against conflicts)
-    static constexpr int CDEC = SB * kTB * CROW;  // bf16 elements per buffer
+    static constexpr int CROW = NPAD + 8;  // 16-bit entries per cdec row (16 B pad against conflicts)
+    static constexpr int CDEC = SB * kTB * CROW;  // entries per tile
+    static constexpr int TILES = BF ? 2 : 1;
     // width: embedding columns staged per slot
     __host__ __device__ static size_t bytes(int width) {
-        return (size_t)CDEC * 2 + (size_t)SB * 2 * width * 4;
+        return (size_t)CDEC * 2 * TILES + (size_t)SB * 2 * width * 4;
     }
 };
 
@@ -194,9 +208,7 @@ __device__ void flash_batch_meta(const FlashArgs& a, int b, int bi, int kend, co
 }
 
 // Producer: each thread owns up to MAXI blocks (slot j, 4 steps, 4 rates) of the batch's
-// cdec tiles and up to MAXE float4 of the embedding copy.  Blocks of 4 steps x 4 rates
-// let the same thread also write the transposed tile cdecT[j][n][t] (TRANS) with 8-byte
-// stores.
+// cdec tiles and up to MAXE float4 of the embedding copy.
 template <int NPAD, int SB, int MAXI, int MAXE>
 struct Producer {
     static constexpr int BPS = (kTB / 4) * (NPAD / 4);  // blocks per slot
@@ -249,11 +261,11 @@ struct Producer {
         }
     }
 
-    // Builds cdec ([SB][kTB][CROW]), optionally cdecT ([SB][NPAD][CTROW]), and E
+    // Builds cdec ([SB][kTB][CROW], fp16), with BF also cdecb (bf16, same layout), and E
     // ([SB][2][width]) of the batch into the staging buffer.
-    template <bool TRANS, int CROW, int CTROW>
+    template <bool BF, int CROW>
     __device__ void store(int t0, int cb, const float* powt, const BatchMeta* meta,
-                          __bf16* cdec, __bf16* cdecT, float* E, int width) {
+                          _Float16* cdec, __bf16* cdecb, float* E, int width) {
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
 #pragma unroll
@@ -263,9 +275,10 @@ struct Producer {
             if (j >= SB) continue;
             const int tq = (item % BPS) / (NPAD / 4);
             const int n0 = (item % (NPAD / 4)) * 4;
-            const float4 sv = s[ii];
+            // Clamped here, not at the load, so that the load's wait stays at this use.
+            const float4 sv = make_float4(fminf(s[ii].x, kCMax), fminf(s[ii].y, kCMax),
+                                          fminf(s[ii].z, kCMax), fminf(s[ii].w, kCMax));
             const uint64_t mask = meta[j].mask;
-            bf16x4 blk[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tl = 4 * tq + r;
@@ -282,23 +295,19 @@ struct Producer {
                     c2 += q.z;
                     c3 += q.w;
                 }
-                bf16x4 w;
-                w[0] = (__bf16)c0;
-                w[1] = (__bf16)c1;
-                w[2] = (__bf16)c2;
-                w[3] = (__bf16)c3;
-                blk[r] = w;
-                *reinterpret_cast<bf16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
-            }
-            if (TRANS) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    bf16x4 w;
-                    w[0] = blk[0][q];
-                    w[1] = blk[1][q];
-                    w[2] = blk[2][q];
-                    w[3] = blk[3][q];
-                    *reinterpret_cast<bf16x4*>(cdecT + (j * NPAD + n0 + q) * CTROW + 4 * tq) = w;
+                f16x4 w;
+                w[0] = (_Float16)c0;
+                w[1] = (_Float16)c1;
+                w[2] = (_Float16)c2;
+                w[3] = (_Float16)c3;
+                *reinterpret_cast<f16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
+                if (BF) {
+                    bf16x4 wb;
+                    wb[0] = (__bf16)c0;
+                    wb[1] = (__bf16)c1;
+                    wb[2] = (__bf16)c2;
+                    wb[3] = (__bf16)c3;
+                    *reinterpret_cast<bf16x4*>(cdecb + (j * kTB + tl) * CROW + n0) = wb;
                 }
             }
         }

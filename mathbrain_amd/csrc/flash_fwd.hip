@@ -2,7 +2,7 @@
 //
 // Replaces _flash_ema_fwd and flash_ema_forward (mathbrain/triton_flash_ema.py:121-241,
 // :529-568).  Semantics, per sequence b, head h, step t and valid slot k:
-//   g[t,k,:] = SiLU(c_dec[t,k,:] . W_pe[:, h])         (bf16 operands, fp32 accumulate)
+//   g[t,k,:] = SiLU(c_dec[t,k,:] . W_pe[:, h])         (fp16 operands, fp32 accumulate)
 //   s[t,k]   = q_t . (e_k[k] * g[t,k]) / sqrt(hd)
 //   O_t      = sum_k softmax_k(s) e_v[k] * g[t,k],   LSE_t = log sum_k exp(s)
 // where, when v_total >= 0, the softmax also holds the V - K_b absent slots of the
@@ -12,7 +12,7 @@
 //
 // Layout: one workgroup per (b, 32-step block) with one wave per head.  The gate GEMM
 // is computed transposed, pre^T[d, t] = W^T[d, :] c_dec^T[:, t], with
-// v_mfma_f32_16x16x32_bf16, so each lane owns one step t (lane % 16 of a 16-step tile)
+// v_mfma_f32_16x16x32_f16, so each lane owns one step t (lane % 16 of a 16-step tile)
 // and 16 of the head's 64 dims (rows 16*dt + 4*(lane/16) + i): the score's sum over d
 // stays in registers (plus two cross-lane adds), and O_t's sum over slots accumulates
 // in registers across the slot loop.  The online softmax runs in the log2 domain
@@ -47,7 +47,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
     int64_t* win = reinterpret_cast<int64_t*>(metas + 3 * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
-#define cdec_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes)
+#define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
 #define meta_of(batch) (metas + ((batch) % 3) * SB)
 
@@ -64,7 +64,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
 
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
     // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
-    bf16x8 wf[DT][NS];
+    f16x8 wf[DT][NS];
     {
         float wraw[DT][NS][8];
 #pragma unroll
@@ -83,7 +83,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int n = 32 * ns + 8 * g + e;
-                    wf[dt][ns][e] = (__bf16)(n < a.N ? wraw[dt][ns][e] * kLog2e : 0.f);
+                    wf[dt][ns][e] = (_Float16)(n < a.N ? wraw[dt][ns][e] * kLog2e : 0.f);
                 }
     }
 
@@ -114,7 +114,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
         prod.load(a, b, cbi, 0, kend, D, 0, D);
         __syncthreads();
-        prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
+        prod.template store<false, S::CROW>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -122,17 +122,17 @@ flash_ema_fwd_kernel(FlashArgs a) {
     for (int bi = 0; bi < nb; ++bi) {
         const int cur = bi & 1;
         if (bi + 1 < nb) prod.load(a, b, cbi, bi + 1, kend, D, 0, D);
-        const __bf16* cdec = cdec_of(cur);
+        const _Float16* cdec = cdec_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
         for (int j = 0; j < SB; ++j) {
             if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
-            bf16x8 cf[2][NS];
+            f16x8 cf[2][NS];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int ns = 0; ns < NS; ++ns)
-                    cf[tt][ns] = *reinterpret_cast<const bf16x8*>(
+                    cf[tt][ns] = *reinterpret_cast<const f16x8*>(
                         cdec + (j * kTB + 16 * tt + c16) * S::CROW + 32 * ns + 8 * g);
             f32x4 ek[DT], ev[DT];
 #pragma unroll
@@ -200,8 +200,8 @@ flash_ema_fwd_kernel(FlashArgs a) {
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<false, S::CROW, 4>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
-                                                 E_of(cur ^ 1), D);
+            prod.template store<false, S::CROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+                                              E_of(cur ^ 1), D);
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();

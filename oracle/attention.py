@@ -15,13 +15,19 @@ Three forms of the same attention, all in torch on the CPU:
                denominator as (V - K_b) * exp(0 - m).  ``absent_mass=False`` gives
                the Triton kernel as executed (triton_flash_ema.py:215-229 wipes the
                absent mass).  ``gate_round="bf16"`` rounds the gate operands to
-               bfloat16 as triton_flash_ema.py:188-190 does; ``gate_round="log2e"``
-               rounds c_dec and W_pe * log2(e) instead (the HIP kernel feeds the
-               MFMA the weights pre-scaled for its base-2 exponentials).
+               bfloat16 as triton_flash_ema.py:188-190 does; ``gate_round="f16"``
+               rounds c_dec and W_pe * log2(e) to float16 instead, as the HIP
+               kernel feeds its MFMA (weights pre-scaled for base-2 exponentials).
 ``sparse_backward_formulas``
                the reference's closed-form gradients (triton_flash_ema.py:336-350
                and :446-465), evaluated loop by loop; autograd of ``sparse`` must
                agree with it.
+
+``t_eval`` (both sparse forms) names the steps at which outputs and gradients are
+evaluated; the counter state still advances over every step.  Steps are independent
+given the state, so this is exact -- for the backward, provided dO is zero at every
+other step (their terms are then identically zero).  It makes the checker affordable
+on full-length sequences (T = 4096, thousands of slots).
 """
 import math
 
@@ -69,24 +75,36 @@ def dense(Q, x, E_k_slots, E_v_slots, rhos, pe_weight, n_heads, use_silu=True, c
 
 
 def _round_gate_operands(W, gate_round):
-    """W_pe as the gate GEMM sees it: exact, bf16-rounded, or bf16(W * log2 e) / log2 e."""
+    """W_pe as the gate GEMM sees it: exact, bf16-rounded, or f16(W * log2 e) / log2 e."""
     if gate_round is None:
         return W
     if gate_round == "bf16":
         return W.to(torch.bfloat16).to(W.dtype)
-    if gate_round == "log2e":
+    if gate_round == "f16":
         l2e = 1.0 / math.log(2.0)
-        return (W.float() * l2e).to(torch.bfloat16).to(W.dtype) / l2e
+        return (W.float() * l2e).to(torch.float16).to(W.dtype) / l2e
     raise ValueError(f"gate_round={gate_round!r}")
 
 
+def _round_gate_counter(c, gate_round):
+    """c_dec as the gate GEMM sees it (rounded through float32, as computed on device)."""
+    if gate_round is None:
+        return c
+    return c.float().to(torch.float16 if gate_round == "f16" else torch.bfloat16).to(c.dtype)
+
+
+def _steps(L, t_eval):
+    return list(range(L)) if t_eval is None else sorted({int(t) for t in t_eval})
+
+
 def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=True,
-           absent_mass=True, gate_round=None, return_lse=False):
+           absent_mass=True, gate_round=None, return_lse=False, t_eval=None):
     """Unique-slot flash-EMA attention.
 
     Q [B, H, L, hd]; x [B, L]; E_k / E_v [B, K, D]; W_pe [N, D] (= pe_proj.weight.T);
     unique [B, K] int64 with -1 padding; c_init [B, K, N] key-side state at t=0
-    (C_bounds[:, 0]).  Returns O [B, H, L, hd] (and LSE [B, H, L]).
+    (C_bounds[:, 0]).  Returns O [B, H, L, hd] (and LSE [B, H, L]); with ``t_eval``,
+    O [B, H, len(t_eval), hd] and LSE [B, H, len(t_eval)] at those steps, in order.
 
     The per-step order is the reference's: c_dec = C * rho (triton_flash_ema.py:185),
     g = SiLU(c_dec @ W_pe[:, head]) (:188-196), s = q.(e_k*g)/sqrt(hd) over valid
@@ -107,10 +125,14 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
     Ev = E_v.reshape(B, K, H, hd).to(dt)
     log_absent = torch.log((V_total - Kb).clamp(min=0).to(dt))       # -inf if none absent
     outs, lses = [], []
+    evaluate = set(_steps(L, t_eval))
     for t in range(L):
         c_dec = C * rho
-        cg = c_dec.float().to(torch.bfloat16).to(dt) if gate_round else c_dec
-        pre = (cg @ W).reshape(B, K, H, hd)
+        if t not in evaluate:
+            match = (x[:, t].unsqueeze(1) == unique) & valid
+            C = c_dec + match.unsqueeze(-1).to(dt)
+            continue
+        pre = (_round_gate_counter(c_dec, gate_round) @ W).reshape(B, K, H, hd)
         g = F.silu(pre) if use_silu else pre
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
         s = (q_t * Ek * g).sum(-1) / math.sqrt(hd)                   # [B,K,H]
@@ -133,7 +155,7 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
 
 @torch.no_grad()
 def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_init=None,
-                             use_silu=True, absent_mass=True, gate_round=None):
+                             use_silu=True, absent_mass=True, gate_round=None, t_eval=None):
     """The reference's closed-form backward, loop by loop (float64 recommended).
 
     D = (dO*O).sum(-1) (triton_flash_ema.py:602); p = exp(s - LSE) (:336);
@@ -143,16 +165,21 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     dW_pe[:, head] = sum c_dec^T dpre (:465).
     Returns dQ [B,H,L,hd], dE_k [B,K,D], dE_v [B,K,D], dW_pe [N,D].
     With ``gate_round`` the gate operands are rounded as in ``sparse`` and the dW_pe
-    product takes bf16 c_dec and bf16 dpre, as triton_flash_ema.py:463-465 does.
+    product takes bf16 c_dec (of the gate's rounded c_dec) and bf16 dpre, as
+    triton_flash_ema.py:463-465 does.
+    With ``t_eval`` only those steps contribute (exact when dO is zero elsewhere); dQ
+    is zero at the other steps.
     """
     B, H, L, hd = Q.shape
     K = unique.shape[1]
     N = rhos.shape[0]
     D = H * hd
     dt = Q.dtype
+    steps = _steps(L, t_eval)
     O, LSE = sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init, use_silu,
-                    absent_mass, gate_round=gate_round, return_lse=True)
-    Dv = (dO * O).sum(-1)                                            # [B,H,L]
+                    absent_mass, gate_round=gate_round, return_lse=True, t_eval=steps)
+    Dv = (dO[:, :, steps] * O).sum(-1)                               # [B,H,len(steps)]
+    slot = {t: i for i, t in enumerate(steps)}
     valid = unique != -1
     C = torch.zeros(B, K, N, dtype=dt) if c_init is None else c_init[:, :, :N].to(dt)
     C = C * valid.unsqueeze(-1).to(dt)
@@ -168,20 +195,26 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     scale = 1.0 / math.sqrt(hd)
     for t in range(L):
         c_dec = C * rho
-        pre = (bf(c_dec) @ W).reshape(B, K, H, hd)
+        if t not in slot:
+            match = (x[:, t].unsqueeze(1) == unique) & valid
+            C = c_dec + match.unsqueeze(-1).to(dt)
+            continue
+        i = slot[t]
+        cg = _round_gate_counter(c_dec, gate_round)
+        pre = (cg @ W).reshape(B, K, H, hd)
         g = F.silu(pre) if use_silu else pre
         gp = silu_grad(pre) if use_silu else torch.ones_like(pre)
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
         do_t = dO[:, :, t].unsqueeze(1)
         s = (q_t * Ek * g).sum(-1) * scale
-        p = torch.exp(s - LSE[:, :, t].unsqueeze(1)) * valid.unsqueeze(-1).to(dt)
+        p = torch.exp(s - LSE[:, :, i].unsqueeze(1)) * valid.unsqueeze(-1).to(dt)
         dp = (do_t * Ev * g).sum(-1)
-        ds = p * (dp - Dv[:, :, t].unsqueeze(1))                     # [B,K,H]
+        ds = p * (dp - Dv[:, :, i].unsqueeze(1))                     # [B,K,H]
         dQ[:, :, t] = (ds.unsqueeze(-1) * Ek * g).sum(1) * scale
         dEk += ds.unsqueeze(-1) * q_t * g * scale
         dEv += p.unsqueeze(-1) * do_t * g
         dpre = (ds.unsqueeze(-1) * q_t * scale * Ek + p.unsqueeze(-1) * do_t * Ev) * gp
-        dW += torch.einsum("bkn,bkd->nd", bf(c_dec), bf(dpre.reshape(B, K, D)))
+        dW += torch.einsum("bkn,bkd->nd", bf(cg), bf(dpre.reshape(B, K, D)))
         match = (x[:, t].unsqueeze(1) == unique) & valid
         C = c_dec + match.unsqueeze(-1).to(dt)
     return dQ, dEk.reshape(B, K, D), dEv.reshape(B, K, D), dW

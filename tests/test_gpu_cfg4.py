@@ -1,0 +1,276 @@
+"""Config 4 at its full shape through the HIP boundary, forward and backward kernels:
+B=16, T=4096, d_model=512 (8 heads x 64), N=128 rates (half-lives 1..4096), V=50257,
+Zipf(1.1) tokens, c_base from a 4096-token warm-up, and a random 0-10 % tail of token-0
+padding per sequence whose loss -- hence dO -- is masked.
+
+Against the oracle, two whole sequences (the most padded one and the one with most slots),
+with dO nonzero only at the checked steps of those two sequences, so that every gradient,
+dW_pe (summed over the batch) included, has the oracle's value:
+  * exact float64 oracle, bf16 tolerance 2e-2, at the configuration's own N(0,0.02)
+    scales: the oracle advances the counters from c_base over all 4096 steps and
+    evaluates the attention at 97 sampled steps;
+  * oracle with the kernel's rounding, 2e-3, at query N(0,1), embeddings N(0,0.25),
+    W_pe N(0,0.02^2) scales (scores reach ~50, counters ~450): three whole 64-step chunks
+    (first, middle, last), each started from the HIP boundary kernel's C_bounds of that
+    chunk, which are themselves checked against the oracle's boundary scan at the EMA
+    tolerance 1e-5, so that the oracle's gate operands are rounded from the same float32
+    counters as the kernel's.
+
+Size-independent properties at the full shape, every sequence, dense dO:
+  * W_pe = 0 gives gates SiLU(0) = 0, hence O = 0 and LSE = log V exactly;
+  * outputs before a changed suffix are bit-identical (causality, padding tail included),
+    and with dO zero on the suffix so are dQ, while dE and dW_pe agree to summation order;
+  * O is linear in E_v (the softmax does not depend on E_v);
+  * every gradient is linear in dO (dW_pe up to its bf16 dpre operand rounding);
+  * permuting the slot order (padding slots interleaved) permutes dE and leaves O, LSE,
+    dQ and dW_pe unchanged up to summation order.  Every slot's terms are bit-identical
+    in both orders (the boundary states are, exactly), but each step sums ~2,400 slots
+    one by one in fp32, with terms spanning many orders of magnitude at these score
+    scales; small terms that meet a large partial sum lose bits, so the order moves
+    results by up to ~K * 2^-24 of the largest term (measured ~2e-4): tolerance 1e-3.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import attention as att
+
+pytestmark = pytest.mark.gpu
+
+B, L, H, HD, N, V, BR = 16, 4096, 8, 64, 128, 50257, 64
+D = H * HD
+TOL_BF16 = 2e-2
+TOL_KERNEL_ROUNDING = 2e-3
+SCALE_ROUNDING = dict(qs=1.0, es=0.5, ws=0.02)
+SCALE_CFG = dict(qs=0.02, es=0.02, ws=0.02)
+
+
+def norm_err(got, want):
+    got = got.detach().double().cpu()
+    want = want.detach().double().cpu()
+    return float((got - want).abs().max() / want.abs().max().clamp(min=1e-300))
+
+
+_DATA = {}
+
+
+def data():
+    if not _DATA:
+        from mathbrain_amd.synthetic import make_batch
+        _DATA.update(make_batch(B, L, V, N, 4096, seed=44, pad_frac=0.1))
+        assert int(_DATA["pad_len"].max()) > 0
+    return _DATA
+
+
+def weights(seed, qs, es, ws):
+    d = data()
+    K = d["unique"].shape[1]
+    g = torch.Generator().manual_seed(seed)
+    return dict(Q=torch.randn(B, H, L, HD, generator=g) * qs,
+                E_k=torch.randn(B, K, D, generator=g) * es,
+                E_v=torch.randn(B, K, D, generator=g) * es,
+                W=torch.randn(N, D, generator=g) * ws)
+
+
+def masked_dO(seed, rows=None, steps=None):
+    """Random dO, zero on each sequence's padding tail; restricted to ``rows`` x ``steps``
+    when given."""
+    d = data()
+    g = torch.Generator().manual_seed(seed)
+    dO = torch.randn(B, H, L, HD, generator=g)
+    for b in range(B):
+        if d["pad_len"][b] > 0:
+            dO[b, :, L - int(d["pad_len"][b]):] = 0
+    if rows is not None:
+        keep = torch.zeros(B, 1, L, 1, dtype=torch.bool)
+        for b in rows:
+            keep[b, 0, steps] = True
+        dO = dO * keep
+    return dO
+
+
+def run(w, x=None, unique=None, c_base=None, dO=None, stored_scores=False):
+    """Boundary states, forward and (with dO) backward on the GPU; CPU results."""
+    from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
+    d = data()
+    x = d["x"] if x is None else x
+    unique = d["unique"] if unique is None else unique
+    c_base = d["c_base"] if c_base is None else c_base
+    cu = lambda t: t.cuda()
+    xg, ug, rg = cu(x), cu(unique), cu(d["rhos"])
+    Q, Ek, Ev, W = cu(w["Q"]), cu(w["E_k"]), cu(w["E_v"]), cu(w["W"])
+    Cb = precompute_boundaries(xg, ug, rg, BR, cu(c_base))
+    O, LSE, _, _, _, S2 = flash_ema_forward(Q, xg, Ek, Ev, W, rg, V, ug, unique.shape[1], Cb,
+                                            Br=BR, return_scores=True)
+    out = dict(O=O.cpu(), LSE=LSE.cpu(), Cb=Cb[..., :N].cpu())
+    if dO is not None:
+        grads = flash_ema_backward(Q, xg, Ek, Ev, W, rg, V, ug, Cb, O, LSE, cu(dO), Br=BR,
+                                   scores=S2 if stored_scores else None)
+        out.update(zip(("dQ", "dE_k", "dE_v", "dW"), (t.cpu() for t in grads)))
+    del S2
+    torch.cuda.synchronize()
+    return out
+
+
+def checked_rows():
+    d = data()
+    rows = [int(d["pad_len"].argmax()), int(d["counts"].argmax())]
+    if rows[0] == rows[1]:
+        rows[1] = (rows[0] + 1) % B
+    return rows
+
+
+def oracle_from_c_base(w, r, dO, steps):
+    """Exact float64 oracle over whole sequences, evaluated at ``steps``."""
+    d = data()
+    dt = torch.float64
+    args = (w["Q"][r].to(dt), d["x"][r], w["E_k"][r].to(dt), w["E_v"][r].to(dt),
+            w["W"].to(dt), d["rhos"].to(dt), V, d["unique"][r])
+    O, LSE = att.sparse(*args, d["c_base"][r].to(dt), return_lse=True, t_eval=steps)
+    grads = att.sparse_backward_formulas(*args, dO[r].to(dt), d["c_base"][r].to(dt),
+                                         t_eval=steps)
+    return (O, LSE) + tuple(grads)
+
+
+def oracle_from_chunk_states(w, r, dO, chunks, Cb):
+    """Kernel-rounding oracle over whole Br-step chunks, each started from ``Cb`` (the
+    key-side state at the chunk start); the chunks' gradient terms add up."""
+    d = data()
+    dt = torch.float64
+    Os, LSEs = [], []
+    dQ = torch.zeros(len(r), H, L, HD, dtype=dt)
+    dEk = dEv = dW = 0
+    for j in chunks:
+        s = slice(j * BR, (j + 1) * BR)
+        args = (w["Q"][r][:, :, s].to(dt), d["x"][r][:, s], w["E_k"][r].to(dt),
+                w["E_v"][r].to(dt), w["W"].to(dt), d["rhos"].to(dt), V, d["unique"][r])
+        c0 = Cb[r, j].to(dt)
+        O, LSE = att.sparse(*args, c0, return_lse=True, gate_round="f16")
+        g = att.sparse_backward_formulas(*args, dO[r][:, :, s].to(dt), c0, gate_round="f16")
+        Os.append(O)
+        LSEs.append(LSE)
+        dQ[:, :, s] = g[0]
+        dEk, dEv, dW = dEk + g[1], dEv + g[2], dW + g[3]
+    return torch.cat(Os, 2), torch.cat(LSEs, 2), dQ, dEk, dEv, dW
+
+
+def check_rows_against_oracle(w, seed, kernel_rounding):
+    d = data()
+    rows = checked_rows()
+    r = torch.tensor(rows)
+    g = torch.Generator().manual_seed(seed)
+    if kernel_rounding:
+        chunks = [0, L // BR // 2 + 5, L // BR - 1]
+        steps = [t for j in chunks for t in range(j * BR, (j + 1) * BR)]
+        tol = TOL_KERNEL_ROUNDING
+    else:
+        steps = sorted(set(torch.randperm(L, generator=g)[:94].tolist()) | {0, 4031, L - 1})
+        tol = TOL_BF16
+    dO = masked_dO(seed + 1, rows, steps)
+    got = run(w, dO=dO)
+    got_s = run(w, dO=dO, stored_scores=True)
+    if kernel_rounding:
+        from oracle import scan as oscan
+        want_cb = oscan.boundary_states(d["x"][r], d["unique"][r], d["rhos"], BR, d["c_base"][r])
+        cb = got["Cb"][r].double().numpy()
+        err = abs(cb - want_cb)
+        print(f"C_bounds worst relative error {float((err / (abs(want_cb) + 1e-30)).max()):.2e}")
+        assert (err <= 1e-5 * abs(want_cb) + 1e-30).all(), float((err / (abs(want_cb) + 1e-30)).max())
+        O, LSE, dQ, dEk, dEv, dW = oracle_from_chunk_states(w, r, dO, chunks, got["Cb"])
+    else:
+        O, LSE, dQ, dEk, dEv, dW = oracle_from_c_base(w, r, dO, steps)
+    errs = {
+        "O": norm_err(got["O"][r][:, :, steps], O),
+        "LSE": norm_err(got["LSE"][r][:, :, steps], LSE),
+        "dQ": norm_err(got["dQ"][r], dQ),
+        "dE_k": norm_err(got["dE_k"][r], dEk),
+        "dE_v": norm_err(got["dE_v"][r], dEv),
+        "dW_pe": norm_err(got["dW"], dW),
+        "dW_pe (stored scores)": norm_err(got_s["dW"], dW),
+        "dE_k (stored scores)": norm_err(got_s["dE_k"][r], dEk),
+    }
+    print(f"rows {rows}, K_b {[int(d['counts'][i]) for i in rows]}, pad "
+          f"{[int(d['pad_len'][i]) for i in rows]}: " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert max(errs.values()) < tol, errs
+    others = [b for b in range(B) if b not in rows]
+    for k in ("dQ", "dE_k", "dE_v"):
+        assert torch.count_nonzero(got[k][others]) == 0, k
+    for k in ("O", "LSE"):
+        assert torch.isfinite(got[k]).all(), k
+
+
+def test_cfg4_whole_chunks_kernel_rounding():
+    check_rows_against_oracle(weights(1, **SCALE_ROUNDING), seed=2, kernel_rounding=True)
+
+
+def test_cfg4_sampled_steps_exact():
+    check_rows_against_oracle(weights(3, **SCALE_CFG), seed=4, kernel_rounding=False)
+
+
+def test_cfg4_zero_gate_weights():
+    w = weights(5, **SCALE_ROUNDING)
+    w["W"].zero_()
+    got = run(w)
+    assert torch.count_nonzero(got["O"]) == 0
+    assert torch.allclose(got["LSE"], torch.full_like(got["LSE"], math.log(V)), rtol=1e-6, atol=0)
+
+
+def test_cfg4_causal_prefix_and_padding_tail():
+    d = data()
+    w = weights(6, **SCALE_ROUNDING)
+    cut = 56 * BR                                   # 3584: before every padding tail here
+    dO = masked_dO(7)
+    dO[:, :, cut:] = 0
+    a = run(w, dO=dO)
+    # a different suffix drawn from each sequence's own slots (unique and c_base unchanged)
+    g = torch.Generator().manual_seed(8)
+    x2 = d["x"].clone()
+    for b in range(B):
+        slots = d["unique"][b, : int(d["counts"][b])]
+        x2[b, cut:] = slots[torch.randint(0, slots.numel(), (L - cut,), generator=g)]
+    assert not torch.equal(x2, d["x"])
+    c = run(w, x=x2, dO=dO)
+    assert torch.equal(a["O"][:, :, :cut], c["O"][:, :, :cut])
+    assert torch.equal(a["LSE"][:, :, :cut], c["LSE"][:, :, :cut])
+    assert not torch.equal(a["O"][:, :, cut:], c["O"][:, :, cut:])
+    assert torch.equal(a["dQ"], c["dQ"])
+    assert torch.count_nonzero(a["dQ"][:, :, cut:]) == 0
+    for k in ("dE_k", "dE_v", "dW"):
+        assert norm_err(c[k], a[k]) < 1e-5, k
+
+
+def test_cfg4_linear_in_value_embeddings():
+    w1 = weights(9, **SCALE_ROUNDING)
+    w2 = dict(w1, E_v=weights(10, **SCALE_ROUNDING)["E_v"])
+    w12 = dict(w1, E_v=w1["E_v"] + w2["E_v"])
+    o1, o2, o12 = run(w1)["O"], run(w2)["O"], run(w12)["O"]
+    e = norm_err(o1 + o2, o12)
+    print(f"O(E_v1) + O(E_v2) vs O(E_v1 + E_v2): {e:.2e}")
+    assert e < 1e-5
+
+
+def test_cfg4_gradients_linear_in_dO():
+    w = weights(11, **SCALE_ROUNDING)
+    dO1, dO2 = masked_dO(12), masked_dO(13)
+    g1, g2, g12 = run(w, dO=dO1), run(w, dO=dO2), run(w, dO=dO1 + dO2)
+    errs = {k: norm_err(g1[k] + g2[k], g12[k]) for k in ("dQ", "dE_k", "dE_v", "dW")}
+    print(", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert max(errs["dQ"], errs["dE_k"], errs["dE_v"]) < 1e-5, errs
+    assert errs["dW"] < 1e-2, errs       # dpre enters the dW_pe MFMA as bf16
+
+
+def test_cfg4_slot_permutation():
+    d = data()
+    w = weights(14, **SCALE_ROUNDING)
+    dO = masked_dO(15)
+    a = run(w, dO=dO)
+    K = d["unique"].shape[1]
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(16))
+    wp = dict(w, E_k=w["E_k"][:, perm], E_v=w["E_v"][:, perm])
+    p = run(wp, unique=d["unique"][:, perm], c_base=d["c_base"][:, perm], dO=dO)
+    errs = {"O": norm_err(p["O"], a["O"]), "LSE": norm_err(p["LSE"], a["LSE"]),
+            "dQ": norm_err(p["dQ"], a["dQ"]), "dE_k": norm_err(p["dE_k"], a["dE_k"][:, perm]),
+            "dE_v": norm_err(p["dE_v"], a["dE_v"][:, perm]), "dW": norm_err(p["dW"], a["dW"])}
+    print(", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert max(errs.values()) < 1e-3, errs

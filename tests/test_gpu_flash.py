@@ -3,14 +3,15 @@ CPU oracle on seeded inputs.
 
 Tolerances are norm-wise, max|got - want| / max|want| (outputs are ~1/V-scaled when the
 absent-slot mass is included, so element-wise relative error is meaningless):
-  * 2e-3 against the oracle with the kernel's own gate rounding (bf16 of c_dec and of
-    W_pe * log2 e), which pins everything but that rounding -- at deliberately large
-    weight scales (queries N(0,1), embeddings N(0,0.25), W_pe N(0,0.09)) so that the
-    softmax is far from uniform and every term matters;
+  * 2e-3 against the oracle with the kernel's own rounding (fp16 c_dec and W_pe * log2 e
+    in the gate, bf16 c_dec and dpre in the dW_pe product), which pins everything but
+    that rounding -- at deliberately large weight scales (queries N(0,1), embeddings
+    N(0,0.25), W_pe N(0,0.09)) so that the softmax is far from uniform and every term
+    matters;
   * 2e-2 against the exact float64 oracle -- the bf16 tolerance of the task -- at the
     configurations' own scale N(0, 0.02) for queries, embeddings and W_pe.  At the large
-    test scales scores reach ~100 and bf16 gate operands alone move O by a few percent,
-    which is what the Triton reference's bf16 gate (triton_flash_ema.py:188-190) does too.
+    test scales scores reach ~100, where 16-bit gate operands alone move O by a percent or
+    more (the Triton reference's bf16 gate, triton_flash_ema.py:188-190, by more still).
 C_bounds come from the oracle's boundary scan, so these tests do not depend on the HIP
 boundary kernel.
 """
@@ -83,7 +84,7 @@ def oracle_forward(c, use_silu=True, absent_mass=True, gate_round=None):
 def check_forward(c, use_silu=True, absent_mass=True, exact=False):
     O, LSE = gpu_forward(c, use_silu, absent_mass)
     assert torch.isfinite(O).all() and torch.isfinite(LSE).all()
-    Ow, LSEw = oracle_forward(c, use_silu, absent_mass, gate_round="log2e")
+    Ow, LSEw = oracle_forward(c, use_silu, absent_mass, gate_round="f16")
     e1 = norm_err(O, Ow)
     e2 = norm_err(LSE, LSEw)
     Oe, LSEe = oracle_forward(c, use_silu, absent_mass)
@@ -155,7 +156,7 @@ def test_fwd_row_without_slots():
     c["unique"][1] = -1
     c["c_base"][1] = 0
     O, LSE = gpu_forward(c)
-    Ow, LSEw = oracle_forward(c, gate_round="log2e")
+    Ow, LSEw = oracle_forward(c, gate_round="f16")
     assert torch.count_nonzero(O[1]) == 0
     assert torch.allclose(LSE[1], torch.full_like(LSE[1], float(np.log(60))), rtol=1e-5)
     assert norm_err(O, Ow) < TOL_KERNEL_ROUNDING
@@ -202,7 +203,7 @@ def check_backward(c, use_silu=True, absent_mass=True, exact=False, seed=0, stor
     g = torch.Generator().manual_seed(seed + 77)
     dO = torch.randn(c["Q"].shape, generator=g)
     got = gpu_backward(c, dO, use_silu, absent_mass, stored_scores)
-    want = oracle_backward(c, dO, use_silu, absent_mass, gate_round="log2e")
+    want = oracle_backward(c, dO, use_silu, absent_mass, gate_round="f16")
     names = ("dQ", "dE_k", "dE_v", "dW_pe")
     errs = [norm_err(a, b) for a, b in zip(got, want)]
     msg = ", ".join(f"{n} {e:.2e}" for n, e in zip(names, errs))
