@@ -1,6 +1,6 @@
 """Benchmark of the Per-Slot EMA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|scan]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|cfg4|scan|gating|model|copy]
 
 Default workload (configuration 2 of the task): one flash-EMA gated attention layer,
 forward + backward, B=56, T=512, d_model=512, 8 heads x 64, N=64 EMA rates, V=50257,
@@ -15,6 +15,9 @@ with HIP events on the launch stream, against the dense bf16/fp16 MFMA peak of 2
 `cpu_baseline` times the CPU restatement of the reference algorithm (the oracle, a port
 of the reference's PyTorch path) on a bounded slice of the same workload on this host.
 
+`--workload cfg4` runs the same step at configuration 4 (B=16, T=4096, N=128, a random
+0-10 % tail of padding per sequence with dO zero there); it is a second measurement, not the
+headline metric.
 `--workload scan` measures the EMA query scan of configuration 3 instead (B=56, T=2048,
 N=128, c_base from an 8192-token warm-up) in GB/s of algorithmic traffic.
 `--workload gating` measures the query gating forward + backward (mb_gating_fwd/bwd with
@@ -41,11 +44,12 @@ if ROOT not in sys.path:
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBS = 8000.0
 
-# HBM bytes per dispatch of the dominant kernels, from the rocprofv3 FETCH_SIZE and
-# WRITE_SIZE passes scaled by a 1 GiB copy (profiles/flash_ema_cfg2.md); re-measured
-# whenever the kernel changes.
+# HBM bytes per backward (its flash_ema_bwd_kernel dispatches), from the rocprofv3
+# FETCH_SIZE and WRITE_SIZE passes scaled by a 1 GiB copy (profiles/flash_ema_cfg2.md,
+# profiles/flash_ema_cfg4.md); re-measured whenever the kernel changes.
 TRAFFIC_BYTES = {
-    "flash_ema_bwd_kernel": 7493.7e6,
+    "cfg2": 13262.1e6,
+    "cfg4": 50715.2e6,
 }
 
 
@@ -53,15 +57,22 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def attention_case(seed=0):
+ATTENTION_CONFIGS = {
+    # name: (B, T, heads, head_dim, N, V, padding tail fraction)
+    "cfg2": (56, 512, 8, 64, 64, 50257, 0.0),
+    "cfg4": (16, 4096, 8, 64, 128, 50257, 0.1),
+}
+
+
+def attention_case(seed=0, config="cfg2"):
     from mathbrain_amd.synthetic import make_batch
-    B, L, H, hd, N, V = 56, 512, 8, 64, 64, 50257
-    d = make_batch(B, L, V, N, 4096, seed=seed)
+    B, L, H, hd, N, V, pad = ATTENTION_CONFIGS[config]
+    d = make_batch(B, L, V, N, 4096, seed=seed, pad_frac=pad)
     dev = torch.device("cuda", torch.cuda.current_device())
     g = torch.Generator().manual_seed(seed + 1)
     K = d["unique"].shape[1]
     D = H * hd
-    c = dict(B=B, L=L, H=H, hd=hd, N=N, V=V, K=K, D=D, counts=d["counts"])
+    c = dict(B=B, L=L, H=H, hd=hd, N=N, V=V, K=K, D=D, counts=d["counts"], config=config)
     c["x"] = d["x"].to(dev)
     c["unique"] = d["unique"].to(dev)
     c["c_base"] = d["c_base"].to(dev)
@@ -70,7 +81,11 @@ def attention_case(seed=0):
     c["E_k"] = (torch.randn(B, K, D, generator=g) * 0.02).to(dev)
     c["E_v"] = (torch.randn(B, K, D, generator=g) * 0.02).to(dev)
     c["W"] = (torch.randn(N, D, generator=g) * 0.02).to(dev)
-    c["dO"] = torch.randn(B, H, L, hd, generator=g).to(dev)
+    dO = torch.randn(B, H, L, hd, generator=g)
+    for b in range(B):                 # the loss is masked on the padding tail
+        if d["pad_len"][b] > 0:
+            dO[b, :, L - int(d["pad_len"][b]):] = 0
+    c["dO"] = dO.to(dev)
     c["cpu"] = d
     return c
 
@@ -127,7 +142,7 @@ def cpu_baseline_attention(c, seconds=12.0):
 
 
 def run_attention(args):
-    c = attention_case()
+    c = attention_case(config="cfg4" if args.workload == "cfg4" else "cfg2")
     for _ in range(args.warmup):
         attention_step(c)
     torch.cuda.synchronize()
@@ -150,8 +165,15 @@ def run_attention(args):
     bwd_flop = pairs * (4 * N * D + 10 * D)
     tokens = c["B"] * L
     bwd_tflops = bwd_flop / (bwd_ms * 1e-3) / 1e12
+    if c["config"] == "cfg2":
+        metric = "flash-EMA attn fwd+bwd tokens/s at B56 T512 d512 N64; % MFMA/HBM peak"
+        workload = "cfg2: one flash-EMA layer fwd+bwd (boundary states + fwd + bwd)"
+    else:
+        metric = "flash-EMA attn fwd+bwd tokens/s at B16 T4096 d512 N128 (configuration 4)"
+        workload = ("cfg4: one flash-EMA layer fwd+bwd (boundary states + fwd + bwd), "
+                    "0-10 % padding tail per sequence")
     line = {
-        "metric": "flash-EMA attn fwd+bwd tokens/s at B56 T512 d512 N64; % MFMA/HBM peak",
+        "metric": metric,
         "value": round(tokens / (ms * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -163,7 +185,7 @@ def run_attention(args):
         "vs_baseline": None,
         "dtype": "fp16 gate MFMA (bf16 dW_pe MFMA), fp32 state/softmax/accumulate",
         "data": "synthetic Zipf(1.1) tokens, seeded; random N(0,0.02) weights",
-        "config": {"workload": "cfg2: one flash-EMA layer fwd+bwd (boundary states + fwd + bwd)",
+        "config": {"workload": workload,
                    "B": c["B"], "T": L, "d_model": D, "heads": c["H"], "head_dim": c["hd"],
                    "N": N, "V": c["V"], "K_max": c["K"], "sum_K_b": int(c["counts"].sum()),
                    "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
@@ -172,9 +194,10 @@ def run_attention(args):
         "roofline": {"bound": "mfma", "kernel": "flash_ema_bwd_kernel",
                      "achieved": round(bwd_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(bwd_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": TRAFFIC_BYTES.get("flash_ema_bwd_kernel")},
+                     "traffic": TRAFFIC_BYTES.get(c["config"])},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and c["config"] == "cfg2":
+        # (at cfg4 one whole sequence alone takes the oracle minutes)
         line["cpu_baseline"] = cpu_baseline_attention(c)
     return line
 
@@ -377,7 +400,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("attention", "scan", "gating", "model", "copy"),
+    ap.add_argument("--workload", choices=("attention", "cfg4", "scan", "gating", "model", "copy"),
                     default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -388,8 +411,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         sys.exit(1)
-    run = {"attention": run_attention, "scan": run_scan, "gating": run_gating, "model": run_model,
-           "copy": run_copy}[args.workload]
+    run = {"attention": run_attention, "cfg4": run_attention, "scan": run_scan,
+           "gating": run_gating, "model": run_model, "copy": run_copy}[args.workload]
     line = run(args)
     print(json.dumps(line), flush=True)
 
