@@ -53,7 +53,12 @@ flash_ema_bwd_kernel(FlashArgs a) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
     constexpr int WID = kBwdHeads * HD;  // embedding columns of this head group
-    using S = Stage<NPAD, SB>;
+    // With SB > 1 the producer writes a transposed bf16 copy of the counter tile for the dW_pe
+    // product; with one slot per batch (N > 64) that copy costs more on the producer's
+    // critical path than the per-wave fp16 -> bf16 conversion it saves (measured), so the
+    // waves convert instead.
+    constexpr bool TT = SB > 1;
+    using S = Stage<NPAD, SB, TT>;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int D = a.H * HD;
@@ -75,7 +80,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
 #define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
-#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
 #define S2_of(i) (E_of(i) + SB * 2 * WID)
 #define meta_of(batch) (metas + ((batch) % kMetaRing) * SB)
 
@@ -178,7 +184,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
         load_scores(0);
         __syncthreads();
         store_scores(S2_of(0));
-        prod.template store<false, S::CROW>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), WID);
+        prod.template store<TT, S::CROW, S::TROW>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0), E_of(0), WID);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -288,20 +294,26 @@ flash_ema_bwd_kernel(FlashArgs a) {
                 }
             }
             // dW^T[d, n] += dpre^T[d, t] c_dec[t, n]: A = dpre (rows d, k = this lane's
-            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16]: four 16-bit reads of
-            // one column of the c_dec tile, fp16 -> bf16 (dpre needs bf16's range).
-            const _Float16* ccol = cdec + (j * kTB + 16 * th + 4 * g) * S::CROW + c16;
+            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16]: one 8-byte read of the
+            // transposed bf16 tile, or four 16-bit reads of a column of the fp16 tile converted
+            // to bf16 (dpre needs bf16's range, so the product is bf16).
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt) {
                 bf16x4 cb4;
+                if (TT) {
+                    const __bf16* ccol = cdecT_of(cur) + (j * NPAD + c16) * S::TROW + 16 * th + 4 * g;
+                    cb4 = *reinterpret_cast<const bf16x4*>(ccol + 16 * (NT0 + nt) * S::TROW);
+                } else {
+                    const _Float16* ccol = cdec + (j * kTB + 16 * th + 4 * g) * S::CROW + c16;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) cb4[e] = (__bf16)(float)ccol[e * S::CROW + 16 * (NT0 + nt)];
+                    for (int e = 0; e < 4; ++e) cb4[e] = (__bf16)(float)ccol[e * S::CROW + 16 * (NT0 + nt)];
+                }
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<false, S::CROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+            prod.template store<TT, S::CROW, S::TROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), cdecT_of(cur ^ 1),
                                                 E_of(cur ^ 1), WID);
             store_scores(S2_of(cur ^ 1));
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
@@ -330,6 +342,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
                 atomicAdd(&a.dW[(int64_t)n * D + h * HD + 16 * dt + 4 * g + i], dWacc[dt][nt][i]);
         }
 #undef cdec_of
+#undef cdecT_of
 #undef E_of
 #undef S2_of
 #undef meta_of
@@ -338,7 +351,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
 template <int HD, int NS, int SB>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
-    return 2 * (Stage<32 * NS, SB>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
+    return 2 * (Stage<32 * NS, SB, (SB > 1)>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
            (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16;
 }

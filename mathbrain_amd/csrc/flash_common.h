@@ -3,7 +3,7 @@
 // Both kernels work on one (sequence b, 32-step block) per workgroup and walk the valid
 // slots of b in batches of SB.  For every batch the whole workgroup first builds, in LDS,
 //   cdec[j][t][n]  (fp16)  the decayed key-side counter c_dec[t, u_j, n] that gates step t,
-//   cdecb[j][t][n] (bf16)  the same counter for the backward's dW_pe product (backward only),
+//   cdecT[j][n][t] (bf16)  the same counter, transposed, for the backward's dW_pe product,
 //   E[j][0|1][D]   (fp32)  the slot's key and value embeddings,
 // and every wave then consumes the batch for its head(s).  The counter comes from the
 // chunk-start state S = C_bounds[b, t0 / Br, k] and the slot's occurrences inside the
@@ -130,16 +130,20 @@ __device__ inline int xcd_major(int bid, int G) {
     return (bid % 8) * (G / 8) + bid / 8;
 }
 
-// LDS carve-up of the per-batch staging buffers: cdec (fp16), with BF the bf16 copy
-// cdecb, then E.
+// LDS carve-up of the per-batch staging buffers: cdec (fp16), with BF the transposed bf16
+// copy cdecT ([SB][NPAD][TROW], steps contiguous, for the backward's dW_pe product), then E.
 template <int NPAD, int SB, bool BF = false>
 struct Stage {
     static constexpr int CROW = NPAD + 8;  // 16-bit entries per cdec row (16 B pad against conflicts)
     static constexpr int CDEC = SB * kTB * CROW;  // entries per tile
-    static constexpr int TILES = BF ? 2 : 1;
+    // cdecT row: kTB steps + 4 entries of padding, so that 16 rates x 4 step groups read by
+    // one wave start on 64 distinct LDS banks
+    static constexpr int TROW = kTB + 4;
+    static constexpr int CT = BF ? SB * NPAD * TROW : 0;
+    static constexpr int EOFF = (CDEC + CT) * 2;  // byte offset of E
     // width: embedding columns staged per slot
     __host__ __device__ static size_t bytes(int width) {
-        return (size_t)CDEC * 2 * TILES + (size_t)SB * 2 * width * 4;
+        return (size_t)EOFF + (size_t)SB * 2 * width * 4;
     }
 };
 
@@ -261,11 +265,11 @@ struct Producer {
         }
     }
 
-    // Builds cdec ([SB][kTB][CROW], fp16), with BF also cdecb (bf16, same layout), and E
+    // Builds cdec ([SB][kTB][CROW], fp16), with BF also cdecT ([SB][NPAD][TROW], bf16), and E
     // ([SB][2][width]) of the batch into the staging buffer.
-    template <bool BF, int CROW>
+    template <bool BF, int CROW, int TROW>
     __device__ void store(int t0, int cb, const float* powt, const BatchMeta* meta,
-                          _Float16* cdec, __bf16* cdecb, float* E, int width) {
+                          _Float16* cdec, __bf16* cdecT, float* E, int width) {
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
 #pragma unroll
@@ -279,6 +283,7 @@ struct Producer {
             const float4 sv = make_float4(fminf(s[ii].x, kCMax), fminf(s[ii].y, kCMax),
                                           fminf(s[ii].z, kCMax), fminf(s[ii].w, kCMax));
             const uint64_t mask = meta[j].mask;
+            bf16x4 tb[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tl = 4 * tq + r;
@@ -301,14 +306,17 @@ struct Producer {
                 w[2] = (_Float16)c2;
                 w[3] = (_Float16)c3;
                 *reinterpret_cast<f16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
-                if (BF) {
-                    bf16x4 wb;
-                    wb[0] = (__bf16)c0;
-                    wb[1] = (__bf16)c1;
-                    wb[2] = (__bf16)c2;
-                    wb[3] = (__bf16)c3;
-                    *reinterpret_cast<bf16x4*>(cdecb + (j * kTB + tl) * CROW + n0) = wb;
+                if (BF) {  // bf16 of the gate's fp16 counter (the gate and dW_pe see one c_dec)
+                    tb[0][r] = (__bf16)(float)w[0];
+                    tb[1][r] = (__bf16)(float)w[1];
+                    tb[2][r] = (__bf16)(float)w[2];
+                    tb[3][r] = (__bf16)(float)w[3];
                 }
+            }
+            if (BF) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<bf16x4*>(cdecT + (j * NPAD + n0 + q) * TROW + 4 * tq) = tb[q];
             }
         }
         const int nvec = SB * 2 * (width / 4);

@@ -48,7 +48,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
 #define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
-#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
 #define meta_of(batch) (metas + ((batch) % 3) * SB)
 
     flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
@@ -114,7 +114,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
         prod.load(a, b, cbi, 0, kend, D, 0, D);
         __syncthreads();
-        prod.template store<false, S::CROW>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
+        prod.template store<false, S::CROW, S::TROW>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -200,7 +200,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<false, S::CROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+            prod.template store<false, S::CROW, S::TROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
                                               E_of(cur ^ 1), D);
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }

@@ -119,6 +119,46 @@ def test_gpu_scan_lengths(L):
     _close(_scan(x, rhos, V).cpu().numpy(), oscan.query_scan(x, rhos, V))
 
 
+@pytest.mark.parametrize("L,V,N,docs", [(2048, 1 << 30, 128, False), (2048, 1 << 30, 20, True),
+                                         (8192, 20000, 16, False), (4096, 1 << 30, 64, True)])
+def test_gpu_scan_more_tokens_than_lds_state(L, V, N, docs):
+    """Sequences with more distinct tokens than one pass's LDS state holds (up to all-distinct)
+    take several passes over the sequence; every output element, the final state and the
+    stamps against the oracle, with c_init keys (duplicates and pads included) and, for
+    `docs`, document boundaries."""
+    rng = np.random.default_rng(L + N)
+    B = 2
+    x = rng.integers(0, V, size=(B, L))
+    x[1] = rng.permutation(V)[:L] if V >= L else x[1]  # row 1: all distinct when V allows
+    rhos = np.exp(-np.log(2.0) / np.logspace(0, np.log10(4096), N)).astype(np.float32)
+    K = 600
+    keys = np.stack([np.concatenate([rng.choice(x[b], K // 2), rng.integers(0, V, K - K // 2)])
+                     for b in range(B)])
+    keys[0, -7:] = -1
+    keys[1, 5] = keys[1, 3]
+    c_init = (rng.random((B, K, N)) * 3).astype(np.float32)
+    doc = np.sort(rng.integers(0, 5, size=(B, L)), axis=1) if docs else None
+    got, st, sp = _scan(x, rhos, V, c_init, keys, doc, return_state=True)
+    _, inv = np.unique(np.concatenate([x.ravel(), keys.ravel()]), return_inverse=True)
+    xs = inv[:x.size].reshape(B, L)
+    ks = np.where(keys >= 0, inv[x.size:].reshape(B, K), -1)
+    Vs = int(inv.max()) + 1
+    want = oscan.query_scan(xs, rhos, Vs, c_init, ks, doc)
+    _close(got.cpu().numpy(), want)
+    sp = sp.cpu().numpy()
+    st = st.cpu().numpy()
+    for b in range(B):
+        for k in range(K):
+            if keys[b, k] < 0 or (keys[b, k + 1:] == keys[b, k]).any():
+                continue  # pads and losing duplicates keep their rows
+            occ = np.nonzero(x[b] == keys[b, k])[0]
+            if occ.size:
+                assert sp[b, k] == occ[-1]
+                _close(st[b, k], want[b, occ[-1]].astype(np.float64) + 1.0)
+            else:
+                assert sp[b, k] == -1
+
+
 def test_gpu_scan_too_long_raises():
     from mathbrain_amd._lib import HipKernelError
     with pytest.raises(HipKernelError, match="unsupported"):
