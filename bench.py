@@ -48,7 +48,7 @@ PEAK_HBM_GBS = 8000.0
 # FETCH_SIZE and WRITE_SIZE passes scaled by a 1 GiB copy (profiles/flash_ema_cfg2.md,
 # profiles/flash_ema_cfg4.md); re-measured whenever the kernel changes.
 TRAFFIC_BYTES = {
-    "cfg2": 13262.1e6,
+    "cfg2": 13261.7e6,
     "cfg4": 50715.2e6,
 }
 
