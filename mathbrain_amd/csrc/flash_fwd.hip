@@ -171,25 +171,23 @@ flash_ema_fwd_kernel(FlashArgs a) {
                 sacc += __shfl_xor(sacc, 32);
                 s[tt] = sacc;
             }
-            if (a.S2out && g == 0) {
-                float* srow = a.S2out + (((int64_t)b * a.H + h) * a.K + bi * SB + j) * a.L;
+            // One (rare) rescale branch for both step tiles, so that the softmax and P.V of
+            // the two tiles form one block the scheduler can interleave.
+            const bool need0 = s[0] > m[0] + kTau;
+            const bool need1 = s[1] > m[1] + kTau;
+            if (__any(need0 || need1)) {
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
-                    const int t = t0 + 16 * tt + c16;
-                    if (t < a.L) srow[t] = s[tt];
-                }
-            }
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const bool need = s[tt] > m[tt] + kTau;
-                if (__any(need)) {
-                    const float mn = need ? s[tt] : m[tt];
+                    const float mn = (tt ? need1 : need0) ? s[tt] : m[tt];
                     const float alpha = __builtin_amdgcn_exp2f(m[tt] - mn);
                     l[tt] *= alpha;
 #pragma unroll
                     for (int dt = 0; dt < DT; ++dt) o[tt][dt] *= alpha;
                     m[tt] = mn;
                 }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
                 const float p = __builtin_amdgcn_exp2f(s[tt] - m[tt]);
                 l[tt] += p;
 #pragma unroll
@@ -197,6 +195,14 @@ flash_ema_fwd_kernel(FlashArgs a) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         o[tt][dt][i] = __builtin_fmaf(p, ev[dt][i] * gt[tt][dt][i], o[tt][dt][i]);
+            }
+            if (a.S2out && g == 0) {
+                float* srow = a.S2out + (((int64_t)b * a.H + h) * a.K + bi * SB + j) * a.L;
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int t = t0 + 16 * tt + c16;
+                    if (t < a.L) srow[t] = s[tt];
+                }
             }
         }
         if (bi + 1 < nb) {
