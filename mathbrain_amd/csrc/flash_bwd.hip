@@ -43,11 +43,11 @@ static int zero_fill(float* p, int64_t n, hipStream_t st) {
     return check_launch("zero fill");
 }
 
-// NT0, NTW: the 16-rate tiles [NT0, NT0 + NTW) of dW_pe this launch accumulates (a 64 x 64
-// fp32 accumulator per wave is 64 registers, so N > 64 takes two launches); DWO: the
-// second such launch, which recomputes the gate and the gradients but adds only its dW_pe
-// tiles (no dQ, no dE).
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NT0, int NTW, bool DWO>
+// NTW: the 16-rate tiles of dW_pe a wave accumulates (a 64 x 64 fp32 accumulator is 64
+// registers).  XH (N > 64 at head_dim 64, one slot per batch): the rate tiles outnumber what
+// a wave holds, so the two half-waves of a head swap their dpre tiles through LDS and each
+// multiplies all 32 steps into its own half of the tiles [NTW th, NTW th + NTW).
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NTW, bool XH>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_bwd_kernel(FlashArgs a) {
     constexpr int NPAD = 32 * NS;
@@ -58,6 +58,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
     // critical path than the per-wave fp16 -> bf16 conversion it saves (measured), so the
     // waves convert instead.
     constexpr bool TT = SB > 1;
+    static_assert(!XH || SB == 1, "the dpre exchange buffer is reused slot after slot");
     using S = Stage<NPAD, SB, TT>;
     extern __shared__ __align__(16) unsigned char smem[];
 
@@ -79,6 +80,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
     int64_t* win = reinterpret_cast<int64_t*>(metas + kMetaRing * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
+    bf16x4* xbuf = reinterpret_cast<bf16x4*>(kinfo + 4);  // XH: [head][half][DT][64 lanes]
 #define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
 #define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CDEC * 2)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
@@ -265,7 +267,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
                     const float yd = p[i] * dov[dt][i];
                     dEk[dt] = __builtin_fmaf(xq, gv, dEk[dt]);
                     dEv[dt] = __builtin_fmaf(yd, gv, dEv[dt]);
-                    if (!DWO) dq[dt][i] = __builtin_fmaf(ds[i] * gv, ek[dt], dq[dt][i]);
+                    dq[dt][i] = __builtin_fmaf(ds[i] * gv, ek[dt], dq[dt][i]);
                     const float av = __builtin_fmaf(xq, ek[dt], yd * ev[dt]);
                     float dsil = 1.f;
                     if (SILU) {  // sig + g (1 - sig), with g = gv ln2
@@ -279,8 +281,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
             // are reduce-scattered with v_permlane16/32_swap so that row g holds dim tile g
             // (DT = 4) or rows 0 and 2 hold tiles 0 and 1 (DT = 2); one atomic per lane.
             const int64_t erow = ((int64_t)b * a.K + bi * SB + j) * D + col0 + hl * HD;
-            if (DWO) {
-            } else if (DT == 4) {
+            if (DT == 4) {
                 const float vk = rows4_reduce_scatter(dEk[0], dEk[1 % DT], dEk[2 % DT], dEk[3 % DT]);
                 const float vv = rows4_reduce_scatter(dEv[0], dEv[1 % DT], dEv[2 % DT], dEv[3 % DT]);
                 atomicAdd(a.dEk + erow + 16 * g + c16, vk * kLn2);
@@ -293,23 +294,48 @@ flash_ema_bwd_kernel(FlashArgs a) {
                     atomicAdd(a.dEv + erow + 8 * g + c16, vv * kLn2);
                 }
             }
-            // dW^T[d, n] += dpre^T[d, t] c_dec[t, n]: A = dpre (rows d, k = this lane's
-            // steps), B = c_dec[t = 16 th + 4 g + e][n = 16 nt + c16]: one 8-byte read of the
+            // dW^T[d, n] += dpre^T[d, t] c_dec[t, n]: A = dpre (rows d, k = 4 steps of a lane),
+            // B = c_dec[t = 16 half + 4 g + e][n = 16 nt + c16]: one 8-byte read of the
             // transposed bf16 tile, or four 16-bit reads of a column of the fp16 tile converted
             // to bf16 (dpre needs bf16's range, so the product is bf16).
-#pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) {
+            auto cop = [&](int half, int ntg) {
                 bf16x4 cb4;
                 if (TT) {
-                    const __bf16* ccol = cdecT_of(cur) + (j * NPAD + c16) * S::TROW + 16 * th + 4 * g;
-                    cb4 = *reinterpret_cast<const bf16x4*>(ccol + 16 * (NT0 + nt) * S::TROW);
+                    const __bf16* ccol = cdecT_of(cur) + (j * NPAD + c16) * S::TROW + 16 * half + 4 * g;
+                    cb4 = *reinterpret_cast<const bf16x4*>(ccol + 16 * ntg * S::TROW);
                 } else {
-                    const _Float16* ccol = cdec + (j * kTB + 16 * th + 4 * g) * S::CROW + c16;
+                    const _Float16* ccol = cdec + (j * kTB + 16 * half + 4 * g) * S::CROW + c16;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) cb4[e] = (__bf16)(float)ccol[e * S::CROW + 16 * (NT0 + nt)];
+                    for (int e = 0; e < 4; ++e) cb4[e] = (__bf16)(float)ccol[e * S::CROW + 16 * ntg];
                 }
+                return cb4;
+            };
+            if (XH) {
+                bf16x4* mine = xbuf + (hl * 2 + th) * DT * 64 + lane;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
+                for (int dt = 0; dt < DT; ++dt) mine[dt * 64] = dpre[dt];
+                __syncthreads();  // uniform: every wave takes the same slots
+                const bf16x4* other = xbuf + (hl * 2 + (th ^ 1)) * DT * 64 + lane;
+                bf16x4 dpo[DT];
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) dpo[dt] = other[dt * 64];
+#pragma unroll
+                for (int nt = 0; nt < NTW; ++nt) {
+                    const bf16x4 co = cop(th, NTW * th + nt);
+                    const bf16x4 cx = cop(th ^ 1, NTW * th + nt);
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) {
+                        dWacc[dt][nt] = mfma16x16x16(dpre[dt], co, dWacc[dt][nt]);
+                        dWacc[dt][nt] = mfma16x16x16(dpo[dt], cx, dWacc[dt][nt]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < NTW; ++nt) {
+                    const bf16x4 cb4 = cop(th, nt);
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
+                }
             }
         }
         if (bi + 1 < nb) {
@@ -326,7 +352,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int t = t0 + 16 * th + 4 * g + i;
-        if (DWO || t >= a.L) continue;
+        if (t >= a.L) continue;
         float* dst = a.dQ + (((int64_t)b * a.H + h) * a.L + t) * HD;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) dst[16 * dt + c16] = dq[dt][i] * qf;
@@ -335,7 +361,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
-            const int n = 16 * (NT0 + nt) + c16;
+            const int n = 16 * ((XH ? NTW * th : 0) + nt) + c16;
             if (n >= a.N) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -348,12 +374,12 @@ flash_ema_bwd_kernel(FlashArgs a) {
 #undef meta_of
 }
 
-template <int HD, int NS, int SB>
+template <int HD, int NS, int SB, bool XH>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
     return 2 * (Stage<32 * NS, SB, (SB > 1)>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
            (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
-           kMaxWin * 8 + 65 * 32 * NS * 4 + 16;
+           kMaxWin * 8 + 65 * 32 * NS * 4 + 16 + (XH ? (size_t)kBwdHeads * 2 * (HD / 16) * 64 * 8 : 0);
 }
 
 template <int HD, int NS, int SB>
@@ -365,22 +391,23 @@ static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
     const int nthr = 64 * 2 * kBwdHeads;
     const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
     const int me = (SB * 2 * (WID / 4) + nthr - 1) / nthr;
-    const size_t lds = bwd_lds_bytes<HD, NS, SB>();
+    // dW_pe tiles per wave: a DT x NTW block of 16x16 fp32 accumulators stays at 64
+    // registers; twice that many tiles take the half-wave dpre exchange (XH).
+    constexpr int NT = NPAD / 16;
+    constexpr int NTW = NT < 256 / HD ? NT : 256 / HD;
+    constexpr bool XH = NT > NTW;
+    static_assert(NT == NTW || NT == 2 * NTW, "at most two half-waves per head");
+    const size_t lds = bwd_lds_bytes<HD, NS, SB, XH>();
     if (lds > 160 * 1024)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: hd=%d, N=%d needs %zu B of LDS", HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
     dim3 grid(a.B * ntb * a.head_groups);
-    // dW_pe tiles per launch: a DT x NTW block of 16x16 fp32 accumulators stays at 64
-    // registers; wider N takes a second, dW-only launch for the remaining tiles.
-    constexpr int NT = NPAD / 16;
-    constexpr int NTW = NT < 256 / HD ? NT : 256 / HD;
-    static_assert(NT == NTW || NT == 2 * NTW, "at most two dW launches");
-#define MB_BWD_ONE(MI, ME, NT0, DWO)                                                        \
+#define MB_BWD(MI, ME)                                                                      \
     do {                                                                                    \
-        auto k = a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NT0, NTW, DWO>   \
-                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NT0, NTW, DWO>) \
-                        : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NT0, NTW, DWO>  \
-                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NT0, NTW, DWO>); \
+        auto k = a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH>   \
+                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH>) \
+                        : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH>  \
+                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH>); \
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
         if (e != hipSuccess) {                                                              \
@@ -389,17 +416,11 @@ static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
         }                                                                                   \
         hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, a);                                \
     } while (0)
-#define MB_BWD(MI, ME)                                  \
-    do {                                                \
-        MB_BWD_ONE(MI, ME, 0, false);                   \
-        if constexpr (NT > NTW) MB_BWD_ONE(MI, ME, NTW, true); \
-    } while (0)
     if (mi <= 1 && me <= 1) MB_BWD(1, 1);
     else if (mi <= 2 && me <= 1) MB_BWD(2, 1);
     else if (mi <= 2 && me <= 2) MB_BWD(2, 2);
     else return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: N=%d too wide", a.N);
 #undef MB_BWD
-#undef MB_BWD_ONE
     return check_launch("mb_flash_ema_bwd");
 }
 
