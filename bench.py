@@ -49,7 +49,7 @@ PEAK_HBM_GBS = 8000.0
 # profiles/flash_ema_cfg4.md); re-measured whenever the kernel changes.
 TRAFFIC_BYTES = {
     "cfg2": 13261.7e6,
-    "cfg4": 50715.2e6,
+    "cfg4": 45724.7e6,
 }
 
 
