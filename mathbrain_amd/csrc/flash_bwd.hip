@@ -53,11 +53,11 @@ flash_ema_bwd_kernel(FlashArgs a) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
     constexpr int WID = kBwdHeads * HD;  // embedding columns of this head group
-    // With SB > 1 the producer writes a transposed bf16 copy of the counter tile for the dW_pe
-    // product; with one slot per batch (N > 64) that copy costs more on the producer's
-    // critical path than the per-wave fp16 -> bf16 conversion it saves (measured), so the
-    // waves convert instead.
-    constexpr bool TT = SB > 1;
+    // The producer writes a transposed bf16 copy of the counter tile for the dW_pe product
+    // (TT) when more than one slot shares a batch or when every wave reads both halves' steps
+    // (XH); otherwise the copy costs more on the producer's critical path than the per-wave
+    // fp16 -> bf16 conversion it saves (measured), and the waves convert instead.
+    constexpr bool TT = SB > 1 || XH;
     static_assert(!XH || SB == 1, "the dpre exchange buffer is reused slot after slot");
     using S = Stage<NPAD, SB, TT>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -377,7 +377,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
 template <int HD, int NS, int SB, bool XH>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
-    return 2 * (Stage<32 * NS, SB, (SB > 1)>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
+    return 2 * (Stage<32 * NS, SB, (SB > 1 || XH)>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
            (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16 + (XH ? (size_t)kBwdHeads * 2 * (HD / 16) * 64 * 8 : 0);
 }
