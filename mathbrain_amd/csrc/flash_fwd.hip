@@ -61,6 +61,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
     const int c16 = lane & 15;
     const int g = lane >> 4;
     const int h = wave;
+    const int x32 = (lane ^ 32) << 2;  // ds_bpermute byte address of lane l ^ 32
 
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
     // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
@@ -167,8 +168,10 @@ flash_ema_fwd_kernel(FlashArgs a) {
                         gt[tt][dt][i] = gv;
                         sacc = __builtin_fmaf(qs[tt][dt][i], ek[dt][i] * gv, sacc);
                     }
-                sacc += __shfl_xor(sacc, 16);
-                sacc += __shfl_xor(sacc, 32);
+                // lanes l ^ 16 (ds_swizzle, bitmask mode: and 0x1f, xor 0x10) and l ^ 32
+                // (ds_bpermute with a byte address computed once)
+                sacc += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(sacc), 0x401F));
+                sacc += __int_as_float(__builtin_amdgcn_ds_bpermute(x32, __float_as_int(sacc)));
                 s[tt] = sacc;
             }
             // One (rare) rescale branch for both step tiles, so that the softmax and P.V of
