@@ -66,7 +66,11 @@ class SlotAttentionLayer(nn.Module):
         self.resid_dropout = nn.Dropout(dropout)
         self.use_silu = use_silu
 
-    def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None):
+    def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None,
+                E_active=None):
+        """``E_active`` optionally carries the gather E_slots[max(unique, 0)] that every layer
+        of the reference recomputes (model.py:63-64); SlotTransformerLM gathers once for all
+        layers, so the embedding backward runs once on the layers' summed gradients."""
         B, L, D = x_q.shape
         if unique_tensor is None or C_bounds is None:
             # model.py:88-99 runs the dense all-vocabulary reference here; it is the CPU
@@ -75,7 +79,8 @@ class SlotAttentionLayer(nn.Module):
                 "SlotAttentionLayer: needs unique_tensor and C_bounds (the dense all-vocabulary "
                 "path is the reference's CPU fallback, not part of this implementation)")
         # 1. slot K/V projections (model.py:63-68)
-        E_active = F.embedding(torch.clamp(unique_tensor, min=0), E_slots)
+        if E_active is None:
+            E_active = F.embedding(torch.clamp(unique_tensor, min=0), E_slots)
         memory_base = self.ln_kv(E_active)
         E_k_active = self.k_proj(memory_base)
         E_v_active = self.v_proj(memory_base)
@@ -104,8 +109,10 @@ class SlotTransformerBlock(nn.Module):
         self.ffn_norm = RMSNorm(d_model)
         self.ffn = SwiGLU(d_model, d_ff)
 
-    def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None):
-        h = x_q + self.attn(self.attn_norm(x_q), x, E_slots, rhos, C_seq, unique_tensor, K_max, C_bounds)
+    def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None,
+                E_active=None):
+        h = x_q + self.attn(self.attn_norm(x_q), x, E_slots, rhos, C_seq, unique_tensor, K_max, C_bounds,
+                            E_active)
         h = h + self.ffn(self.ffn_norm(h))
         return h
 
@@ -169,7 +176,10 @@ class SlotTransformerLM(nn.Module):
             unique_tensor, K_max = _build_unique_index(x, device)
             c_base_kv = None
         C_bounds = precompute_boundaries(x, unique_tensor, self.ema_rhos, 64, c_init=c_base_kv)
+        # The slot rows every layer gathers (model.py:63-64) are the same: gather once, so that
+        # autograd sums the layers' gradients first and runs one embedding backward.
+        E_active = F.embedding(torch.clamp(unique_tensor, min=0), E_slots)
         for layer in self.layers:
-            x_q = layer(x_q, x, E_slots, self.ema_rhos, C_seq, unique_tensor, K_max, C_bounds)
+            x_q = layer(x_q, x, E_slots, self.ema_rhos, C_seq, unique_tensor, K_max, C_bounds, E_active)
         x_q = self.final_norm(x_q)
         return self.lm_head(x_q)
