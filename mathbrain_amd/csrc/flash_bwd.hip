@@ -74,6 +74,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
     // LDS: 2 staging buffers (cdec | E | scores [SB][heads][kTB]) | W fragments |
     // meta ring | window | power table | slot info
     constexpr int SCN = HAS_S ? SB * kBwdHeads * kTB : 0;  // staged scores per buffer
+    static_assert(SCN <= 2 * kBwdHeads * 64, "one staged score per thread");
     const int stage_bytes = (int)S::bytes(WID) + SCN * 4;
     f16x8* wfr = reinterpret_cast<f16x8*>(smem + 2 * stage_bytes);
     BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + kBwdHeads * DT * NS * 64);
@@ -154,31 +155,21 @@ flash_ema_bwd_kernel(FlashArgs a) {
 
     Producer<NPAD, SB, MAXI, MAXE> prod;
     const int col0 = hg * WID;
-    // Forward scores of a batch, one float4 (4 steps) per thread < SCN / 4.
-    float4 s2pre = make_float4(0.f, 0.f, 0.f, 0.f);
+    // Forward scores of a batch, one float per thread (SCN <= blockDim.x): one register held
+    // across the slot loop, not four.
+    float s2pre = 0.f;
     auto load_scores = [&](int batch) {
-        if (!HAS_S || (int)threadIdx.x >= SCN / 4) return;
-        const int j = threadIdx.x / (kBwdHeads * kTB / 4);
-        const int hh = (threadIdx.x / (kTB / 4)) % kBwdHeads;
-        const int tq = threadIdx.x % (kTB / 4);
+        if (!HAS_S || (int)threadIdx.x >= SCN) return;
+        const int j = threadIdx.x / (kBwdHeads * kTB);
+        const int hh = (threadIdx.x / kTB) % kBwdHeads;
+        const int t = t0 + threadIdx.x % kTB;
         const int k = batch * SB + j;
-        const int t = t0 + 4 * tq;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (k < kend) {
-            const float* src = a.S2in + (((int64_t)b * a.H + hg * kBwdHeads + hh) * a.K + k) * a.L + t;
-            if ((a.L & 3) == 0 && t + 3 < a.L) {
-                v = *reinterpret_cast<const float4*>(src);
-            } else {
-                if (t + 0 < a.L) v.x = src[0];
-                if (t + 1 < a.L) v.y = src[1];
-                if (t + 2 < a.L) v.z = src[2];
-                if (t + 3 < a.L) v.w = src[3];
-            }
-        }
-        s2pre = v;
+        s2pre = (k < kend && t < a.L)
+                    ? a.S2in[(((int64_t)b * a.H + hg * kBwdHeads + hh) * a.K + k) * a.L + t]
+                    : 0.f;
     };
     auto store_scores = [&](float* dst) {
-        if (HAS_S && (int)threadIdx.x < SCN / 4) reinterpret_cast<float4*>(dst)[threadIdx.x] = s2pre;
+        if (HAS_S && (int)threadIdx.x < SCN) dst[threadIdx.x] = s2pre;
     };
     if (nb > 0) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));

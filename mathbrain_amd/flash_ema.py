@@ -172,7 +172,8 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
 # With SAVE_SCORES, FlashEMAFunction keeps the forward's scores ([B, H, K_max, L] fp32,
 # 1.4 GB at B=56, T=512, H=8, K_max=1638) and the backward skips recomputing them.  Off by
 # default: on gfx950 the extra live registers of that variant cost more than the skipped
-# score arithmetic (30.1 ms recomputing vs 33.3 ms reading them, configuration 2).
+# score arithmetic (configuration 2: backward 23.0 ms recomputing vs 23.5 ms reading them,
+# and 0.3 ms more in the forward to write them).
 SAVE_SCORES = False
 
 
