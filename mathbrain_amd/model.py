@@ -162,8 +162,11 @@ class SlotTransformerLM(nn.Module):
             C_seq = F.dropout(C_seq, p=self.ema_dropout, training=True)
         if unique_slots is not None and pad_mask is not None:
             unique_tensor = unique_slots.masked_fill(~pad_mask, -1)
-            K_max = max(int(pad_mask.sum(dim=1).max().item()), 16)
-            unique_tensor = unique_tensor[:, :K_max]
+            # K_max: the slot list's width (at least 16).  The reference reads back the largest
+            # valid count instead (model.py:169, a host sync every step) and cuts the list
+            # there; with the data loader's prefix masks both are the width, and the kernels
+            # skip a row's trailing padding slots either way.
+            K_max = max(unique_tensor.shape[1], 16)
             c_base_kv = c_base[:, :K_max, :] if c_base is not None else None
             if unique_tensor.shape[1] < K_max:
                 # fewer than 16 slots in every row: pad the slot list to the 16 the
