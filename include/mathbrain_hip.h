@@ -3,8 +3,9 @@
  *
  * Every entry point takes device pointers, plain sizes and strides, and a HIP stream
  * (hipStream_t passed as void*; NULL = the null stream).  Nothing here allocates:
- * callers pass every output buffer, and no call needs a workspace.  Calls are
- * asynchronous on the stream.
+ * callers pass every output buffer, and the one call that needs device scratch
+ * (mb_corpus_states) takes it as a workspace argument.  Calls are asynchronous on
+ * the stream.
  *
  * Return value: MB_OK (0) on success; a negative MB_ERR_* code for an argument the call
  * rejects before launching anything; a positive hipError_t code when the HIP runtime
@@ -208,6 +209,75 @@ int mb_gating_bwd(const float *dy, const float *x_q, int64_t xq_row_stride, cons
                   const float *mu, const float *rstd, int64_t rows, int D, int use_silu,
                   float *dx_q, float *dp_pre, float *dbias, float *dln_w, float *dln_b,
                   void *stream);
+
+/*
+ * Data pipeline on the device (the producers of the hot path's inputs).
+ *
+ * Per-position EMA states of a whole corpus.  Replaces the preprocessing scan of
+ * preprocess_corpus (mathbrain/data.py:276-303):
+ *
+ *   states[t,:] = sum_{s <= t, tokens[s] = tokens[t], segment[s] = segment[t]} rho^(t-s)
+ *
+ * the state of token tokens[t] just after its occurrence at t, restarted wherever the
+ * document changes (data.py:287-290).
+ *
+ *   tokens   [T] int32
+ *   segment  [T] int32: document segment of each position, nondecreasing, a new value
+ *            wherever the document id changes
+ *   order    [T] int64: the positions sorted by token, ascending within a token (a stable
+ *            argsort of tokens)
+ *   rhos     [N] fp32, 1 <= N <= 128
+ *   states   [T, N] fp32 output
+ *   work     device workspace of at least mb_corpus_states_workspace(T, N) bytes
+ *
+ * Limits: T <= 2^31 - 1 (positions are int32, as in pos_dict.pkl).
+ */
+int64_t mb_corpus_states_workspace(int64_t T, int N);
+int mb_corpus_states(const int32_t *tokens, const int32_t *segment, const int64_t *order,
+                     int64_t T, const float *rhos, int N, float *states, void *work,
+                     int64_t work_bytes, void *stream);
+
+/*
+ * Slot lists of a batch of chunks (first half of the batch builder).  Replaces the slot
+ * expansion of WikiTextMMapDataset.__getitem__ (mathbrain/data.py:101-125).  Chunk b is
+ * tokens[start[b]:end[b]) of a document that begins at doc_start[b]; its slots are the
+ * distinct tokens of the chunk in increasing id order (torch.unique, :103-105), then the
+ * distinct tokens of tokens[doc_start[b]:start[b]) that are not in the chunk, in
+ * increasing id order (:110-123).
+ *
+ *   tokens     [T] int32, ids in [0, V) (others are ignored)
+ *   next_pos   [T] int32: position of the next occurrence of the same token, >= T if none
+ *   doc_start, start, end  [B] int64 on the device; a row without
+ *              0 <= doc_start <= start < end <= T is treated as empty
+ *   last       [B, V] int32 out: last occurrence before start[b] in the document, or -1
+ *   slot_of    [B, V] int32 out: slot of each token in row b, or -1
+ *   slot_tok   [B, V] int64 out: token of each slot (the first counts[b][1] entries)
+ *   counts     [B, 2] int32 out: (number of chunk tokens, number of slots)
+ */
+int mb_slot_lists(const int32_t *tokens, const int32_t *next_pos, int64_t T, int64_t V,
+                  const int64_t *doc_start, const int64_t *start, const int64_t *end, int B,
+                  int32_t *last, int32_t *slot_of, int64_t *slot_tok, int32_t *counts,
+                  void *stream);
+
+/*
+ * The collated batch (second half).  Replaces the c_base lookup of __getitem__
+ * (mathbrain/data.py:127-140) and dynamic_collate_fn (:205-232):
+ *
+ *   c_base[b,k,:] = states[p,:] * rho^(start[b] - p),  p = last[b, slot_tok[b,k]]
+ *
+ * (zero when p < 0 or k >= counts[b][1]); unique_slots [B, K_max] int64 (0 past the
+ * slots), pad_mask [B, K_max] uint8, and per chunk position chunks [B, L] int64 (0
+ * past the chunk), doc_out [B, L] int64 (-1 past), inverse [B, L] int64 (the slot of the
+ * token, 0 past).  Inputs as mb_slot_lists plus doc_ids [T] int32, states [T, N] fp32
+ * and rhos [N]; K_max >= max_b counts[b][1] and L >= max_b (end[b] - start[b]) give
+ * full rows (smaller values truncate).
+ */
+int mb_slot_batch(const int32_t *tokens, const int32_t *doc_ids, const float *states,
+                  const float *rhos, int N, int64_t T, int64_t V, const int64_t *doc_start,
+                  const int64_t *start, const int64_t *end, int B, const int32_t *last,
+                  const int32_t *slot_of, const int64_t *slot_tok, const int32_t *counts, int L,
+                  int K_max, int64_t *chunks, int64_t *doc_out, int64_t *unique_slots,
+                  uint8_t *pad_mask, int64_t *inverse, float *c_base, void *stream);
 
 #ifdef __cplusplus
 }

@@ -139,3 +139,24 @@ def make_doc_batch(B, T, V, N, alpha=1.1, median_len=1500, sigma=1.0, min_hl=1.0
         c_base[b, :counts[b]] = cbs[b]
     return dict(x=x, unique=unique, c_base=c_base, counts=counts, rhos=rhos, targets=targets,
                 lengths=torch.tensor(lens, dtype=torch.int64))
+
+
+def zipf_corpus(T, V, alpha=1.1, median_len=1500, sigma=1.0, seed=0):
+    """A flat synthetic corpus shaped like preprocess_corpus's input (mathbrain/data.py:
+    254-260): documents of lognormal length (median ``median_len``, at least 1 token)
+    with Zipf(alpha) tokens, cut to T tokens in all.  Returns (tokens int32 [T], doc_ids
+    int32 [T]) as numpy arrays, doc ids counting up from 0."""
+    import numpy as np
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(V, generator=gen)
+    tokens = zipf_tokens((T,), V, alpha, gen, perm).to(torch.int32).numpy()
+    rng = np.random.default_rng(seed)
+    lens = []
+    total = 0
+    while total < T:
+        n = max(1, int(np.exp(np.log(median_len) + sigma * rng.standard_normal())))
+        n = min(n, T - total)
+        lens.append(n)
+        total += n
+    doc_ids = np.repeat(np.arange(len(lens), dtype=np.int32), lens)
+    return tokens, doc_ids
