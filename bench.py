@@ -1,6 +1,6 @@
 """Benchmark of the Per-Slot EMA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|cfg4|scan|gating|model|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|cfg4|scan|gating|model|copy|corpus|batch]
 
 Default workload (configuration 2 of the task): one flash-EMA gated attention layer,
 forward + backward, B=56, T=512, d_model=512, 8 heads x 64, N=64 EMA rates, V=50257,
@@ -27,6 +27,10 @@ d_model 512, 8 heads, N=64, V=50257, B=56, T=512, bf16 autocast, AdamW, gradient
 clipping) on chunks of synthetic lognormal-length Zipf documents with carried c_base.
 `--workload copy` runs a plain 1 GiB device-to-device copy: the reference dispatch that
 scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes.
+`--workload corpus` runs the corpus EMA state scan of preprocess_corpus (mb_corpus_states)
+over a 64 M-token synthetic corpus, and `--workload batch` the device batch builder
+(mb_slot_lists + mb_slot_batch) on 56 chunks of 513 tokens with history-expanded slots and
+c_base; both in tokens/s with an HBM roofline.
 """
 import argparse
 import json
@@ -50,6 +54,7 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC_BYTES = {
     "cfg2": 13261.7e6,
     "cfg4": 45724.7e6,
+    "corpus": 19654.0e6,   # the three mb_corpus_states launches (profiles/corpus_states_64M_tokens.md)
 }
 
 
@@ -395,12 +400,194 @@ def run_copy(args):
                        "bytes_written": n * 4}}
 
 
+def run_corpus(args):
+    """The corpus state scan of preprocess_corpus (mb_corpus_states) over a 64 M-token
+    synthetic corpus (50257 ids, Zipf(1.1), lognormal documents of median 3000, N=64)."""
+    import numpy as np
+    from mathbrain_amd import _lib
+    from mathbrain_amd.data import chain_order, corpus_states
+    from mathbrain_amd.synthetic import zipf_corpus
+    T, V, N = 1 << 26, 50257, 64
+    tokens, doc_ids = zipf_corpus(T, V, median_len=3000, seed=11)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    rh = torch.exp(-math.log(2.0) / torch.logspace(0.0, math.log10(2048.0), N, dtype=torch.float64)
+                   ).to(torch.float32).to(dev)
+    tok, docs = torch.from_numpy(tokens).to(dev), torch.from_numpy(doc_ids).to(dev)
+    chain, order = chain_order(tok, docs)
+    states = torch.empty(T, N, dtype=torch.float32, device=dev)
+    ws = int(_lib.lib().mb_corpus_states_workspace(T, N))
+    work = torch.empty(ws, dtype=torch.uint8, device=dev)
+    st = _lib.stream(dev)
+
+    def call():
+        _lib.call("mb_corpus_states", _lib.ptr(order), _lib.ptr(chain), T, _lib.ptr(rh), N,
+                  _lib.ptr(states), _lib.ptr(work), ws, st)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    t0, t1 = _events()
+    t0.record()
+    for _ in range(args.steps):
+        call()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    w0, w1 = _events()
+    w0.record()
+    corpus_states(tok, docs, rh)          # with the (segment, token) sort and allocations
+    w1.record()
+    torch.cuda.synchronize()
+    wrapper_ms = w0.elapsed_time(w1)
+    # algorithmic bytes: the sorted positions and keys read once, one state row written per
+    # position
+    nbytes = T * (16 + 4 * N)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "corpus EMA state scan tokens/s (preprocess_corpus, T=64M, N=64)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "corpus state scan (C-ABI call on the sorted chains, outputs "
+                               "preallocated)", "T": T, "V": V, "N": N,
+                   "bytes_per_call": nbytes, "python_entry_ms_with_sort": round(wrapper_ms, 3)},
+        "roofline": {"bound": "hbm", "kernel": "mb_corpus_states (its 3 launches)",
+                     "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES["corpus"]},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import data as od
+        n = 1 << 22
+        c0 = time.perf_counter()
+        od.corpus_states(tokens[:n], doc_ids[:n], rh.cpu().numpy())
+        sec = time.perf_counter() - c0
+        line["cpu_baseline"] = {"value": round(n / sec, 1), "unit": "tokens/s", "cores": 1,
+                                "kind": "port",
+                                "sample": "the first 2^22 tokens of the same corpus, data.py:276-303 "
+                                          f"per-token loop in numpy ({sec:.1f} s)"}
+    return line
+
+
+def run_batch(args):
+    """The batch builder (mb_slot_lists + mb_slot_batch): 56 chunks of 512 + 1 tokens of a
+    16 M-token synthetic corpus (50257 ids, lognormal documents of median 4000, N=64),
+    slots expanded with each document's history and c_base gathered from the state rows."""
+    import numpy as np
+    from mathbrain_amd import _lib
+    from mathbrain_amd.data import chunk_index, corpus_states, next_occurrence
+    from mathbrain_amd.synthetic import zipf_corpus
+    T, V, N, B, block = 1 << 24, 50257, 64, 56, 512
+    tokens, doc_ids = zipf_corpus(T, V, median_len=4000, seed=12)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    rh = torch.exp(-math.log(2.0) / torch.logspace(0.0, math.log10(2048.0), N, dtype=torch.float64)
+                   ).to(torch.float32).to(dev)
+    tok, docs = torch.from_numpy(tokens).to(dev), torch.from_numpy(doc_ids).to(dev)
+    states = corpus_states(tok, docs, rh)
+    nxt = next_occurrence(tok)
+    cs, ce, cd, starts = chunk_index(doc_ids, block)
+    cds = np.asarray([starts[int(d)] for d in cd], np.int64)
+    rng = np.random.default_rng(0)
+    sets = []
+    for _ in range(8):
+        idx = rng.choice(len(cs), size=B, replace=False)
+        desc = torch.from_numpy(np.stack([cds[idx], cs[idx], ce[idx]])).to(dev)
+        sets.append((idx, desc, int((ce[idx] - cs[idx]).max())))
+    tabs = dict(last=torch.empty(B, V, dtype=torch.int32, device=dev),
+                slot_of=torch.empty(B, V, dtype=torch.int32, device=dev),
+                slot_tok=torch.empty(B, V, dtype=torch.int64, device=dev),
+                counts=torch.empty(B, 2, dtype=torch.int32, device=dev))
+    st = _lib.stream(dev)
+    P = _lib.ptr
+
+    def lists(desc):
+        _lib.call("mb_slot_lists", P(tok), P(nxt), T, V, P(desc[0]), P(desc[1]), P(desc[2]), B,
+                  P(tabs["last"]), P(tabs["slot_of"]), P(tabs["slot_tok"]), P(tabs["counts"]), st)
+
+    kmax = []
+    for _, desc, _ in sets:
+        lists(desc)
+        kmax.append(int(tabs["counts"][:, 1].max()))
+    K_max, L = max(kmax), max(x[2] for x in sets)
+    out = dict(chunks=torch.empty(B, L, dtype=torch.int64, device=dev),
+               docs=torch.empty(B, L, dtype=torch.int64, device=dev),
+               inv=torch.empty(B, L, dtype=torch.int64, device=dev),
+               slots=torch.empty(B, K_max, dtype=torch.int64, device=dev),
+               mask=torch.empty(B, K_max, dtype=torch.bool, device=dev),
+               c_base=torch.empty(B, K_max, N, dtype=torch.float32, device=dev))
+
+    def call(i):
+        desc = sets[i % len(sets)][1]
+        lists(desc)
+        _lib.call("mb_slot_batch", P(tok), P(docs), P(states), P(rh), N, T, V, P(desc[0]),
+                  P(desc[1]), P(desc[2]), B, P(tabs["last"]), P(tabs["slot_of"]),
+                  P(tabs["slot_tok"]), P(tabs["counts"]), L, K_max, P(out["chunks"]),
+                  P(out["docs"]), P(out["slots"]), P(out["mask"]), P(out["inv"]),
+                  P(out["c_base"]), st)
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    t0, t1 = _events()
+    t0.record()
+    for i in range(args.steps):
+        call(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    # algorithmic bytes of one batch: the history and chunk tokens scanned (token + next
+    # position), the state rows read and c_base written, the chunk rows and slot lists written
+    span = sum(int((ce[x[0]] - cds[x[0]]).sum()) for x in sets) / len(sets)
+    slots = sum(kmax) / len(kmax) * B
+    nbytes = span * 8 + 2 * slots * N * 4 + B * L * 24 + B * K_max * 9
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "slot batch builder tokens/s (56 chunks x 513 tokens, V=50257, N=64)",
+        "value": round(B * L / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32 / int64",
+        "data": "synthetic",
+        "config": {"workload": "collated batch with history-expanded slots and c_base "
+                               "(mb_slot_lists + mb_slot_batch, outputs preallocated)",
+                   "B": B, "L": L, "V": V, "N": N, "corpus_tokens": T, "mean_slots": round(slots / B, 1),
+                   "K_max": K_max, "mean_doc_prefix_scanned": round(span / B, 1),
+                   "bytes_per_call": int(nbytes)},
+        "roofline": {"bound": "hbm", "kernel": "mb_slot_lists + mb_slot_batch (their 5 launches)",
+                     "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import data as od
+        rhn = rh.cpu().numpy()
+        st_h = states.cpu().numpy()
+        pos = {}
+        order = np.argsort(tokens, kind="stable").astype(np.int32)
+        srt = tokens[order]
+        cuts = np.flatnonzero(srt[1:] != srt[:-1]) + 1
+        pos = {int(k): p for k, p in zip(srt[np.concatenate([[0], cuts])], np.split(order, cuts))}
+        c0 = time.perf_counter()
+        ntok, nb = 0, 0
+        while nb < len(sets) and time.perf_counter() - c0 < 10.0:
+            idx = sets[nb][0]
+            items = [od.get_item(tokens, doc_ids, st_h, pos, starts,
+                                 (int(cs[i]), int(ce[i]), int(cd[i])), rhn) for i in idx]
+            od.collate(items)
+            ntok += B * int((ce[idx] - cs[idx]).max())
+            nb += 1
+        sec = time.perf_counter() - c0
+        line["cpu_baseline"] = {"value": round(ntok / sec, 1), "unit": "tokens/s", "cores": 1,
+                                "kind": "port",
+                                "sample": f"{nb} of the timed batches, data.py:93-148 per-sample loop "
+                                          f"+ collate in numpy ({sec:.1f} s)"}
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("attention", "cfg4", "scan", "gating", "model", "copy"),
+    ap.add_argument("--workload", choices=("attention", "cfg4", "scan", "gating", "model", "copy",
+                                           "corpus", "batch"),
                     default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -412,7 +599,8 @@ def main():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         sys.exit(1)
     run = {"attention": run_attention, "cfg4": run_attention, "scan": run_scan,
-           "gating": run_gating, "model": run_model, "copy": run_copy}[args.workload]
+           "gating": run_gating, "model": run_model, "copy": run_copy, "corpus": run_corpus,
+           "batch": run_batch}[args.workload]
     line = run(args)
     print(json.dumps(line), flush=True)
 

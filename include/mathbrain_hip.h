@@ -216,16 +216,15 @@ int mb_gating_bwd(const float *dy, const float *x_q, int64_t xq_row_stride, cons
  * Per-position EMA states of a whole corpus.  Replaces the preprocessing scan of
  * preprocess_corpus (mathbrain/data.py:276-303):
  *
- *   states[t,:] = sum_{s <= t, tokens[s] = tokens[t], segment[s] = segment[t]} rho^(t-s)
+ *   states[t,:] = sum_{s <= t, tokens[s] = tokens[t], s in t's document segment} rho^(t-s)
  *
  * the state of token tokens[t] just after its occurrence at t, restarted wherever the
- * document changes (data.py:287-290).
+ * document changes (data.py:287-290).  The corpus comes as its positions sorted by chain:
  *
- *   tokens   [T] int32
- *   segment  [T] int32: document segment of each position, nondecreasing, a new value
- *            wherever the document id changes
- *   order    [T] int64: the positions sorted by token, ascending within a token (a stable
- *            argsort of tokens)
+ *   order    [T] int64: the positions 0..T-1 sorted by (document segment, token), ascending
+ *            positions inside one key (a stable sort of the key)
+ *   chain    [T] int64: the key of each sorted entry (equal keys = one token in one
+ *            document segment; any encoding, e.g. segment << 32 | token)
  *   rhos     [N] fp32, 1 <= N <= 128
  *   states   [T, N] fp32 output
  *   work     device workspace of at least mb_corpus_states_workspace(T, N) bytes
@@ -233,9 +232,8 @@ int mb_gating_bwd(const float *dy, const float *x_q, int64_t xq_row_stride, cons
  * Limits: T <= 2^31 - 1 (positions are int32, as in pos_dict.pkl).
  */
 int64_t mb_corpus_states_workspace(int64_t T, int N);
-int mb_corpus_states(const int32_t *tokens, const int32_t *segment, const int64_t *order,
-                     int64_t T, const float *rhos, int N, float *states, void *work,
-                     int64_t work_bytes, void *stream);
+int mb_corpus_states(const int64_t *order, const int64_t *chain, int64_t T, const float *rhos,
+                     int N, float *states, void *work, int64_t work_bytes, void *stream);
 
 /*
  * Slot lists of a batch of chunks (first half of the batch builder).  Replaces the slot

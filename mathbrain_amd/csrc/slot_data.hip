@@ -12,44 +12,28 @@ namespace {
 
 // ---- corpus states ------------------------------------------------------------------------
 //
-// The positions, sorted by token (ascending positions within a token), form one chain per
-// token.  Along the sorted order each occurrence e applies the affine map
-//     s -> a_e * s + 1,   a_e = rho^(p_e - p_{e-1}) when e-1 is the same token in the same
-//                         document segment, else 0 (a restart),
+// The positions, sorted by (document segment, token) with ascending positions inside a
+// key, form one chain per key.  Along the sorted order each occurrence e applies
+//     s -> a_e * s + 1,   a_e = rho^(p_e - p_{e-1}) when e-1 has the same key, else 0,
 // and states[p_e] is the result.  The sorted order is cut into units of kUnit occurrences:
 // pass 1 composes each unit's maps (one wave per unit, lanes over rates), pass 2 scans the
 // unit compositions per rate, pass 3 re-walks each unit from its incoming state and writes
-// the state rows.  Every occurrence costs one exp2 per rate in passes 1 and 3; the rows are
-// written once, 4*N contiguous bytes each.
+// the state rows.  Both walks read the sorted positions and keys contiguously (16 B per
+// occurrence); each occurrence costs one exp2 per rate per walk, and every state row is
+// written once, 4*N contiguous bytes.
 
 constexpr int kUnit = 1024;
 constexpr int kUnitWaves = 4;
 constexpr int kScanThreads = 1024;
 constexpr int kMaxRates = 128;
 
-// Loads occurrence e of the sorted order (position, token, segment), or -1s outside [0, T).
-__device__ inline void load_occ(const int64_t* __restrict__ order, const int32_t* __restrict__ tokens,
-                                const int32_t* __restrict__ segment, int64_t e, int64_t T, int& p,
-                                int& tk, int& sg) {
-    p = tk = sg = -1;
-    if (e >= 0 && e < T) {
-        const int64_t q = order[e];
-        if (q >= 0 && q < T) {
-            p = (int)q;
-            tk = tokens[q];
-            sg = segment[q];
-        }
-    }
-}
-
 // WALK = false: pass 1, writes the composition (A, B) of each unit into agg[2][N][n_units].
 // WALK = true: pass 3, starts from s_in[N][n_units] and writes states[p][n].
 template <bool WALK, int NV>
 __global__ void __launch_bounds__(64 * kUnitWaves)
-corpus_unit_kernel(const int64_t* __restrict__ order, const int32_t* __restrict__ tokens,
-                   const int32_t* __restrict__ segment, int64_t T, const float* __restrict__ rhos,
-                   int N, int64_t n_units, float* __restrict__ agg, const float* __restrict__ s_in,
-                   float* __restrict__ states) {
+corpus_unit_kernel(const int64_t* __restrict__ order, const int64_t* __restrict__ chain, int64_t T,
+                   const float* __restrict__ rhos, int N, int64_t n_units, float* __restrict__ agg,
+                   const float* __restrict__ s_in, float* __restrict__ states) {
     const int lane = threadIdx.x & 63;
     const int64_t u = (int64_t)blockIdx.x * kUnitWaves + (threadIdx.x >> 6);
     if (u >= n_units) return;
@@ -64,24 +48,34 @@ corpus_unit_kernel(const int64_t* __restrict__ order, const int32_t* __restrict_
     }
     const int64_t e0 = u * kUnit;
     const int64_t e1 = e0 + kUnit < T ? e0 + kUnit : T;
-    int pp, tp, sp;  // occurrence e0 - 1, the predecessor of the unit's first one
-    load_occ(order, tokens, segment, e0 - 1, T, pp, tp, sp);
+    // occurrence e0 - 1, the predecessor of the unit's first one
+    int pp = -1;
+    int64_t kp = 0;
+    if (e0 > 0) {
+        const int64_t q = order[e0 - 1];
+        pp = (q >= 0 && q < T) ? (int)q : -1;
+        kp = chain[e0 - 1];
+    }
     for (int64_t b0 = e0; b0 < e1; b0 += 64) {
         const int64_t e = b0 + lane;
-        int p, tk, sg;
-        load_occ(order, tokens, segment, e < e1 ? e : -1, T, p, tk, sg);
-        int p_prev = __shfl_up(p, 1, 64), t_prev = __shfl_up(tk, 1, 64), s_prev = __shfl_up(sg, 1, 64);
+        int p = -1;
+        int64_t key = 0;
+        if (e < e1) {
+            const int64_t q = order[e];
+            p = (q >= 0 && q < T) ? (int)q : -1;
+            key = chain[e];
+        }
+        int p_prev = __shfl_up(p, 1, 64);
+        int64_t k_prev = __shfl_up(key, 1, 64);
         if (lane == 0) {
             p_prev = pp;
-            t_prev = tp;
-            s_prev = sp;
+            k_prev = kp;
         }
-        const bool link = p >= 0 && p_prev >= 0 && tk == t_prev && sg == s_prev && p > p_prev;
+        const bool link = p >= 0 && p_prev >= 0 && key == k_prev && p > p_prev;
         const int step = link ? p - p_prev : -1;
         const int cnt = (int)(e1 - b0 < 64 ? e1 - b0 : 64);
         pp = __shfl(p, cnt - 1, 64);
-        tp = __shfl(tk, cnt - 1, 64);
-        sp = __shfl(sg, cnt - 1, 64);
+        kp = __shfl(key, cnt - 1, 64);
         for (int j = 0; j < cnt; ++j) {
             const int d = __builtin_amdgcn_readlane(step, j);
             const int pj = __builtin_amdgcn_readlane(p, j);
@@ -255,6 +249,8 @@ slot_compact_kernel(int64_t V, const int64_t* __restrict__ doc_start, const int6
 }
 
 // c_base, slot list and pad mask: each wave fills kRowsPerWave consecutive (b, k) rows.
+// Lanes 0..kRowsPerWave-1 first look up their row's slot token and last occurrence, so the
+// state rows of all kRowsPerWave rows are fetched together.
 __global__ void __launch_bounds__(256)
 slot_fill_kernel(const float* __restrict__ states, const float* __restrict__ rhos, int N, int64_t T,
                  int64_t V, const int64_t* __restrict__ start, const int32_t* __restrict__ last,
@@ -272,28 +268,42 @@ slot_fill_kernel(const float* __restrict__ states, const float* __restrict__ rho
         hi[q] = lo[q] = 0.0f;
         if (n < N) log2_split(rhos[n], hi[q], lo[q]);
     }
-    for (int64_t r = r0; r < r0 + kRowsPerWave && r < rows; ++r) {
-        const int b = (int)(r / K_max), k = (int)(r % K_max);
-        const int Kb = counts[2 * b + 1];
-        int64_t v = 0;
-        int p = -1;
-        if (k < Kb) {
-            v = slot_tok[(int64_t)b * V + k];
-            if (v >= 0 && v < V) p = last[(int64_t)b * V + v];
+    // lane j < kRowsPerWave: row r0 + j's token, source position and decay steps
+    int my_p = -1, my_steps = 0, my_valid = 0;
+    int64_t my_v = 0;
+    {
+        const int64_t r = r0 + lane;
+        if (lane < kRowsPerWave && r < rows) {
+            const int b = (int)(r / K_max), k = (int)(r % K_max);
+            if (k < counts[2 * b + 1]) {
+                my_valid = 1;
+                const int64_t v = slot_tok[(int64_t)b * V + k];
+                my_v = v;
+                if (v >= 0 && v < V) {
+                    const int p = last[(int64_t)b * V + v];
+                    const int64_t s0 = start[b];
+                    if (p >= 0 && p < T && p < s0) {
+                        my_p = p;
+                        my_steps = (int)(s0 - p);
+                    }
+                }
+            }
+            unique_slots[r] = my_valid ? my_v : 0;
+            pad_mask[r] = (uint8_t)my_valid;
         }
-        const int64_t s0 = start[b];
-        const bool have = p >= 0 && p < T && p < s0;
-        const int steps = have ? (int)(s0 - p) : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+        const int64_t r = r0 + j;
+        if (r >= rows) break;
+        const int p = __builtin_amdgcn_readlane(my_p, j);
+        const int steps = __builtin_amdgcn_readlane(my_steps, j);
         float* dst = c_base + r * N;
 #pragma unroll
         for (int q = 0; q < kMaxRates / 64; ++q) {
             const int n = lane + 64 * q;
             if (n < N)
-                dst[n] = have ? states[(int64_t)p * N + n] * pow_steps(hi[q], lo[q], steps) : 0.0f;
-        }
-        if (lane == 0) {
-            unique_slots[r] = k < Kb ? v : 0;
-            pad_mask[r] = k < Kb;
+                dst[n] = p >= 0 ? states[(int64_t)p * N + n] * pow_steps(hi[q], lo[q], steps) : 0.0f;
         }
     }
 }
@@ -336,16 +346,16 @@ extern "C" int64_t mb_corpus_states_workspace(int64_t T, int N) {
     return units_for(T) * (int64_t)N * 3 * (int64_t)sizeof(float);
 }
 
-extern "C" int mb_corpus_states(const int32_t* tokens, const int32_t* segment, const int64_t* order,
-                                int64_t T, const float* rhos, int N, float* states, void* work,
+extern "C" int mb_corpus_states(const int64_t* order, const int64_t* chain, int64_t T,
+                                const float* rhos, int N, float* states, void* work,
                                 int64_t work_bytes, void* stream) {
     MB_REQUIRE(T >= 0, "mb_corpus_states: negative T=%lld", (long long)T);
     MB_REQUIRE(N >= 1 && N <= kMaxRates, "mb_corpus_states: N=%d must be in [1, %d]", N, kMaxRates);
     MB_REQUIRE(T <= INT_MAX, "mb_corpus_states: T=%lld exceeds the int32 position range",
                (long long)T);
     if (T == 0) return MB_OK;
-    MB_REQUIRE(tokens && segment && order && rhos && states,
-               "mb_corpus_states: tokens, segment, order, rhos and states must be non-null");
+    MB_REQUIRE(order && chain && rhos && states,
+               "mb_corpus_states: order, chain, rhos and states must be non-null");
     const int64_t need = mb_corpus_states_workspace(T, N);
     if (!work || work_bytes < need)
         return fail(MB_ERR_WORKSPACE, "mb_corpus_states: workspace of %lld B given, %lld B needed",
@@ -357,22 +367,22 @@ extern "C" int mb_corpus_states(const int32_t* tokens, const int32_t* segment, c
     const dim3 ugrid((unsigned)((nu + kUnitWaves - 1) / kUnitWaves));
     const dim3 ublock(64 * kUnitWaves);
     if (N <= 64) {
-        hipLaunchKernelGGL((corpus_unit_kernel<false, 1>), ugrid, ublock, 0, st, order, tokens,
-                           segment, T, rhos, N, nu, agg, nullptr, nullptr);
+        hipLaunchKernelGGL((corpus_unit_kernel<false, 1>), ugrid, ublock, 0, st, order, chain, T,
+                           rhos, N, nu, agg, nullptr, nullptr);
     } else {
-        hipLaunchKernelGGL((corpus_unit_kernel<false, 2>), ugrid, ublock, 0, st, order, tokens,
-                           segment, T, rhos, N, nu, agg, nullptr, nullptr);
+        hipLaunchKernelGGL((corpus_unit_kernel<false, 2>), ugrid, ublock, 0, st, order, chain, T,
+                           rhos, N, nu, agg, nullptr, nullptr);
     }
     int rc = check_launch("mb_corpus_states (unit compositions)");
     if (rc) return rc;
     hipLaunchKernelGGL(corpus_scan_kernel, dim3(N), dim3(kScanThreads), 0, st, agg, nu, N, s_in);
     if ((rc = check_launch("mb_corpus_states (unit scan)"))) return rc;
     if (N <= 64) {
-        hipLaunchKernelGGL((corpus_unit_kernel<true, 1>), ugrid, ublock, 0, st, order, tokens,
-                           segment, T, rhos, N, nu, nullptr, s_in, states);
+        hipLaunchKernelGGL((corpus_unit_kernel<true, 1>), ugrid, ublock, 0, st, order, chain, T,
+                           rhos, N, nu, nullptr, s_in, states);
     } else {
-        hipLaunchKernelGGL((corpus_unit_kernel<true, 2>), ugrid, ublock, 0, st, order, tokens,
-                           segment, T, rhos, N, nu, nullptr, s_in, states);
+        hipLaunchKernelGGL((corpus_unit_kernel<true, 2>), ugrid, ublock, 0, st, order, chain, T,
+                           rhos, N, nu, nullptr, s_in, states);
     }
     return check_launch("mb_corpus_states (state rows)");
 }

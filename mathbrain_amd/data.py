@@ -72,31 +72,35 @@ def next_occurrence(tokens, srt=None, order=None):
     return nxt
 
 
-def corpus_states(tokens, doc_ids, rhos, order=None):
+def chain_order(tokens, doc_ids):
+    """(sorted keys, positions) of a stable sort by (document segment, token): the chains
+    of one token inside one document that the state scan walks."""
+    key = (_segments(doc_ids).to(torch.int64) << 32) | tokens.to(torch.int64)
+    return torch.sort(key, stable=True)
+
+
+def corpus_states(tokens, doc_ids, rhos):
     """EMA state of each position's token just after that occurrence, restarted at every
     change of document id (the preprocessing scan, data.py:276-303):
 
         states[t] = sum_{s <= t, tokens[s] = tokens[t], same document segment} rho^(t-s)
 
-    tokens, doc_ids: [T] int32 on the GPU; rhos [N] float32.  Returns [T, N] float32.
+    tokens [T] int32 (ids >= 0), doc_ids [T] int32, rhos [N] float32, on the GPU.
+    Returns [T, N] float32.
     """
     dev = _lib.require_gpu(tokens, doc_ids, rhos, what="corpus_states")
     T = tokens.numel()
     N = rhos.numel()
-    tok = tokens.to(torch.int32).contiguous()
-    seg = _segments(doc_ids.to(torch.int32).contiguous())
-    if order is None:
-        _, order = sorted_occurrences(tok)
-    order = order.to(torch.int64).contiguous()
     rh = rhos.detach().to(torch.float32).contiguous()
     states = torch.empty(T, N, dtype=torch.float32, device=dev)
     if T == 0:
         return states
+    chain, order = chain_order(tokens.reshape(-1), doc_ids.reshape(-1))
     ws = _lib.lib().mb_corpus_states_workspace(T, N)
     work = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        _lib.call("mb_corpus_states", _lib.ptr(tok), _lib.ptr(seg), _lib.ptr(order), T, _lib.ptr(rh),
-                  N, _lib.ptr(states), _lib.ptr(work), int(ws), _lib.stream(dev))
+        _lib.call("mb_corpus_states", _lib.ptr(order), _lib.ptr(chain), T, _lib.ptr(rh), N,
+                  _lib.ptr(states), _lib.ptr(work), int(ws), _lib.stream(dev))
     return states
 
 
@@ -110,21 +114,22 @@ def preprocess_corpus(documents: list, data_dir: str, N: int = 64, min_hl: float
     lens = [len(d) for d in documents]
     tokens = np.fromiter((t for d in documents for t in d), dtype=np.int32, count=sum(lens))
     doc_ids = np.repeat(np.arange(len(documents), dtype=np.int32), lens)
+    if len(tokens) and int(tokens.min()) < 0:
+        raise ValueError("preprocess_corpus: negative token ids")
     tokens.tofile(os.path.join(data_dir, "tokens.bin"))
     doc_ids.tofile(os.path.join(data_dir, "doc_ids.bin"))
     rhos = _rhos(N, min_hl, max_hl)
     T = len(tokens)
     print(f"Preprocessing {T} tokens across {len(documents)} documents...")
     tok_d = torch.from_numpy(tokens).to(dev)
-    srt, order = sorted_occurrences(tok_d)
-    states = corpus_states(tok_d, torch.from_numpy(doc_ids).to(dev), torch.from_numpy(rhos).to(dev),
-                           order=order)
+    states = corpus_states(tok_d, torch.from_numpy(doc_ids).to(dev), torch.from_numpy(rhos).to(dev))
     with open(os.path.join(data_dir, "states.bin"), "wb") as f:
         step = max(1, (1 << 28) // (4 * N))  # 256 MB of rows per host copy
         for s in range(0, T, step):
             f.write(states[s:s + step].cpu().numpy().tobytes())
     del states
     # pos_dict: token -> int32 array of its global positions (data.py:281, 293, 311-315)
+    srt, order = sorted_occurrences(tok_d)
     srt_h = srt.cpu().numpy()
     order_h = order.to(torch.int32).cpu().numpy()
     cuts = np.flatnonzero(srt_h[1:] != srt_h[:-1]) + 1
