@@ -277,6 +277,57 @@ int mb_slot_batch(const int32_t *tokens, const int32_t *doc_ids, const float *st
                   int K_max, int64_t *chunks, int64_t *doc_out, int64_t *unique_slots,
                   uint8_t *pad_mask, int64_t *inverse, float *c_base, void *stream);
 
+/*
+ * Factored linear EMA (mathbrain/factored_ema.py:22-96; the reference is a PyTorch loop
+ * with an [N, hd, hd] state per (b, h) updated at every step).  Per sequence b and head h,
+ * with q_t = Q[b,t,h*hd:], W_n = W_pe[n,h*hd:], e = E[x[b,s], h*hd:] rows of E_k / E_v:
+ *
+ *   o_t = sum_{s<t} A[t,s] e_v[x_s] + sum_n rho_n^(t+1) sum_i q_t[i] W_n[i] S_n[i,:]
+ *   A[t,s] = sum_i q_t[i] e_k[x_s][i] G[t-s][i],  G[d] = sum_n rho_n^d W_n  ([L+1, D])
+ *   S_n = sum_k c_base[b,k,n] e_k[u_k] ⊗ e_v[u_k]   (the initial state, factored_ema.py:52-67)
+ *
+ * All fp32, rows of D = H*hd elements; head_dim 32 or 64.  Token ids outside [0, V) are
+ * skipped; gathered row indices are clamped below at 0 (the reference's clamp of -1 slot
+ * ids) and skipped at or above nrows.
+ *
+ * mb_factored_outer: out[b,h,n,i,j] = sum_{r<R} alpha[b*as_b + r*as_r + n*as_n]
+ *     * X[row_x(b,r)*ld + h*hd + i] * Y[row_y(b,r)*ld + h*hd + j], row(b,r) = idx[b*R+r] or
+ *     b*R + r when idx is NULL; out [B, H, N, hd, hd].  Builds S_n (alpha = c_base, rows =
+ *     slots) and, in the backward, M_n = sum_t rho_n^(t+1) q_t ⊗ dO_t.
+ */
+int mb_factored_outer(const float *X, const int64_t *xrow, const float *Y, const int64_t *yrow,
+                      int64_t ld, int64_t nrows, const float *alpha, int64_t as_b, int64_t as_r,
+                      int64_t as_n, int B, int R, int H, int N, int hd, float *out, void *stream);
+
+/*
+ * mb_factored_apply: contracts a state [B, H, N, hd, hd] with rows,
+ *   transpose = 0: out[b,r,h*hd+i] (+)= sum_n alpha[..] sum_j w[n*ldw+h*hd+i] M[b,h,n,i,j] Y[row(b,r),h*hd+j]
+ *   transpose = 1: out[b,r,h*hd+j] (+)= sum_n alpha[..] sum_i w[n*ldw+h*hd+i] M[b,h,n,i,j] Y[row(b,r),h*hd+i]
+ * (w NULL: 1; accumulate = 1 adds to out, row stride ldo).  The c_base part of the output
+ * (M = S, rows Q, transpose 1) and of dQ (rows dO, transpose 0), and the slot gradients
+ * from M (rows E_v / E_k of the slots, alpha = c_base).
+ */
+int mb_factored_apply(const float *M, const float *w, int64_t ldw, const float *Y,
+                      const int64_t *yrow, int64_t ld, int64_t nrows, const float *alpha,
+                      int64_t as_b, int64_t as_r, int64_t as_n, int B, int R, int H, int N, int hd,
+                      int transpose, float *out, int64_t ldo, int accumulate, void *stream);
+
+/*
+ * mb_factored_tok_fwd: the token part of o (written, not added): Q [B, L, D], x [B, L]
+ * int64, E_k / E_v [V, D], G [L+1, D], O [B, L, D].
+ * mb_factored_tok_bwd: its gradients for dO [B, L, D]: dQ [B, L, D] (written), the
+ * per-position embedding gradients dEk_tok / dEv_tok [B, L, D] (to be added into rows
+ * x[b,s] of dE_k / dE_v) and dG_b [B, L, D] = sum_t dA[t,t-d] q_t ⊙ e_k[x_{t-d}] per
+ * sequence (row 0 zero), from which dW_pe = sum_d rho^d sum_b dG_b[b,d].
+ */
+int mb_factored_tok_fwd(const float *Q, const int64_t *x, int64_t V, const float *E_k,
+                        const float *E_v, const float *G, int B, int L, int H, int hd, float *O,
+                        void *stream);
+int mb_factored_tok_bwd(const float *Q, const float *dO, const int64_t *x, int64_t V,
+                        const float *E_k, const float *E_v, const float *G, int B, int L, int H,
+                        int hd, float *dQ, float *dEk_tok, float *dEv_tok, float *dG_b,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

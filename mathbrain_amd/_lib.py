@@ -43,6 +43,12 @@ SIGNATURES = {
     "mb_slot_lists": ([_p, _p, _i64, _i64, _p, _p, _p, _i, _p, _p, _p, _p, _p], _i),
     "mb_slot_batch": ([_p, _p, _p, _p, _i, _i64, _i64, _p, _p, _p, _i, _p, _p, _p, _p, _i, _i,
                        _p, _p, _p, _p, _p, _p, _p], _i),
+    "mb_factored_outer": ([_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i, _i, _i, _i, _i,
+                           _p, _p], _i),
+    "mb_factored_apply": ([_p, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i, _i, _i, _i,
+                           _i, _i, _p, _i64, _i, _p], _i),
+    "mb_factored_tok_fwd": ([_p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _p, _p], _i),
+    "mb_factored_tok_bwd": ([_p, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p], _i),
 }
 
 MB_FLASH_SILU = 1
