@@ -1,6 +1,6 @@
 """Benchmark of the Per-Slot EMA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|cfg4|scan|gating|model|copy|corpus|batch]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|cfg4|scan|gating|model|copy|corpus|batch|factored]
 
 Default workload (configuration 2 of the task): one flash-EMA gated attention layer,
 forward + backward, B=56, T=512, d_model=512, 8 heads x 64, N=64 EMA rates, V=50257,
@@ -31,6 +31,8 @@ scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes.
 over a 64 M-token synthetic corpus, and `--workload batch` the device batch builder
 (mb_slot_lists + mb_slot_batch) on 56 chunks of 513 tokens with history-expanded slots and
 c_base; both in tokens/s with an HBM roofline.
+`--workload factored` runs the factored linear EMA (factored_ema_forward + backward) at
+configuration 2's shapes with c_base, against the fp32 peak.
 """
 import argparse
 import json
@@ -581,13 +583,87 @@ def run_batch(args):
     return line
 
 
+def run_factored(args):
+    """The factored linear EMA (factored_ema_forward, fwd + bwd) at configuration 2's shapes:
+    B=56, T=512, d_model 512, 8 heads x 64, N=64, V=50257, c_base over the history-expanded
+    slots of a 4096-token warm-up per sequence."""
+    from mathbrain_amd.factored_ema import factored_ema_forward
+    from mathbrain_amd.synthetic import make_batch
+    B, T, H, hd, N, V = 56, 512, 8, 64, 64, 50257
+    D = H * hd
+    d = make_batch(B, T, V, N, 4096, min_hl=1.0, max_hl=4096.0, seed=0)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = torch.Generator().manual_seed(1)
+    Q = (torch.randn(B, T, D, generator=g) * 0.02).to(dev).requires_grad_(True)
+    Ek = (torch.randn(V, D, generator=g) * 0.02).to(dev).requires_grad_(True)
+    Ev = (torch.randn(V, D, generator=g) * 0.02).to(dev).requires_grad_(True)
+    W = (torch.randn(N, D, generator=g) * 0.02).to(dev).requires_grad_(True)
+    dO = torch.randn(B, T, D, generator=torch.Generator().manual_seed(2)).to(dev)
+    x, u, cb, rh = d["x"].to(dev), d["unique"].to(dev), d["c_base"].to(dev), d["rhos"].to(dev)
+    pm = u >= 0
+
+    def step():
+        for t in (Q, Ek, Ev, W):
+            t.grad = None
+        O = factored_ema_forward(Q, x, Ek, Ev, rh, W, H, c_base=cb, unique_slots=u, pad_mask=pm)
+        O.backward(dO)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = _events()
+    t0.record()
+    for _ in range(args.steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    K = int(d["counts"].sum())
+    pairs = B * T * (T - 1) // 2
+    # algorithmic flops: token pairs 23*hd (forward 5, backward 18), the c_base state built,
+    # applied to the steps and to the slots (6 K N hd^2 + 6 T N hd^2 per sequence and head)
+    flops = H * (pairs * 23 * hd + 6 * K * N * hd * hd + 6 * B * T * N * hd * hd)
+    tf = flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "factored linear EMA fwd+bwd tokens/s (cfg2 shapes: B56 T512 d512 H8x64 N64)",
+        "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic Zipf(1.1) tokens, c_base from a 4096-token warm-up, weights N(0, 0.02)",
+        "config": {"workload": "factored_ema_forward + backward (autograd, c_base state)",
+                   "B": B, "T": T, "D": D, "H": H, "N": N, "V": V, "slots": K,
+                   "algorithmic_tflop": round(flops / 1e12, 3)},
+        "roofline": {"bound": "mfma", "kernel": "all factored kernels (fp32 VALU)",
+                     "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": round(tf / 157.3, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import factored as of
+        torch.set_num_threads(min(16, len(os.sched_getaffinity(0))))
+        Tc = 128
+        Qc = Q.detach().cpu()[:1, :Tc].clone().requires_grad_(True)
+        Ekc = Ek.detach().cpu().requires_grad_(True)
+        Evc = Ev.detach().cpu().requires_grad_(True)
+        Wc = W.detach().cpu().requires_grad_(True)
+        c0 = time.perf_counter()
+        o = of.loop_forward(Qc, d["x"][:1, :Tc], Ekc, Evc, d["rhos"], Wc, H, c_base=d["c_base"][:1],
+                            unique_slots=d["unique"][:1], pad_mask=d["unique"][:1] >= 0)
+        o.backward(dO.cpu()[:1, :Tc])
+        sec = time.perf_counter() - c0
+        line["cpu_baseline"] = {"value": round(Tc / sec, 1), "unit": "tokens/s",
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": f"one sequence, its first {Tc} steps, factored_ema.py:22-96 "
+                                          f"loop in torch fp32 + autograd backward ({sec:.1f} s)"}
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=("attention", "cfg4", "scan", "gating", "model", "copy",
-                                           "corpus", "batch"),
+                                           "corpus", "batch", "factored"),
                     default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -600,7 +676,7 @@ def main():
         sys.exit(1)
     run = {"attention": run_attention, "cfg4": run_attention, "scan": run_scan,
            "gating": run_gating, "model": run_model, "copy": run_copy, "corpus": run_corpus,
-           "batch": run_batch}[args.workload]
+           "batch": run_batch, "factored": run_factored}[args.workload]
     line = run(args)
     print(json.dumps(line), flush=True)
 

@@ -64,8 +64,12 @@ fac_outer_kernel(const float* __restrict__ X, const int64_t* __restrict__ xrow,
 
 // TRANS = false: out[b,r,h,i] (+)= sum_n alpha[b,r,n] sum_j w[n,i] M[b,h,n,i,j] Y[row(b,r),h,j]
 // TRANS = true:  out[b,r,h,j] (+)= sum_n alpha[b,r,n] sum_i w[n,i] M[b,h,n,i,j] Y[row(b,r),h,i]
-// (w NULL: 1).  Block (64 rows, h, b); thread (row, quarter of the outputs); M_n is staged
-// in LDS once per rate for the 64 rows.
+// (w NULL: 1).  A register-tiled GEMM per rate: block (kApplyRows rows, h, b), 16 x 16 threads
+// each owning kApplyRows/16 rows x HD/16 outputs; the Y rows and the rows' alphas are staged
+// once, the (scaled, oriented) M_n tile once per rate, with the next rate's tile loaded into
+// registers while the current one is used.
+constexpr int kApplyRows = 128;
+
 template <int HD, bool TRANS>
 __global__ void __launch_bounds__(256)
 fac_apply_kernel(const float* __restrict__ M, const float* __restrict__ w, int64_t ldw,
@@ -73,237 +77,398 @@ fac_apply_kernel(const float* __restrict__ M, const float* __restrict__ w, int64
                  int64_t nrows, const float* __restrict__ alpha, int64_t as_b, int64_t as_r,
                  int64_t as_n, int R, int H, int N, float* __restrict__ out, int64_t ldo,
                  int accumulate) {
-    constexpr int QP = HD / 4;
-    __shared__ float Ms[HD][HD + 1];
+    constexpr int RS = HD + 4;              // LDS row stride (floats)
+    constexpr int CO = HD / 16;             // outputs per thread
+    constexpr int RO = kApplyRows / 16;     // rows per thread
+    constexpr int AN = 16;                  // rates whose alphas are staged at a time
+    constexpr int ME = HD * HD / 256;       // M_n elements per thread
+    __shared__ __align__(16) float Ys[kApplyRows * RS];
+    __shared__ __align__(16) float Mt[HD * RS];
+    __shared__ float As[kApplyRows * AN];
     const int b = blockIdx.z, h = blockIdx.y;
-    const int r = blockIdx.x * 64 + threadIdx.x / 4;
-    const int part = threadIdx.x % 4;
-    const bool rok = r < R;
-    int64_t ry = -1;
-    if (rok) ry = clamp_row(yrow, (int64_t)b * R + r, nrows);
-    float y[HD];
+    const int r0 = blockIdx.x * kApplyRows;
+    const int tid = threadIdx.x;
+    const int tr = tid / 16, to = tid % 16;
+    for (int e = tid; e < kApplyRows * (HD / 4); e += 256) {
+        const int rr = e / (HD / 4), c = e % (HD / 4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r0 + rr < R) {
+            const int64_t ry = clamp_row(yrow, (int64_t)b * R + r0 + rr, nrows);
+            if (ry >= 0) v = *reinterpret_cast<const float4*>(Y + ry * ld + h * HD + 4 * c);
+        }
+        *reinterpret_cast<float4*>(Ys + rr * RS + 4 * c) = v;
+    }
+    const float* Mb = M + ((int64_t)b * H + h) * N * HD * HD;
+    float mreg[ME];
+    auto load_m = [&](int n) {
 #pragma unroll
-    for (int k = 0; k < HD; ++k) y[k] = ry >= 0 ? Y[ry * ld + h * HD + k] : 0.0f;
-    float acc[QP];
+        for (int q = 0; q < ME; ++q) {
+            const int e = tid + 256 * q;
+            float v = Mb[(int64_t)n * HD * HD + e];
+            if (w) v *= w[n * ldw + h * HD + e / HD];
+            mreg[q] = v;
+        }
+    };
+    load_m(0);
+    float acc[RO][CO];
 #pragma unroll
-    for (int o = 0; o < QP; ++o) acc[o] = 0.0f;
+    for (int a = 0; a < RO; ++a)
+#pragma unroll
+        for (int c = 0; c < CO; ++c) acc[a][c] = 0.0f;
     for (int n = 0; n < N; ++n) {
         __syncthreads();
-        const float* Mn = M + (((int64_t)b * H + h) * N + n) * HD * HD;
-        for (int e = threadIdx.x; e < HD * HD; e += 256) {
+        if (n % AN == 0) {
+            for (int e = tid; e < kApplyRows * AN; e += 256) {
+                const int rr = e / AN, nn = n + e % AN;
+                As[e] = (r0 + rr < R && nn < N)
+                            ? alpha[b * as_b + (int64_t)(r0 + rr) * as_r + nn * as_n] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < ME; ++q) {
+            const int e = tid + 256 * q;
             const int i = e / HD, j = e % HD;
-            float v = Mn[e];
-            if (w) v *= w[n * ldw + h * HD + i];
-            if (TRANS) Ms[j][i] = v;
-            else Ms[i][j] = v;
+            if (TRANS) Mt[j * RS + i] = mreg[q];
+            else Mt[i * RS + j] = mreg[q];
         }
         __syncthreads();
-        const float a = rok ? alpha[b * as_b + r * as_r + n * as_n] : 0.0f;
+        if (n + 1 < N) load_m(n + 1);
+        float sacc[RO][CO];
 #pragma unroll
-        for (int o = 0; o < QP; ++o) {
-            const float* row = Ms[part * QP + o];
-            float s = 0.0f;
+        for (int a = 0; a < RO; ++a)
 #pragma unroll
-            for (int k = 0; k < HD; ++k) s = __builtin_fmaf(row[k], y[k], s);
-            acc[o] = __builtin_fmaf(a, s, acc[o]);
+            for (int c = 0; c < CO; ++c) sacc[a][c] = 0.0f;
+#pragma unroll 2
+        for (int k0 = 0; k0 < HD; k0 += 4) {
+            float4 mv[CO];
+#pragma unroll
+            for (int c = 0; c < CO; ++c) mv[c] = *reinterpret_cast<const float4*>(Mt + (to * CO + c) * RS + k0);
+#pragma unroll
+            for (int a = 0; a < RO; ++a) {
+                const float4 yv = *reinterpret_cast<const float4*>(Ys + (tr * RO + a) * RS + k0);
+#pragma unroll
+                for (int c = 0; c < CO; ++c) {
+                    float t = sacc[a][c];
+                    t = __builtin_fmaf(yv.x, mv[c].x, t);
+                    t = __builtin_fmaf(yv.y, mv[c].y, t);
+                    t = __builtin_fmaf(yv.z, mv[c].z, t);
+                    t = __builtin_fmaf(yv.w, mv[c].w, t);
+                    sacc[a][c] = t;
+                }
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < RO; ++a) {
+            const float al = As[(tr * RO + a) * AN + n % AN];
+#pragma unroll
+            for (int c = 0; c < CO; ++c) acc[a][c] = __builtin_fmaf(al, sacc[a][c], acc[a][c]);
         }
     }
-    if (rok) {
-        float* dst = out + ((int64_t)b * R + r) * ldo + h * HD + part * QP;
 #pragma unroll
-        for (int o = 0; o < QP; ++o) dst[o] = accumulate ? dst[o] + acc[o] : acc[o];
+    for (int a = 0; a < RO; ++a) {
+        const int r = r0 + tr * RO + a;
+        if (r >= R) continue;
+        float* dst = out + ((int64_t)b * R + r) * ldo + h * HD + to * CO;
+#pragma unroll
+        for (int c = 0; c < CO; ++c) dst[c] = accumulate ? dst[c] + acc[a][c] : acc[a][c];
     }
-}
-
-// Reduction over the four lanes that hold the quarters of one row.
-__device__ inline float quad_sum(float a) {
-    a += __shfl_xor(a, 1, 64);
-    a += __shfl_xor(a, 2, 64);
-    return a;
 }
 
 __device__ inline bool tok_ok(int64_t v, int64_t V) { return v >= 0 && v < V; }
 
-// Token part of the forward: O[b,t,h,:] = sum_{s<t} A[t,s] ev_s.  Block (64 steps, h, b);
-// thread (t, quarter): q_t and o_t quarters in registers, e_k / e_v rows of step s shared
-// by the block, G[t-s] per thread.
+// ---- token pairs ---------------------------------------------------------------------------
+//
+// The four kernels share one shape.  A block of 4 waves covers 64 steps of one (b, h) on its
+// lanes (the "lane steps") and walks the 64-step blocks of the other index (the "walked
+// steps"); the 4 waves take every fourth walked step and their partial sums are added in LDS
+// at the end.  The rows of the walked step (q, dO, e_k or e_v: one row for the whole wave)
+// are read by every lane at the same address; the distance-dependent G rows differ per lane
+// and come from LDS, where each tile stages the 127 distances it needs.  Each lane holds
+// whole hd-rows in registers, so no cross-lane sums are needed per pair.
+
+constexpr int kTW = 4;  // waves per block
+
 template <int HD>
-__global__ void __launch_bounds__(256)
+struct TokLds {
+    static constexpr int RS = HD + 4;  // padded row stride (floats) of the staged rows
+    static constexpr int GROWS = 127;
+};
+
+// Stages rows [lo, lo + n) of a [rows_total, D] table (head slice h) into dst with stride RS;
+// rows outside [0, rows_total) are zero.
+template <int HD>
+__device__ inline void stage_rows(float* dst, const float* src, int64_t D, int h, int lo, int n,
+                                  int rows_total) {
+    constexpr int RS = TokLds<HD>::RS;
+    constexpr int C4 = HD / 4;
+    for (int e = threadIdx.x; e < n * C4; e += 64 * kTW) {
+        const int r = e / C4, c = e % C4;
+        const int row = lo + r;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row >= 0 && row < rows_total)
+            v = *reinterpret_cast<const float4*>(src + (int64_t)row * D + h * HD + 4 * c);
+        *reinterpret_cast<float4*>(dst + r * RS + 4 * c) = v;
+    }
+}
+
+// Same for token-indexed rows: row r is E[x[b, lo + r]] (zero outside [0, L) or for ids
+// outside [0, V)).
+template <int HD>
+__device__ inline void stage_tok_rows(float* dst, const float* E, const int64_t* xb, int64_t V,
+                                      int64_t D, int h, int lo, int n, int L) {
+    constexpr int RS = TokLds<HD>::RS;
+    constexpr int C4 = HD / 4;
+    for (int e = threadIdx.x; e < n * C4; e += 64 * kTW) {
+        const int r = e / C4, c = e % C4;
+        const int s = lo + r;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (s >= 0 && s < L) {
+            const int64_t xs = xb[s];
+            if (tok_ok(xs, V)) v = *reinterpret_cast<const float4*>(E + xs * D + h * HD + 4 * c);
+        }
+        *reinterpret_cast<float4*>(dst + r * RS + 4 * c) = v;
+    }
+}
+
+// Adds the kTW waves' per-lane rows acc[HD] in LDS (red holds (kTW-1)*64*HD floats) and
+// leaves the sum in wave 0.
+template <int HD>
+__device__ inline void reduce_waves(float (&acc)[HD], float* red) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (w > 0) {
+#pragma unroll
+        for (int k = 0; k < HD; ++k) red[((w - 1) * HD + k) * 64 + lane] = acc[k];
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+        for (int k = 0; k < HD; ++k) {
+#pragma unroll
+            for (int v = 0; v < kTW - 1; ++v) acc[k] += red[(v * HD + k) * 64 + lane];
+        }
+    }
+}
+
+template <int HD>
+constexpr int tok_lds_floats() {
+    constexpr int a = TokLds<HD>::GROWS * TokLds<HD>::RS;
+    constexpr int r = (kTW - 1) * 64 * HD;
+    return a > r ? a : r;
+}
+
+// Forward token part (lanes = steps t, walked = steps s < t):
+//   O[b,t,h,:] = sum_{s<t} (sum_i q_t[i] e_k[x_s][i] G[t-s][i]) e_v[x_s].
+template <int HD>
+__global__ void __launch_bounds__(64 * kTW)
 fac_tok_fwd_kernel(const float* __restrict__ Q, const int64_t* __restrict__ x, int64_t V,
                    const float* __restrict__ Ek, const float* __restrict__ Ev,
                    const float* __restrict__ G, int L, int H, float* __restrict__ O) {
-    constexpr int QP = HD / 4;
+    constexpr int RS = TokLds<HD>::RS;
+    __shared__ __align__(16) float lds[tok_lds_floats<HD>()];
     const int64_t D = (int64_t)H * HD;
-    const int b = blockIdx.z, h = blockIdx.y;
-    const int t = blockIdx.x * 64 + threadIdx.x / 4;
-    const int part = threadIdx.x % 4;
-    const int off = h * HD + part * QP;
+    const int b = blockIdx.z, h = blockIdx.y, tb = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = tb * 64 + lane;
     const bool tv = t < L;
-    float q[QP], o[QP];
+    const int64_t* xb = x + (int64_t)b * L;
+    float q[HD], o[HD];
 #pragma unroll
-    for (int k = 0; k < QP; ++k) {
-        q[k] = tv ? Q[((int64_t)b * L + t) * D + off + k] : 0.0f;
+    for (int k = 0; k < HD; ++k) {
+        q[k] = tv ? Q[((int64_t)b * L + t) * D + h * HD + k] : 0.0f;
         o[k] = 0.0f;
     }
-    const int t_hi = min(L, blockIdx.x * 64 + 64);  // s < t < t_hi
-    for (int s = 0; s < t_hi - 1; ++s) {
-        const int64_t xs = x[(int64_t)b * L + s];
-        if (!tok_ok(xs, V)) continue;
-        const float* ek = Ek + xs * D + off;
-        const float* ev = Ev + xs * D + off;
-        float a = 0.0f;
-        if (tv && t > s) {
-            const float* g = G + (int64_t)(t - s) * D + off;
+    for (int sb = 0; sb <= tb; ++sb) {
+        const int dlo = (tb - sb) * 64 - 63;
+        __syncthreads();
+        stage_rows<HD>(lds, G, D, h, dlo, TokLds<HD>::GROWS, L + 1);
+        __syncthreads();
+        const int s_hi = min(sb * 64 + 64, L);
+        for (int s = sb * 64 + w; s < s_hi; s += kTW) {
+            const int64_t xs = xb[s];
+            if (!tok_ok(xs, V)) continue;
+            const float* ek = Ek + xs * D + h * HD;
+            const float* ev = Ev + xs * D + h * HD;
+            const int di = t - s - dlo;
+            const bool pair = tv && t > s;
+            const float* g = lds + (pair ? di : 0) * RS;
+            float a = 0.0f;
 #pragma unroll
-            for (int k = 0; k < QP; ++k) a = __builtin_fmaf(q[k] * ek[k], g[k], a);
+            for (int k = 0; k < HD; ++k) a = __builtin_fmaf(q[k] * ek[k], g[k], a);
+            a = pair ? a : 0.0f;
+#pragma unroll
+            for (int k = 0; k < HD; ++k) o[k] = __builtin_fmaf(a, ev[k], o[k]);
         }
-        a = quad_sum(a);
-#pragma unroll
-        for (int k = 0; k < QP; ++k) o[k] = __builtin_fmaf(a, ev[k], o[k]);
     }
-    if (tv) {
+    reduce_waves<HD>(o, lds);
+    if (w == 0 && tv) {
 #pragma unroll
-        for (int k = 0; k < QP; ++k) O[((int64_t)b * L + t) * D + off + k] = o[k];
+        for (int k = 0; k < HD; ++k) O[((int64_t)b * L + t) * D + h * HD + k] = o[k];
     }
 }
 
-// Backward by rows: dQ[b,t,h,i] = sum_{s<t} dA[t,s] ek_s[i] G[t-s][i], dA = dO_t . ev_s.
+// Backward by rows (lanes = t, walked = s < t): dQ[b,t,h,:] = sum_{s<t} (dO_t . e_v[x_s])
+// e_k[x_s] ⊙ G[t-s].
 template <int HD>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * kTW)
 fac_tok_bwd_row_kernel(const float* __restrict__ dO, const int64_t* __restrict__ x, int64_t V,
                        const float* __restrict__ Ek, const float* __restrict__ Ev,
                        const float* __restrict__ G, int L, int H, float* __restrict__ dQ) {
-    constexpr int QP = HD / 4;
+    constexpr int RS = TokLds<HD>::RS;
+    __shared__ __align__(16) float lds[tok_lds_floats<HD>()];
     const int64_t D = (int64_t)H * HD;
-    const int b = blockIdx.z, h = blockIdx.y;
-    const int t = blockIdx.x * 64 + threadIdx.x / 4;
-    const int part = threadIdx.x % 4;
-    const int off = h * HD + part * QP;
+    const int b = blockIdx.z, h = blockIdx.y, tb = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = tb * 64 + lane;
     const bool tv = t < L;
-    float g_o[QP], dq[QP];
+    const int64_t* xb = x + (int64_t)b * L;
+    float go[HD], dq[HD];
 #pragma unroll
-    for (int k = 0; k < QP; ++k) {
-        g_o[k] = tv ? dO[((int64_t)b * L + t) * D + off + k] : 0.0f;
+    for (int k = 0; k < HD; ++k) {
+        go[k] = tv ? dO[((int64_t)b * L + t) * D + h * HD + k] : 0.0f;
         dq[k] = 0.0f;
     }
-    const int t_hi = min(L, blockIdx.x * 64 + 64);
-    for (int s = 0; s < t_hi - 1; ++s) {
-        const int64_t xs = x[(int64_t)b * L + s];
-        if (!tok_ok(xs, V)) continue;
-        const float* ek = Ek + xs * D + off;
-        const float* ev = Ev + xs * D + off;
-        float da = 0.0f;
+    for (int sb = 0; sb <= tb; ++sb) {
+        const int dlo = (tb - sb) * 64 - 63;
+        __syncthreads();
+        stage_rows<HD>(lds, G, D, h, dlo, TokLds<HD>::GROWS, L + 1);
+        __syncthreads();
+        const int s_hi = min(sb * 64 + 64, L);
+        for (int s = sb * 64 + w; s < s_hi; s += kTW) {
+            const int64_t xs = xb[s];
+            if (!tok_ok(xs, V)) continue;
+            const float* ek = Ek + xs * D + h * HD;
+            const float* ev = Ev + xs * D + h * HD;
+            const int di = t - s - dlo;
+            const bool pair = tv && t > s;
+            const float* g = lds + (pair ? di : 0) * RS;
+            float da = 0.0f;
 #pragma unroll
-        for (int k = 0; k < QP; ++k) da = __builtin_fmaf(g_o[k], ev[k], da);
-        da = quad_sum(da);
-        if (tv && t > s) {
-            const float* g = G + (int64_t)(t - s) * D + off;
+            for (int k = 0; k < HD; ++k) da = __builtin_fmaf(go[k], ev[k], da);
+            da = pair ? da : 0.0f;
 #pragma unroll
-            for (int k = 0; k < QP; ++k) dq[k] = __builtin_fmaf(da * ek[k], g[k], dq[k]);
+            for (int k = 0; k < HD; ++k) dq[k] = __builtin_fmaf(da * ek[k], g[k], dq[k]);
         }
     }
-    if (tv) {
+    reduce_waves<HD>(dq, lds);
+    if (w == 0 && tv) {
 #pragma unroll
-        for (int k = 0; k < QP; ++k) dQ[((int64_t)b * L + t) * D + off + k] = dq[k];
+        for (int k = 0; k < HD; ++k) dQ[((int64_t)b * L + t) * D + h * HD + k] = dq[k];
     }
 }
 
-// Backward by columns: for step s, dEk_tok[b,s,h,i] = sum_{t>s} dA[t,s] q_t[i] G[t-s][i] and
-// dEv_tok[b,s,h,j] = sum_{t>s} A[t,s] dO_t[j].
-template <int HD>
-__global__ void __launch_bounds__(256)
+// Backward by columns (lanes = s, walked = t > s).  KEY = true: dEk_tok[b,s,h,:] =
+// sum_{t>s} (dO_t . e_v[x_s]) q_t ⊙ G[t-s]; KEY = false: dEv_tok[b,s,h,:] =
+// sum_{t>s} (sum_i q_t[i] e_k[x_s][i] G[t-s][i]) dO_t.
+template <int HD, bool KEY>
+__global__ void __launch_bounds__(64 * kTW)
 fac_tok_bwd_col_kernel(const float* __restrict__ Q, const float* __restrict__ dO,
                        const int64_t* __restrict__ x, int64_t V, const float* __restrict__ Ek,
                        const float* __restrict__ Ev, const float* __restrict__ G, int L, int H,
-                       float* __restrict__ dEk, float* __restrict__ dEv) {
-    constexpr int QP = HD / 4;
+                       float* __restrict__ out) {
+    constexpr int RS = TokLds<HD>::RS;
+    __shared__ __align__(16) float lds[tok_lds_floats<HD>()];
     const int64_t D = (int64_t)H * HD;
-    const int b = blockIdx.z, h = blockIdx.y;
-    const int s = blockIdx.x * 64 + threadIdx.x / 4;
-    const int part = threadIdx.x % 4;
-    const int off = h * HD + part * QP;
+    const int b = blockIdx.z, h = blockIdx.y, sb = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int s = sb * 64 + lane;
     bool sv = s < L;
-    int64_t xs = sv ? x[(int64_t)b * L + s] : 0;
+    const int64_t xs = sv ? x[(int64_t)b * L + s] : 0;
     sv = sv && tok_ok(xs, V);
-    float ek[QP], ev[QP], dek[QP], dev[QP];
+    const float* E = KEY ? Ev : Ek;  // the row this lane keeps: e_v for dA, e_k for A
+    float e[HD], acc[HD];
 #pragma unroll
-    for (int k = 0; k < QP; ++k) {
-        ek[k] = sv ? Ek[xs * D + off + k] : 0.0f;
-        ev[k] = sv ? Ev[xs * D + off + k] : 0.0f;
-        dek[k] = dev[k] = 0.0f;
+    for (int k = 0; k < HD; ++k) {
+        e[k] = sv ? E[xs * D + h * HD + k] : 0.0f;
+        acc[k] = 0.0f;
     }
-    for (int t = blockIdx.x * 64 + 1; t < L; ++t) {
-        const float* q = Q + ((int64_t)b * L + t) * D + off;
-        const float* go = dO + ((int64_t)b * L + t) * D + off;
-        const bool pair = sv && t > s;
-        float gv[QP];
-        const float* g = G + (int64_t)(pair ? t - s : 0) * D + off;
+    const int nb = (L + 63) / 64;
+    for (int tb = sb; tb < nb; ++tb) {
+        const int dlo = (tb - sb) * 64 - 63;
+        __syncthreads();
+        stage_rows<HD>(lds, G, D, h, dlo, TokLds<HD>::GROWS, L + 1);
+        __syncthreads();
+        const int t_hi = min(tb * 64 + 64, L);
+        for (int t = tb * 64 + w; t < t_hi; t += kTW) {
+            const float* q = Q + ((int64_t)b * L + t) * D + h * HD;
+            const float* go = dO + ((int64_t)b * L + t) * D + h * HD;
+            const int di = t - s - dlo;
+            const bool pair = sv && t > s;
+            const float* g = lds + (pair ? di : 0) * RS;
+            if (KEY) {
+                float da = 0.0f;
 #pragma unroll
-        for (int k = 0; k < QP; ++k) gv[k] = pair ? g[k] : 0.0f;
-        float a = 0.0f, da = 0.0f;
+                for (int k = 0; k < HD; ++k) da = __builtin_fmaf(go[k], e[k], da);
+                da = pair ? da : 0.0f;
 #pragma unroll
-        for (int k = 0; k < QP; ++k) {
-            a = __builtin_fmaf(q[k] * ek[k], gv[k], a);
-            da = __builtin_fmaf(go[k], ev[k], da);
-        }
-        a = quad_sum(a);
-        da = quad_sum(da);
-        if (pair) {
+                for (int k = 0; k < HD; ++k) acc[k] = __builtin_fmaf(da * q[k], g[k], acc[k]);
+            } else {
+                float a = 0.0f;
 #pragma unroll
-            for (int k = 0; k < QP; ++k) {
-                dev[k] = __builtin_fmaf(a, go[k], dev[k]);
-                dek[k] = __builtin_fmaf(da * q[k], gv[k], dek[k]);
+                for (int k = 0; k < HD; ++k) a = __builtin_fmaf(q[k] * e[k], g[k], a);
+                a = pair ? a : 0.0f;
+#pragma unroll
+                for (int k = 0; k < HD; ++k) acc[k] = __builtin_fmaf(a, go[k], acc[k]);
             }
         }
     }
-    if (s < L) {
+    reduce_waves<HD>(acc, lds);
+    if (w == 0 && s < L) {
 #pragma unroll
-        for (int k = 0; k < QP; ++k) {
-            dEk[((int64_t)b * L + s) * D + off + k] = dek[k];
-            dEv[((int64_t)b * L + s) * D + off + k] = dev[k];
-        }
+        for (int k = 0; k < HD; ++k) out[((int64_t)b * L + s) * D + h * HD + k] = acc[k];
     }
 }
 
-// Backward by diagonals: dGb[b,d,h,i] = sum_t dA[t,t-d] q_t[i] ek_{t-d}[i] for d in [1, L);
-// row 0 is zero.  Thread (d, quarter); each thread gathers its own e_k / e_v rows.
+// Backward by diagonals (lanes = distances d, walked = t): dGb[b,d,h,:] =
+// sum_t (dO_t . e_v[x_{t-d}]) q_t ⊙ e_k[x_{t-d}] for d in [1, L); row 0 is zero.  The e_k /
+// e_v rows of the 127 steps t - d a tile needs are staged in LDS.
 template <int HD>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * kTW)
 fac_tok_bwd_diag_kernel(const float* __restrict__ Q, const float* __restrict__ dO,
                         const int64_t* __restrict__ x, int64_t V, const float* __restrict__ Ek,
                         const float* __restrict__ Ev, int L, int H, float* __restrict__ dGb) {
-    constexpr int QP = HD / 4;
+    constexpr int RS = TokLds<HD>::RS;
+    constexpr int GR = TokLds<HD>::GROWS;
+    constexpr int NF = 2 * GR * RS > (kTW - 1) * 64 * HD ? 2 * GR * RS : (kTW - 1) * 64 * HD;
+    __shared__ __align__(16) float lds[NF];
+    float* sk = lds;
+    float* sv = lds + GR * RS;
     const int64_t D = (int64_t)H * HD;
-    const int b = blockIdx.z, h = blockIdx.y;
-    const int d = blockIdx.x * 64 + threadIdx.x / 4;
-    const int part = threadIdx.x % 4;
-    const int off = h * HD + part * QP;
-    float dg[QP];
+    const int b = blockIdx.z, h = blockIdx.y, db = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int d = db * 64 + lane;
+    const bool dv = d >= 1 && d < L;
+    const int64_t* xb = x + (int64_t)b * L;
+    float dg[HD];
 #pragma unroll
-    for (int k = 0; k < QP; ++k) dg[k] = 0.0f;
-    for (int t = blockIdx.x * 64; t < L; ++t) {
-        const int s = t - d;
-        const bool pair = d >= 1 && d < L && s >= 0;
-        int64_t xs = pair ? x[(int64_t)b * L + s] : 0;
-        const bool ok = pair && tok_ok(xs, V);
-        const float* q = Q + ((int64_t)b * L + t) * D + off;
-        const float* go = dO + ((int64_t)b * L + t) * D + off;
-        float ek[QP], ev[QP];
+    for (int k = 0; k < HD; ++k) dg[k] = 0.0f;
+    const int nb = (L + 63) / 64;
+    for (int tb = db; tb < nb; ++tb) {
+        const int slo = tb * 64 - db * 64 - 63;  // s = t - d spans [slo, slo + 126]
+        __syncthreads();
+        stage_tok_rows<HD>(sk, Ek, xb, V, D, h, slo, GR, L);
+        stage_tok_rows<HD>(sv, Ev, xb, V, D, h, slo, GR, L);
+        __syncthreads();
+        const int t_hi = min(tb * 64 + 64, L);
+        for (int t = tb * 64 + w; t < t_hi; t += kTW) {
+            const float* q = Q + ((int64_t)b * L + t) * D + h * HD;
+            const float* go = dO + ((int64_t)b * L + t) * D + h * HD;
+            const int si = t - d - slo;
+            const bool pair = dv && t - d >= 0;
+            const float* ekr = sk + (pair ? si : 0) * RS;
+            const float* evr = sv + (pair ? si : 0) * RS;
+            float da = 0.0f;
 #pragma unroll
-        for (int k = 0; k < QP; ++k) {
-            ek[k] = ok ? Ek[xs * D + off + k] : 0.0f;
-            ev[k] = ok ? Ev[xs * D + off + k] : 0.0f;
+            for (int k = 0; k < HD; ++k) da = __builtin_fmaf(go[k], evr[k], da);
+            da = pair ? da : 0.0f;
+#pragma unroll
+            for (int k = 0; k < HD; ++k) dg[k] = __builtin_fmaf(da * q[k], ekr[k], dg[k]);
         }
-        float da = 0.0f;
-#pragma unroll
-        for (int k = 0; k < QP; ++k) da = __builtin_fmaf(go[k], ev[k], da);
-        da = quad_sum(da);
-#pragma unroll
-        for (int k = 0; k < QP; ++k) dg[k] = __builtin_fmaf(da * q[k], ek[k], dg[k]);
     }
-    if (d < L) {
+    reduce_waves<HD>(dg, lds);
+    if (w == 0 && d < L) {
 #pragma unroll
-        for (int k = 0; k < QP; ++k) dGb[((int64_t)b * L + d) * D + off + k] = d >= 1 ? dg[k] : 0.0f;
+        for (int k = 0; k < HD; ++k) dGb[((int64_t)b * L + d) * D + h * HD + k] = dv ? dg[k] : 0.0f;
     }
 }
 
@@ -353,7 +518,7 @@ extern "C" int mb_factored_apply(const float* M, const float* w, int64_t ldw, co
     if (B == 0 || R == 0) return MB_OK;
     MB_REQUIRE(M && Y && alpha && out, "mb_factored_apply: null pointer argument");
     hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((R + 63) / 64, H, B), blk(256);
+    const dim3 grid((R + kApplyRows - 1) / kApplyRows, H, B), blk(256);
 #define MB_FAC_APPLY(HDV, TR)                                                                     \
     hipLaunchKernelGGL((fac_apply_kernel<HDV, TR>), grid, blk, 0, st, M, w, ldw, Y, yrow, ld, nrows, \
                        alpha, as_b, as_r, as_n, R, H, N, out, ldo, accumulate)
@@ -374,7 +539,7 @@ extern "C" int mb_factored_tok_fwd(const float* Q, const int64_t* x, int64_t V, 
     if (B == 0 || L == 0) return MB_OK;
     MB_REQUIRE(Q && x && E_k && E_v && G && O, "mb_factored_tok_fwd: null pointer argument");
     hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((L + 63) / 64, H, B), blk(256);
+    const dim3 grid((L + 63) / 64, H, B), blk(64 * kTW);
     if (hd == 64)
         hipLaunchKernelGGL(fac_tok_fwd_kernel<64>, grid, blk, 0, st, Q, x, V, E_k, E_v, G, L, H, O);
     else
@@ -392,19 +557,20 @@ extern "C" int mb_factored_tok_bwd(const float* Q, const float* dO, const int64_
     MB_REQUIRE(Q && dO && x && E_k && E_v && G && dQ && dEk_tok && dEv_tok && dG_b,
                "mb_factored_tok_bwd: null pointer argument");
     hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((L + 63) / 64, H, B), blk(256);
-    if (hd == 64) {
-        hipLaunchKernelGGL(fac_tok_bwd_row_kernel<64>, grid, blk, 0, st, dO, x, V, E_k, E_v, G, L, H, dQ);
-        hipLaunchKernelGGL(fac_tok_bwd_col_kernel<64>, grid, blk, 0, st, Q, dO, x, V, E_k, E_v, G, L,
-                           H, dEk_tok, dEv_tok);
-        hipLaunchKernelGGL(fac_tok_bwd_diag_kernel<64>, grid, blk, 0, st, Q, dO, x, V, E_k, E_v, L, H,
-                           dG_b);
-    } else {
-        hipLaunchKernelGGL(fac_tok_bwd_row_kernel<32>, grid, blk, 0, st, dO, x, V, E_k, E_v, G, L, H, dQ);
-        hipLaunchKernelGGL(fac_tok_bwd_col_kernel<32>, grid, blk, 0, st, Q, dO, x, V, E_k, E_v, G, L,
-                           H, dEk_tok, dEv_tok);
-        hipLaunchKernelGGL(fac_tok_bwd_diag_kernel<32>, grid, blk, 0, st, Q, dO, x, V, E_k, E_v, L, H,
-                           dG_b);
-    }
+    const dim3 grid((L + 63) / 64, H, B), blk(64 * kTW);
+#define MB_FAC_BWD(HDV)                                                                           \
+    do {                                                                                          \
+        hipLaunchKernelGGL(fac_tok_bwd_row_kernel<HDV>, grid, blk, 0, st, dO, x, V, E_k, E_v, G, L, \
+                           H, dQ);                                                                \
+        hipLaunchKernelGGL((fac_tok_bwd_col_kernel<HDV, true>), grid, blk, 0, st, Q, dO, x, V, E_k, \
+                           E_v, G, L, H, dEk_tok);                                                \
+        hipLaunchKernelGGL((fac_tok_bwd_col_kernel<HDV, false>), grid, blk, 0, st, Q, dO, x, V,     \
+                           E_k, E_v, G, L, H, dEv_tok);                                           \
+        hipLaunchKernelGGL(fac_tok_bwd_diag_kernel<HDV>, grid, blk, 0, st, Q, dO, x, V, E_k, E_v, L, \
+                           H, dG_b);                                                              \
+    } while (0)
+    if (hd == 64) MB_FAC_BWD(64);
+    else MB_FAC_BWD(32);
+#undef MB_FAC_BWD
     return check_launch("mb_factored_tok_bwd");
 }
