@@ -70,3 +70,37 @@ def test_cpu_tensors_are_rejected():
     from mathbrain_amd.ema_query import compute_query_ema_history
     with pytest.raises(NotImplementedError, match="no CPU path"):
         compute_query_ema_history(torch.zeros(1, 4, dtype=torch.long), torch.ones(2), 10)
+
+
+def test_data_and_factored_argument_errors_need_no_gpu(lib):
+    """The data-pipeline and factored entry points check sizes and workspace on the host."""
+    from mathbrain_amd import _lib
+    L = _lib.lib()
+    assert L.mb_corpus_states_workspace(0, 64) == 0
+    assert L.mb_corpus_states_workspace(1024, 64) == 1024 // 1024 * 64 * 3 * 4
+    rc = L.mb_corpus_states(None, None, 10, None, 200, None, None, 0, None)
+    assert rc == _lib.MB_ERR_INVALID_ARGUMENT and b"N=200" in L.mb_last_error()
+    rc = L.mb_corpus_states(1, 1, 10, 1, 4, 1, None, 0, None)   # no workspace
+    assert rc == _lib.MB_ERR_WORKSPACE and b"workspace" in L.mb_last_error()
+    assert L.mb_corpus_states(None, None, 0, None, 4, None, None, 0, None) == 0
+    rc = L.mb_slot_lists(None, None, 10, 0, None, None, None, 2, None, None, None, None, None)
+    assert rc == _lib.MB_ERR_INVALID_ARGUMENT and b"V=0" in L.mb_last_error()
+    assert L.mb_slot_lists(None, None, 10, 5, None, None, None, 0, None, None, None, None, None) == 0
+    rc = L.mb_slot_batch(None, None, None, None, 0, 10, 5, None, None, None, 1, None, None, None,
+                         None, 4, 4, None, None, None, None, None, None, None)
+    assert rc == _lib.MB_ERR_INVALID_ARGUMENT and b"N=0" in L.mb_last_error()
+    rc = L.mb_factored_tok_fwd(None, None, 10, None, None, None, 1, 4, 2, 48, None, None)
+    assert rc == _lib.MB_ERR_UNSUPPORTED and b"head_dim=48" in L.mb_last_error()
+    rc = L.mb_factored_outer(None, None, None, None, 64, 10, None, 0, 0, 0, 1, 4, 2, 4, 64, None, None)
+    assert rc == _lib.MB_ERR_INVALID_ARGUMENT and b"row stride" in L.mb_last_error()
+    rc = L.mb_factored_apply(None, None, 0, None, None, 128, 10, None, 0, 0, 0, 1, 4, 2, 4, 16, 0,
+                             None, 128, 0, None)
+    assert rc == _lib.MB_ERR_UNSUPPORTED and b"head_dim=16" in L.mb_last_error()
+
+
+def test_factored_and_data_cpu_tensors_are_rejected():
+    import torch
+    from mathbrain_amd.factored_ema import factored_ema_forward
+    with pytest.raises(NotImplementedError, match="no CPU path"):
+        factored_ema_forward(torch.zeros(1, 4, 8), torch.zeros(1, 4, dtype=torch.long),
+                             torch.zeros(5, 8), torch.zeros(5, 8), torch.ones(2), torch.zeros(2, 8), 2)
