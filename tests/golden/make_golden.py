@@ -9,6 +9,10 @@
 * attention_small.npz -- a seeded flash-EMA case (absent-slot mass, SiLU gate) with the
   exact float64 oracle's O, LSE and the reference-formula gradients for a seeded dO
   (stored as float32).
+* data_small.npz -- a six-document corpus (one of length 1, one of length 2) with the
+  oracle's states, chunk list (block 7) and one collated batch of six chunks.
+* factored_small.npz -- a seeded factored linear EMA case with c_base and padding slots,
+  with the float64 step-by-step oracle's output and gradients for a seeded dO.
 
 The outputs come from this repository's oracle (oracle/), never from the reference; the
 fixtures pin the oracle against regressions and give the GPU tests fixed expected values.
@@ -93,11 +97,55 @@ def attention_case():
                 O=t(O), LSE=t(LSE), dQ=t(dQ), dE_k=t(dEk), dE_v=t(dEv), dW=t(dW))
 
 
+def data_case():
+    from oracle import data as od
+    rng = np.random.default_rng(31)
+    lens = [60, 2, 1, 95, 40, 102]
+    tokens = np.concatenate([rng.integers(0, 40, n) for n in lens]).astype(np.int32)
+    doc_ids = np.repeat(np.arange(len(lens), dtype=np.int32), lens)
+    rhos = od.rhos_for(6, 1.0, 128.0)
+    states, pos = od.corpus_states(tokens, doc_ids, rhos)
+    chunks, starts = od.chunk_index(doc_ids, 7)
+    idx = np.array([0, 5, len(chunks) - 1, 9, 20, 31], np.int64)
+    items = [od.get_item(tokens, doc_ids, states, pos, starts, chunks[i], rhos) for i in idx]
+    ch, us, pm, inv, cb, K, dd = od.collate(items)
+    return dict(tokens=tokens, doc_ids=doc_ids, rhos=rhos, block=np.array(7), states=states,
+                chunks_index=np.array(chunks, np.int64), batch=idx, chunks=ch, unique_slots=us,
+                pad_mask=pm, inverse=inv, c_base=cb, K_max=np.array(K), doc_out=dd)
+
+
+def factored_case():
+    from oracle import factored as of
+    g = torch.Generator().manual_seed(41)
+    B, L, V, H, hd, N, K = 2, 40, 30, 2, 32, 6, 8
+    D = H * hd
+    f = torch.float64
+    Q = torch.randn(B, L, D, generator=g, dtype=f)
+    x = torch.randint(0, V, (B, L), generator=g)
+    Ek = torch.randn(V, D, generator=g, dtype=f) * 0.5
+    Ev = torch.randn(V, D, generator=g, dtype=f) * 0.5
+    rhos = torch.exp(-math.log(2.0) / torch.logspace(0, math.log10(64.0), N, dtype=f))
+    W = torch.randn(N, D, generator=g, dtype=f) * 0.5
+    u = torch.randint(-1, V, (B, K), generator=g)
+    cb = torch.rand(B, K, N, generator=g, dtype=f) * 3
+    leaves = [t.clone().requires_grad_(True) for t in (Q, Ek, Ev, W)]
+    O = of.loop_forward(leaves[0], x, leaves[1], leaves[2], rhos, leaves[3], H, c_base=cb,
+                        unique_slots=u, pad_mask=u >= 0)
+    dO = torch.randn(B, L, D, generator=g, dtype=f)
+    O.backward(dO)
+    t = lambda v: v.detach().numpy().astype(np.float32)
+    return dict(Q=t(Q), x=x.numpy(), E_k=t(Ek), E_v=t(Ev), rhos=t(rhos), W=t(W), unique=u.numpy(),
+                c_base=t(cb), H=np.array(H), dO=t(dO), O=t(O), dQ=t(leaves[0].grad),
+                dE_k=t(leaves[1].grad), dE_v=t(leaves[2].grad), dW=t(leaves[3].grad))
+
+
 def main():
     with open(os.path.join(HERE, "reference_kats.json"), "w") as fh:
         json.dump(kats(), fh, indent=1)
     np.savez_compressed(os.path.join(HERE, "scan_small.npz"), **scan_case())
     np.savez_compressed(os.path.join(HERE, "attention_small.npz"), **attention_case())
+    np.savez_compressed(os.path.join(HERE, "data_small.npz"), **data_case())
+    np.savez_compressed(os.path.join(HERE, "factored_small.npz"), **factored_case())
     print("wrote", sorted(f for f in os.listdir(HERE) if not f.endswith(".py")))
 
 

@@ -1,6 +1,7 @@
 """The oracle against the committed fixtures of tests/golden/ (written by
-tests/golden/make_golden.py): the reference's own scan known answers, and seeded scan and
-attention cases whose expected outputs pin the oracle against regressions."""
+tests/golden/make_golden.py): the reference's own scan known answers, and seeded scan,
+attention, data-pipeline and factored cases whose expected outputs pin the oracle against
+regressions."""
 import json
 import os
 
@@ -62,3 +63,34 @@ def test_oracle_reproduces_attention_fixture():
                                          f["dO"].to(d), f["c_base"].to(d))
     for name, g in zip(("dQ", "dE_k", "dE_v", "dW"), grads):
         assert _normwise(g, f[name]) < 1e-6, name
+
+
+def test_oracle_reproduces_data_fixture():
+    from oracle import data as od
+    f = np.load(os.path.join(GOLD, "data_small.npz"))
+    states, pos = od.corpus_states(f["tokens"], f["doc_ids"], f["rhos"])
+    np.testing.assert_allclose(states, f["states"], rtol=1e-6, atol=1e-30)
+    chunks, starts = od.chunk_index(f["doc_ids"], int(f["block"]))
+    assert np.array_equal(np.array(chunks, np.int64), f["chunks_index"])
+    items = [od.get_item(f["tokens"], f["doc_ids"], states, pos, starts, chunks[i], f["rhos"])
+             for i in f["batch"]]
+    ch, us, pm, inv, cb, K, dd = od.collate(items)
+    for name, got in (("chunks", ch), ("unique_slots", us), ("pad_mask", pm), ("inverse", inv),
+                      ("doc_out", dd)):
+        assert np.array_equal(got, f[name]), name
+    assert K == int(f["K_max"])
+    np.testing.assert_allclose(cb, f["c_base"], rtol=1e-6, atol=1e-30)
+
+
+def test_oracle_reproduces_factored_fixture():
+    from oracle import factored as of
+    f = {k: torch.from_numpy(v) for k, v in np.load(os.path.join(GOLD, "factored_small.npz")).items()}
+    d = torch.float64
+    leaves = [f[k].to(d).requires_grad_(True) for k in ("Q", "E_k", "E_v", "W")]
+    O = of.closed_form(leaves[0], f["x"], leaves[1], leaves[2], f["rhos"].to(d), leaves[3],
+                       int(f["H"]), c_base=f["c_base"].to(d), unique_slots=f["unique"],
+                       pad_mask=f["unique"] >= 0)
+    O.backward(f["dO"].to(d))
+    assert _normwise(O, f["O"]) < 1e-6
+    for name, leaf in zip(("dQ", "dE_k", "dE_v", "dW"), leaves):
+        assert _normwise(leaf.grad, f[name]) < 1e-6, name
