@@ -75,7 +75,7 @@ def next_occurrence(tokens, srt=None, order=None):
 def chain_order(tokens, doc_ids):
     """(sorted keys, positions) of a stable sort by (document segment, token): the chains
     of one token inside one document that the state scan walks."""
-    key = (_segments(doc_ids).to(torch.int64) << 32) | tokens.to(torch.int64)
+    key = (_segments(doc_ids).to(torch.int64) << 32) | (tokens.to(torch.int64) & 0xFFFFFFFF)
     return torch.sort(key, stable=True)
 
 

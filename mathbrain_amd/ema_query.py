@@ -1,7 +1,8 @@
 """Query-side EMA history: the per-position counter rows C_seq that gate the queries.
 
-Drop-in for mathbrain/triton_ema_query.py:120-169 (``compute_query_ema_history``);
-the work runs in the gfx950 kernel behind ``mb_ema_query_scan``.
+Drop-in for mathbrain/triton_ema_query.py:120-169 (``compute_query_ema_history``) and
+:67-117 (``compute_query_ema_history_pt``, the same scan under the reference's second
+name); the work runs in the gfx950 kernel behind ``mb_ema_query_scan``.
 """
 import torch
 
@@ -59,3 +60,10 @@ def compute_query_ema_history(x, rhos, vocab_size, c_init=None, c_init_keys=None
     if return_state:
         return C_seq, state, stamps
     return C_seq
+
+
+def compute_query_ema_history_pt(x, rhos, vocab_size, c_init=None, c_init_keys=None, doc_ids=None):
+    """The reference's second name for the same scan (triton_ema_query.py:67-117, its
+    PyTorch loop).  Same semantics and arguments; here it runs the same HIP kernel as
+    ``compute_query_ema_history`` and, like it, needs GPU tensors (there is no CPU path)."""
+    return compute_query_ema_history(x, rhos, vocab_size, c_init, c_init_keys, doc_ids)
