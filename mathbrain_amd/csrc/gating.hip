@@ -65,30 +65,43 @@ __device__ inline float wave_sum(float v) {
 
 // Gate pre-activation of rows r0 .. r0 + kGateRows - 1 at column col.  `cst` holds
 // (C_seq + 1) transposed, [N][kGateRows], for the folded projection.
-template <bool FUSED>
-__device__ inline void gate_pre(const GateArgs& a, int64_t r0, int nr, int col, const float* cst,
-                                float (&pre)[kGateRows]) {
+// Pre-activations of all CPT columns of this thread for the tile's rows, one pass over the
+// rates: each rate's eight staged counts are read once for all columns.
+template <bool FUSED, int CPT>
+__device__ inline void gate_pre_all(const GateArgs& a, int64_t r0, int nr, int tid, const float* cst,
+                                    float (&pre)[CPT][kGateRows]) {
     if (FUSED) {
 #pragma unroll
-        for (int r = 0; r < kGateRows; ++r) pre[r] = 0.f;
+        for (int j = 0; j < CPT; ++j)
+#pragma unroll
+            for (int r = 0; r < kGateRows; ++r) pre[j][r] = 0.f;
+#pragma unroll 8
         for (int n = 0; n < a.N; ++n) {
-            const float w = a.W[(int64_t)n * a.D + col];
             const float4 c0 = *reinterpret_cast<const float4*>(cst + n * kGateRows);
             const float4 c1 = *reinterpret_cast<const float4*>(cst + n * kGateRows + 4);
-            pre[0] = __builtin_fmaf(c0.x, w, pre[0]);
-            pre[1] = __builtin_fmaf(c0.y, w, pre[1]);
-            pre[2] = __builtin_fmaf(c0.z, w, pre[2]);
-            pre[3] = __builtin_fmaf(c0.w, w, pre[3]);
-            pre[4] = __builtin_fmaf(c1.x, w, pre[4]);
-            pre[5] = __builtin_fmaf(c1.y, w, pre[5]);
-            pre[6] = __builtin_fmaf(c1.z, w, pre[6]);
-            pre[7] = __builtin_fmaf(c1.w, w, pre[7]);
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) {
+                const int col = tid + j * kGateThreads;
+                const float w = col < a.D ? a.W[(int64_t)n * a.D + col] : 0.f;
+                pre[j][0] = __builtin_fmaf(c0.x, w, pre[j][0]);
+                pre[j][1] = __builtin_fmaf(c0.y, w, pre[j][1]);
+                pre[j][2] = __builtin_fmaf(c0.z, w, pre[j][2]);
+                pre[j][3] = __builtin_fmaf(c0.w, w, pre[j][3]);
+                pre[j][4] = __builtin_fmaf(c1.x, w, pre[j][4]);
+                pre[j][5] = __builtin_fmaf(c1.y, w, pre[j][5]);
+                pre[j][6] = __builtin_fmaf(c1.z, w, pre[j][6]);
+                pre[j][7] = __builtin_fmaf(c1.w, w, pre[j][7]);
+            }
         }
     } else {
-        const float bv = a.bias[col];
 #pragma unroll
-        for (int r = 0; r < kGateRows; ++r)
-            pre[r] = r < nr ? a.pp[(r0 + r) * a.pp_sr + col] + bv : 0.f;
+        for (int j = 0; j < CPT; ++j) {
+            const int col = tid + j * kGateThreads;
+            const float bv = col < a.D ? a.bias[col] : 0.f;
+#pragma unroll
+            for (int r = 0; r < kGateRows; ++r)
+                pre[j][r] = (r < nr && col < a.D) ? a.pp[(r0 + r) * a.pp_sr + col] + bv : 0.f;
+        }
     }
 }
 
@@ -121,16 +134,16 @@ gating_fwd_kernel(GateArgs a) {
             stage_counts(a, r0, nr, cst);
             __syncthreads();
         }
+        float pre[CPT][kGateRows];
+        gate_pre_all<FUSED, CPT>(a, r0, nr, tid, cst, pre);
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int col = tid + j * kGateThreads;
             if (col >= a.D) break;
-            float pre[kGateRows];
-            gate_pre<FUSED>(a, r0, nr, col, cst, pre);
 #pragma unroll
             for (int r = 0; r < kGateRows; ++r) {
                 if (r >= nr) break;
-                const float g = SILU ? pre[r] * sigmoidf_(pre[r]) : pre[r];
+                const float g = SILU ? pre[j][r] * sigmoidf_(pre[j][r]) : pre[j][r];
                 xe[r * a.D + col] = a.xq[(r0 + r) * a.xq_sr + col] * g;
             }
         }
@@ -190,12 +203,13 @@ gating_bwd_kernel(GateArgs a) {
             __syncthreads();
         }
         float gv[CPT][kGateRows], ds[CPT][kGateRows];
+        float pre_all[CPT][kGateRows];
+        gate_pre_all<FUSED, CPT>(a, r0, nr, tid, cst, pre_all);
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int col = tid + j * kGateThreads;
             if (col >= a.D) break;
-            float pre[kGateRows];
-            gate_pre<FUSED>(a, r0, nr, col, cst, pre);
+            const float* pre = pre_all[j];
             const float w = a.lnw[col];
 #pragma unroll
             for (int r = 0; r < kGateRows; ++r) {
