@@ -95,8 +95,11 @@ class FactoredEMAFunction(torch.autograd.Function):
             dW = (P[:, :L] @ dGb.sum(0).to(torch.float64)).to(f32)
             dE_k = torch.zeros(V, D, dtype=f32, device=dev)
             dE_v = torch.zeros(V, D, dtype=f32, device=dev)
-            dE_k.index_add_(0, xx.reshape(-1), dEk_t.view(-1, D))
-            dE_v.index_add_(0, xx.reshape(-1), dEv_t.view(-1, D))
+            # ids outside [0, V) were skipped by the kernels (their rows are zero): clamped
+            # here only so that index_add_ stays in range
+            tok_rows = xx.reshape(-1).clamp(0, V - 1)
+            dE_k.index_add_(0, tok_rows, dEk_t.view(-1, D))
+            dE_v.index_add_(0, tok_rows, dEv_t.view(-1, D))
             if S is not None:
                 K = u.shape[1]
                 _lib.call("mb_factored_apply", p(S), p(W), D, p(g), None, D, B * L, p(R), 0, N, 1,
@@ -111,7 +114,7 @@ class FactoredEMAFunction(torch.autograd.Function):
                           B, K, H, N, hd, 0, p(dk_u), D, 0, st)
                 _lib.call("mb_factored_apply", p(M), p(W), D, p(Ek), p(u), D, V, p(c), K * N, N, 1,
                           B, K, H, N, hd, 1, p(dv_u), D, 0, st)
-                rows = u.clamp(min=0).reshape(-1)
+                rows = u.clamp(0, V - 1).reshape(-1)
                 dE_k.index_add_(0, rows, dk_u.view(-1, D))
                 dE_v.index_add_(0, rows, dv_u.view(-1, D))
         qd, kd, vd, wd = ctx.in_dtypes
@@ -125,7 +128,8 @@ def factored_ema_forward(Q, x, E_k_slots, E_v_slots, rhos, W_pe, n_heads,
     Q [B, L, D] (already projected), x [B, L] token ids, E_k_slots / E_v_slots [V, D],
     rhos [N], W_pe [N, D] (pe_proj.weight.t()), c_base [B, K, N] with unique_slots [B, K]
     (-1 = padding, read as row 0 as the reference's clamp does) and pad_mask [B, K].
-    Returns [B, L, D].
+    Returns [B, L, D].  Token ids outside [0, V) contribute nothing (the reference's
+    indexing would raise; checking here would cost a device-to-host sync per call).
     """
     if Q.device.type != "cuda":
         raise NotImplementedError("factored_ema_forward: tensors must be on an MI355X GPU; "
