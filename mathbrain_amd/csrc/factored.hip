@@ -16,7 +16,7 @@
 // c_base part of o, of dQ and of the slot gradients), and the three token-pair kernels
 // (forward; backward by rows for dQ, by columns for the token embedding gradients, by
 // diagonals for dG[d], from which dW_pe = P dG with P[n,d] = rho_n^d).
-#include "common.h"
+#include "flash_common.h"
 
 namespace mb {
 namespace {
@@ -172,6 +172,203 @@ fac_apply_kernel(const float* __restrict__ M, const float* __restrict__ w, int64
 #pragma unroll
         for (int c = 0; c < CO; ++c) dst[c] = accumulate ? dst[c] + acc[a][c] : acc[a][c];
     }
+}
+
+// ---- MFMA forms of the state kernels (hd = 64) ------------------------------------------
+//
+// The state contractions are plain GEMMs per rate.  These forms run them on the bf16 matrix
+// cores with every fp32 operand split into bf16 hi + lo parts and three products
+// (hi*hi + hi*lo + lo*hi, fp32 accumulation), which keeps about 2^-16 relative error per
+// product.  Operand layout of v_mfma_f32_16x16x16_bf16: A[row = lane%16][k = 4 (lane/16) + e],
+// B[k = 4 (lane/16) + e][col = lane%16], D[row = 4 (lane/16) + i][col = lane%16].
+
+__device__ inline void split_bf16x4(const float (&v)[4], bf16x4& hi, bf16x4& lo) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const __bf16 t = (__bf16)v[e];
+        hi[e] = t;
+        lo[e] = (__bf16)(v[e] - (float)t);
+    }
+}
+
+__device__ inline f32x4 mfma3(bf16x4 ah, bf16x4 al, bf16x4 bh, bf16x4 bl, f32x4 c) {
+    c = mfma16x16x16(ah, bh, c);
+    c = mfma16x16x16(ah, bl, c);
+    return mfma16x16x16(al, bh, c);
+}
+
+// fac_apply_kernel for hd = 64: block (64 rows, h, b); wave w owns outputs [16w, 16w + 16)
+// of the 64 rows (4 row tiles); the Y rows are split once, each rate's M_n tile per rate.
+template <bool TRANS>
+__global__ void __launch_bounds__(256)
+fac_apply_mfma_kernel(const float* __restrict__ M, const float* __restrict__ w, int64_t ldw,
+                      const float* __restrict__ Y, const int64_t* __restrict__ yrow, int64_t ld,
+                      int64_t nrows, const float* __restrict__ alpha, int64_t as_b, int64_t as_r,
+                      int64_t as_n, int R, int H, int N, float* __restrict__ out, int64_t ldo,
+                      int accumulate) {
+    constexpr int HD = 64;
+    constexpr int AN = 64;
+    __shared__ float As[64 * AN];
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int r0 = blockIdx.x * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int c16 = lane & 15, g = lane >> 4;
+    bf16x4 ahi[4][4], alo[4][4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+        const int r = r0 + 16 * rt + c16;
+        const int64_t ry = r < R ? clamp_row(yrow, (int64_t)b * R + r, nrows) : -1;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (ry >= 0) {
+                const float4 q = *reinterpret_cast<const float4*>(Y + ry * ld + h * HD + 16 * kt + 4 * g);
+                v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+            }
+            split_bf16x4(v, ahi[rt][kt], alo[rt][kt]);
+        }
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int o = 16 * wv + c16;
+    const float* Mb = M + ((int64_t)b * H + h) * N * HD * HD;
+    for (int n = 0; n < N; ++n) {
+        if (n % AN == 0) {
+            __syncthreads();
+            for (int e = tid; e < 64 * AN; e += 256) {
+                const int rr = e / AN, nn = n + e % AN;
+                As[e] = (r0 + rr < R && nn < N)
+                            ? alpha[b * as_b + (int64_t)(r0 + rr) * as_r + nn * as_n] : 0.0f;
+            }
+            __syncthreads();
+        }
+        const float* Mn = Mb + (int64_t)n * HD * HD;
+        bf16x4 bhi[4], blo[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            float v[4];
+            if (!TRANS) {  // B[k][o] = w[n, o] M_n[o][k]
+                const float4 q = *reinterpret_cast<const float4*>(Mn + o * HD + 16 * kt + 4 * g);
+                const float ws = w ? w[n * ldw + h * HD + o] : 1.0f;
+                v[0] = q.x * ws; v[1] = q.y * ws; v[2] = q.z * ws; v[3] = q.w * ws;
+            } else {       // B[k][o] = w[n, k] M_n[k][o]
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int k = 16 * kt + 4 * g + e;
+                    v[e] = Mn[k * HD + o] * (w ? w[n * ldw + h * HD + k] : 1.0f);
+                }
+            }
+            split_bf16x4(v, bhi[kt], blo[kt]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) sacc = mfma3(ahi[rt][kt], alo[rt][kt], bhi[kt], blo[kt], sacc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[rt][i] = __builtin_fmaf(As[(16 * rt + 4 * g + i) * AN + n % AN], sacc[i], acc[rt][i]);
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = r0 + 16 * rt + 4 * g + i;
+            if (r >= R) continue;
+            float* dst = out + ((int64_t)b * R + r) * ldo + h * HD + o;
+            *dst = accumulate ? *dst + acc[rt][i] : acc[rt][i];
+        }
+}
+
+// fac_outer_kernel for hd = 64: block (4 rates, h, b), wave w = rate 4 blockIdx.x + w, the
+// whole 64 x 64 output of its rate in 16 tiles.  The walked rows come in blocks of 32 (two
+// MFMA k steps), staged in LDS once for the four rates: they share the X and Y rows and
+// differ only in the weights alpha.
+constexpr int kOuterRows = 32;
+
+__global__ void __launch_bounds__(256)
+fac_outer_mfma_kernel(const float* __restrict__ X, const int64_t* __restrict__ xrow,
+                      const float* __restrict__ Y, const int64_t* __restrict__ yrow, int64_t ld,
+                      int64_t nrows, const float* __restrict__ alpha, int64_t as_b, int64_t as_r,
+                      int64_t as_n, int R, int H, int N, float* __restrict__ out) {
+    constexpr int HD = 64;
+    constexpr int RS = HD + 4;
+    __shared__ __align__(16) float Xs[kOuterRows * RS];
+    __shared__ __align__(16) float Ys[kOuterRows * RS];
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int n = blockIdx.x * 4 + (tid >> 6);
+    const int c16 = lane & 15, g = lane >> 4;
+    const bool nv = n < N;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) acc[it][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < R; k0 += kOuterRows) {
+        __syncthreads();
+        // stage the block's rows: thread tid copies float4 (tid % 16) of row tid / 16 of X
+        // and of Y (rows of zero weight for every rate are staged as zeros)
+        for (int e = tid; e < kOuterRows * (HD / 4); e += 256) {
+            const int rr = e / (HD / 4), c = e % (HD / 4);
+            const int r = k0 + rr;
+            float4 vx = make_float4(0.f, 0.f, 0.f, 0.f), vy = vx;
+            if (r < R) {
+                const int64_t ex = (int64_t)b * R + r;
+                const int64_t rx = clamp_row(xrow, ex, nrows), ry = clamp_row(yrow, ex, nrows);
+                if (rx >= 0 && ry >= 0) {
+                    vx = *reinterpret_cast<const float4*>(X + rx * ld + h * HD + 4 * c);
+                    vy = *reinterpret_cast<const float4*>(Y + ry * ld + h * HD + 4 * c);
+                }
+            }
+            *reinterpret_cast<float4*>(Xs + rr * RS + 4 * c) = vx;
+            *reinterpret_cast<float4*>(Ys + rr * RS + 4 * c) = vy;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < kOuterRows / 16; ++ks) {
+            float al[4];
+            bool any = false;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = k0 + 16 * ks + 4 * g + e;
+                al[e] = (nv && r < R) ? alpha[b * as_b + (int64_t)r * as_r + n * as_n] : 0.0f;
+                any = any || al[e] != 0.0f;
+            }
+            if (!__any(any)) continue;
+            const float* xr = Xs + (16 * ks + 4 * g) * RS;
+            const float* yr = Ys + (16 * ks + 4 * g) * RS;
+            bf16x4 ahi[4], alo[4], bhi[4], blo[4];
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = al[e] * xr[e * RS + 16 * it + c16];
+                split_bf16x4(v, ahi[it], alo[it]);
+            }
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = yr[e * RS + 16 * jt + c16];
+                split_bf16x4(v, bhi[jt], blo[jt]);
+            }
+#pragma unroll
+            for (int it = 0; it < 4; ++it)
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) acc[it][jt] = mfma3(ahi[it], alo[it], bhi[jt], blo[jt], acc[it][jt]);
+        }
+    }
+    if (!nv) return;
+    float* o = out + (((int64_t)b * H + h) * N + n) * HD * HD;
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[(16 * it + 4 * g + i) * HD + 16 * jt + c16] = acc[it][jt][i];
 }
 
 __device__ inline bool tok_ok(int64_t v, int64_t V) { return v >= 0 && v < V; }
@@ -496,7 +693,7 @@ extern "C" int mb_factored_outer(const float* X, const int64_t* xrow, const floa
     hipStream_t st = (hipStream_t)stream;
     const dim3 blk(256);
     if (hd == 64) {
-        hipLaunchKernelGGL(fac_outer_kernel<64>, dim3((N + 3) / 4, H, B), blk, 0, st, X, xrow, Y,
+        hipLaunchKernelGGL(fac_outer_mfma_kernel, dim3((N + 3) / 4, H, B), blk, 0, st, X, xrow, Y,
                            yrow, ld, nrows, alpha, as_b, as_r, as_n, R, H, N, out);
     } else {
         hipLaunchKernelGGL(fac_outer_kernel<32>, dim3((N + 7) / 8, H, B), blk, 0, st, X, xrow, Y,
@@ -523,7 +720,13 @@ extern "C" int mb_factored_apply(const float* M, const float* w, int64_t ldw, co
     hipLaunchKernelGGL((fac_apply_kernel<HDV, TR>), grid, blk, 0, st, M, w, ldw, Y, yrow, ld, nrows, \
                        alpha, as_b, as_r, as_n, R, H, N, out, ldo, accumulate)
     if (hd == 64) {
-        if (transpose) MB_FAC_APPLY(64, true); else MB_FAC_APPLY(64, false);
+        const dim3 g64((R + 63) / 64, H, B);
+        if (transpose)
+            hipLaunchKernelGGL(fac_apply_mfma_kernel<true>, g64, blk, 0, st, M, w, ldw, Y, yrow, ld,
+                               nrows, alpha, as_b, as_r, as_n, R, H, N, out, ldo, accumulate);
+        else
+            hipLaunchKernelGGL(fac_apply_mfma_kernel<false>, g64, blk, 0, st, M, w, ldw, Y, yrow, ld,
+                               nrows, alpha, as_b, as_r, as_n, R, H, N, out, ldo, accumulate);
     } else {
         if (transpose) MB_FAC_APPLY(32, true); else MB_FAC_APPLY(32, false);
     }
