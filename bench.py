@@ -633,7 +633,8 @@ def run_factored(args):
         "config": {"workload": "factored_ema_forward + backward (autograd, c_base state)",
                    "B": B, "T": T, "D": D, "H": H, "N": N, "V": V, "slots": K,
                    "algorithmic_tflop": round(flops / 1e12, 3)},
-        "roofline": {"bound": "mfma", "kernel": "all factored kernels (fp32 VALU)",
+        "roofline": {"bound": "mfma", "kernel": "all factored kernels (token pairs fp32 VALU; "
+                                               "state GEMMs bf16 MFMA on hi/lo-split fp32 operands)",
                      "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(tf / 157.3, 4), "traffic": None},
     }
