@@ -10,8 +10,10 @@ same module tree.  The reference runs a Python loop over steps that decays and u
     A[t,s] = sum_i q_t[i] e_k[x_s][i] G_{t-s}[i],   G_d = sum_n rho_n^d W_n,
     S_n = sum_k c_base[k,n] e_k[u_k] ⊗ e_v[u_k]   (the reference's initial state),
 
-by the gfx950 kernels behind mb_factored_tok_fwd / mb_factored_tok_bwd (the token pairs)
-and mb_factored_outer / mb_factored_apply (the c_base state), in fp32.  The small
+by the gfx950 kernels behind mb_factored_tok_fwd / mb_factored_tok_bwd (the token pairs,
+fp32) and mb_factored_outer / mb_factored_apply (the c_base state; at head_dim 64 on the
+bf16 matrix cores with every fp32 operand split into bf16 hi + lo, three products and fp32
+accumulation, about 2^-16 relative error per product).  The small
 [L+1, N] x [N, D] products with P[n,d] = rho_n^d (G and dW_pe's token part) are library
 GEMMs in float64.  CPU tensors raise NotImplementedError: there is no CPU path.
 """
