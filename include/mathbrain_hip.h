@@ -286,7 +286,10 @@ int mb_slot_batch(const int32_t *tokens, const int32_t *doc_ids, const float *st
  *   A[t,s] = sum_i q_t[i] e_k[x_s][i] G[t-s][i],  G[d] = sum_n rho_n^d W_n  ([L+1, D])
  *   S_n = sum_k c_base[b,k,n] e_k[u_k] ⊗ e_v[u_k]   (the initial state, factored_ema.py:52-67)
  *
- * All fp32, rows of D = H*hd elements; head_dim 32 or 64.  Token ids outside [0, V) are
+ * fp32 tensors, rows of D = H*hd elements; head_dim 32 or 64 (at 64 mb_factored_outer and
+ * mb_factored_apply run on the bf16 matrix cores with every fp32 operand split into bf16
+ * hi + lo, three products and fp32 accumulation: about 2^-16 relative error per product).
+ * Token ids outside [0, V) are
  * skipped; gathered row indices are clamped below at 0 (the reference's clamp of -1 slot
  * ids) and skipped at or above nrows.
  *

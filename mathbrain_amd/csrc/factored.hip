@@ -1,4 +1,4 @@
-// Factored linear EMA (mathbrain/factored_ema.py:22-146) on gfx950, fp32.
+// Factored linear EMA (mathbrain/factored_ema.py:22-146) on gfx950, fp32-accurate.
 //
 // Per sequence b and head h the reference runs a per-step state recurrence
 // (S_n <- rho_n S_n; o_t = sum_n (q_t ⊙ W_n)^T S_n; S_n += e_k[x_t] ⊗ e_v[x_t]), which is
