@@ -378,10 +378,10 @@ __device__ inline bool tok_ok(int64_t v, int64_t V) { return v >= 0 && v < V; }
 // The four kernels share one shape.  A block of 4 waves covers 64 steps of one (b, h) on its
 // lanes (the "lane steps") and walks the 64-step blocks of the other index (the "walked
 // steps"); the 4 waves take every fourth walked step and their partial sums are added in LDS
-// at the end.  The rows of the walked step (q, dO, e_k or e_v: one row for the whole wave)
-// are read by every lane at the same address; the distance-dependent G rows differ per lane
-// and come from LDS, where each tile stages the 127 distances it needs.  Each lane holds
-// whole hd-rows in registers, so no cross-lane sums are needed per pair.
+// at the end.  Each tile stages in LDS the rows of its walked block (q, dO, e_k or e_v: one
+// row for the whole wave, read by every lane at the same address) and the 127
+// distance-dependent G rows it needs (a different row per lane).  Each lane holds whole
+// hd-rows in registers, so no cross-lane sums are needed per pair.
 
 constexpr int kTW = 4;  // waves per block
 
@@ -447,9 +447,11 @@ __device__ inline void reduce_waves(float (&acc)[HD], float* red) {
     }
 }
 
+// LDS of a token-pair block: the tile's 127 distance rows plus the walked block's two row
+// sets (64 rows each), or the wave partials at the end.
 template <int HD>
 constexpr int tok_lds_floats() {
-    constexpr int a = TokLds<HD>::GROWS * TokLds<HD>::RS;
+    constexpr int a = (TokLds<HD>::GROWS + 2 * 64) * TokLds<HD>::RS;
     constexpr int r = (kTW - 1) * 64 * HD;
     return a > r ? a : r;
 }
@@ -475,17 +477,19 @@ fac_tok_fwd_kernel(const float* __restrict__ Q, const int64_t* __restrict__ x, i
         q[k] = tv ? Q[((int64_t)b * L + t) * D + h * HD + k] : 0.0f;
         o[k] = 0.0f;
     }
+    float* sk = lds + TokLds<HD>::GROWS * RS;  // e_k rows of the walked block
+    float* sv = sk + 64 * RS;                   // e_v rows
     for (int sb = 0; sb <= tb; ++sb) {
         const int dlo = (tb - sb) * 64 - 63;
         __syncthreads();
         stage_rows<HD>(lds, G, D, h, dlo, TokLds<HD>::GROWS, L + 1);
+        stage_tok_rows<HD>(sk, Ek, xb, V, D, h, sb * 64, 64, L);
+        stage_tok_rows<HD>(sv, Ev, xb, V, D, h, sb * 64, 64, L);
         __syncthreads();
         const int s_hi = min(sb * 64 + 64, L);
         for (int s = sb * 64 + w; s < s_hi; s += kTW) {
-            const int64_t xs = xb[s];
-            if (!tok_ok(xs, V)) continue;
-            const float* ek = Ek + xs * D + h * HD;
-            const float* ev = Ev + xs * D + h * HD;
+            const float* ek = sk + (s - sb * 64) * RS;
+            const float* ev = sv + (s - sb * 64) * RS;
             const int di = t - s - dlo;
             const bool pair = tv && t > s;
             const float* g = lds + (pair ? di : 0) * RS;
@@ -525,17 +529,19 @@ fac_tok_bwd_row_kernel(const float* __restrict__ dO, const int64_t* __restrict__
         go[k] = tv ? dO[((int64_t)b * L + t) * D + h * HD + k] : 0.0f;
         dq[k] = 0.0f;
     }
+    float* sk = lds + TokLds<HD>::GROWS * RS;
+    float* sv = sk + 64 * RS;
     for (int sb = 0; sb <= tb; ++sb) {
         const int dlo = (tb - sb) * 64 - 63;
         __syncthreads();
         stage_rows<HD>(lds, G, D, h, dlo, TokLds<HD>::GROWS, L + 1);
+        stage_tok_rows<HD>(sk, Ek, xb, V, D, h, sb * 64, 64, L);
+        stage_tok_rows<HD>(sv, Ev, xb, V, D, h, sb * 64, 64, L);
         __syncthreads();
         const int s_hi = min(sb * 64 + 64, L);
         for (int s = sb * 64 + w; s < s_hi; s += kTW) {
-            const int64_t xs = xb[s];
-            if (!tok_ok(xs, V)) continue;
-            const float* ek = Ek + xs * D + h * HD;
-            const float* ev = Ev + xs * D + h * HD;
+            const float* ek = sk + (s - sb * 64) * RS;
+            const float* ev = sv + (s - sb * 64) * RS;
             const int di = t - s - dlo;
             const bool pair = tv && t > s;
             const float* g = lds + (pair ? di : 0) * RS;
@@ -580,15 +586,19 @@ fac_tok_bwd_col_kernel(const float* __restrict__ Q, const float* __restrict__ dO
         acc[k] = 0.0f;
     }
     const int nb = (L + 63) / 64;
+    float* sq = lds + TokLds<HD>::GROWS * RS;  // q rows of the walked block
+    float* so = sq + 64 * RS;                   // dO rows
     for (int tb = sb; tb < nb; ++tb) {
         const int dlo = (tb - sb) * 64 - 63;
         __syncthreads();
         stage_rows<HD>(lds, G, D, h, dlo, TokLds<HD>::GROWS, L + 1);
+        stage_rows<HD>(sq, Q + (int64_t)b * L * D, D, h, tb * 64, 64, L);
+        stage_rows<HD>(so, dO + (int64_t)b * L * D, D, h, tb * 64, 64, L);
         __syncthreads();
         const int t_hi = min(tb * 64 + 64, L);
         for (int t = tb * 64 + w; t < t_hi; t += kTW) {
-            const float* q = Q + ((int64_t)b * L + t) * D + h * HD;
-            const float* go = dO + ((int64_t)b * L + t) * D + h * HD;
+            const float* q = sq + (t - tb * 64) * RS;
+            const float* go = so + (t - tb * 64) * RS;
             const int di = t - s - dlo;
             const bool pair = sv && t > s;
             const float* g = lds + (pair ? di : 0) * RS;
@@ -648,6 +658,8 @@ fac_tok_bwd_diag_kernel(const float* __restrict__ Q, const float* __restrict__ d
         __syncthreads();
         const int t_hi = min(tb * 64 + 64, L);
         for (int t = tb * 64 + w; t < t_hi; t += kTW) {
+            // the walked rows come from global memory here: staging them too (104 KB of LDS)
+            // leaves one block per CU and measured slower
             const float* q = Q + ((int64_t)b * L + t) * D + h * HD;
             const float* go = dO + ((int64_t)b * L + t) * D + h * HD;
             const int si = t - d - slo;
