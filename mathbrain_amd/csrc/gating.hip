@@ -130,6 +130,16 @@ gating_fwd_kernel(GateArgs a) {
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t r0 = tile * kGateRows;
         const int nr = (int)std::min<int64_t>(kGateRows, a.rows - r0);
+        // the tile's x_q values are requested first, so that their latency overlaps the
+        // staging and the gate sums
+        float xv[CPT][kGateRows];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int col = tid + j * kGateThreads;
+#pragma unroll
+            for (int r = 0; r < kGateRows; ++r)
+                xv[j][r] = (col < a.D && r < nr) ? a.xq[(r0 + r) * a.xq_sr + col] : 0.f;
+        }
         if (FUSED) {
             stage_counts(a, r0, nr, cst);
             __syncthreads();
@@ -144,7 +154,7 @@ gating_fwd_kernel(GateArgs a) {
             for (int r = 0; r < kGateRows; ++r) {
                 if (r >= nr) break;
                 const float g = SILU ? pre[j][r] * sigmoidf_(pre[j][r]) : pre[j][r];
-                xe[r * a.D + col] = a.xq[(r0 + r) * a.xq_sr + col] * g;
+                xe[r * a.D + col] = xv[j][r] * g;
             }
         }
         __syncthreads();
@@ -198,6 +208,23 @@ gating_bwd_kernel(GateArgs a) {
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t r0 = tile * kGateRows;
         const int nr = (int)std::min<int64_t>(kGateRows, a.rows - r0);
+        // this tile's inputs are requested first (their latency overlaps the gate sums)
+        float xv[CPT][kGateRows], dyv_[CPT][kGateRows], muv[kGateRows], rsv[kGateRows];
+#pragma unroll
+        for (int r = 0; r < kGateRows; ++r) {
+            muv[r] = r < nr ? a.mu[r0 + r] : 0.f;
+            rsv[r] = r < nr ? a.rstd[r0 + r] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int col = tid + j * kGateThreads;
+#pragma unroll
+            for (int r = 0; r < kGateRows; ++r) {
+                const bool ok = col < a.D && r < nr;
+                xv[j][r] = ok ? a.xq[(r0 + r) * a.xq_sr + col] : 0.f;
+                dyv_[j][r] = ok ? a.dy[(r0 + r) * a.D + col] : 0.f;
+            }
+        }
         if (FUSED) {
             stage_counts(a, r0, nr, cst);
             __syncthreads();
@@ -222,9 +249,9 @@ gating_bwd_kernel(GateArgs a) {
                 }
                 gv[j][r] = g;
                 ds[j][r] = dsil;
-                const float x = a.xq[(r0 + r) * a.xq_sr + col];
-                const float dyv = a.dy[(r0 + r) * a.D + col];
-                const float xhat = (x * g - a.mu[r0 + r]) * a.rstd[r0 + r];
+                const float x = xv[j][r];
+                const float dyv = dyv_[j][r];
+                const float xhat = (x * g - muv[r]) * rsv[r];
                 xh[r * a.D + col] = xhat;
                 dxh[r * a.D + col] = dyv * w;
                 acc_w[j] = __builtin_fmaf(dyv, xhat, acc_w[j]);
@@ -255,8 +282,8 @@ gating_bwd_kernel(GateArgs a) {
             for (int r = 0; r < kGateRows; ++r) {
                 if (r >= nr) break;
                 const float dxe = (dxh[r * a.D + col] - stats[2 * r] - xh[r * a.D + col] * stats[2 * r + 1]) *
-                                  a.rstd[r0 + r];
-                const float x = a.xq[(r0 + r) * a.xq_sr + col];
+                                  rsv[r];
+                const float x = xv[j][r];
                 a.dxq[(r0 + r) * a.D + col] = dxe * gv[j][r];
                 const float dp = dxe * x * ds[j][r];
                 a.dpp[(r0 + r) * a.D + col] = dp;
