@@ -33,7 +33,7 @@ extern "C" {
 /* Message of the last failing call on this thread ("" if none). */
 const char *mb_last_error(void);
 
-/* ABI version of this library (bumped on any signature change). */
+/* ABI version of this library (bumped on any signature or flag change). */
 int mb_abi_version(void);
 
 /*
@@ -93,6 +93,8 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
 /* Flags of the flash-EMA entry points. */
 #define MB_FLASH_SILU 1        /* gate = SiLU(pre); otherwise the linear gate (use_silu=False) */
 #define MB_FLASH_ABSENT_MASS 2 /* softmax also over the V - K_b absent slots (score 0) */
+#define MB_FLASH_VOCAB_ROWS 4  /* E_k, E_v (dE_k, dE_v) are [V_total, H*hd] tables indexed by
+                                  the slot's token id instead of [B, K, H*hd] gathered rows */
 
 /*
  * Flash-EMA gated cross-attention forward.  Replaces flash_ema_forward and its kernel
@@ -112,7 +114,12 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
  *
  *   Q         [B, H, L, hd] fp32, element strides q_sb, q_sh, q_sl, q_sd
  *   x         [B, L] int64, element strides x_sb, x_sl
- *   E_k, E_v  [B, K, H*hd] fp32 contiguous
+ *   E_k, E_v  [B, K, H*hd] fp32 contiguous: row (b, k) is slot k of sequence b; with
+ *             MB_FLASH_VOCAB_ROWS [V_total, H*hd], row unique[b,k] (ids are clamped to
+ *             [0, V_total); padding slots read row 0 and contribute nothing).  The
+ *             projections k_proj(ln_kv(E)) act row by row, so projecting the vocabulary
+ *             table once gives the rows the slots would gather (fewer rows when
+ *             B*K > V_total, and no gather).
  *   W_pe      [N, H*hd] fp32 contiguous (pe_proj.weight transposed)
  *   rhos      [N] fp32
  *   unique    [B, K] int64 contiguous, -1 = padding slot
@@ -144,7 +151,8 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
  *   O, LSE    the forward's outputs (contiguous)
  *   scores    NULL (recompute the scores), or the forward's scores output
  *   dQ        [B, H, L, hd] fp32 contiguous output
- *   dE_k/dE_v [B, K, H*hd] fp32 contiguous outputs (zero for padding slots)
+ *   dE_k/dE_v [B, K, H*hd] fp32 contiguous outputs (zero for padding slots); with
+ *             MB_FLASH_VOCAB_ROWS [V_total, H*hd], the sums over every slot of each token
  *   dW_pe     [N, H*hd] fp32 contiguous output
  *
  * dQ is written once per element.  dE_k, dE_v and dW_pe are cleared by the call (with a

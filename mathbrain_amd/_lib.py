@@ -53,6 +53,7 @@ SIGNATURES = {
 
 MB_FLASH_SILU = 1
 MB_FLASH_ABSENT_MASS = 2
+MB_FLASH_VOCAB_ROWS = 4
 
 _lib = None
 

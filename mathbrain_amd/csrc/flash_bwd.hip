@@ -47,9 +47,10 @@ static int zero_fill(float* p, int64_t n, hipStream_t st) {
 // registers).  XH (N > 64 at head_dim 64, one slot per batch): the rate tiles outnumber what
 // a wave holds, so the two half-waves of a head swap their dpre tiles through LDS and each
 // multiplies all 32 steps into its own half of the tiles [NTW th, NTW th + NTW).
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NTW, bool XH>
+// VR: E_k / E_v and dE_k / dE_v are vocabulary tables indexed by the slot's token id.
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NTW, bool XH, bool VR>
 __global__ void __launch_bounds__(512, 1)
-flash_ema_bwd_kernel(FlashArgs a) {
+flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
     constexpr int WID = kBwdHeads * HD;  // embedding columns of this head group
@@ -173,7 +174,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
     };
     if (nb > 0) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
-        prod.load(a, b, cbi, 0, kend, D, col0, WID);
+        if (VR) __syncthreads();  // the load reads the batch's token ids
+        prod.template load<VR>(a, b, cbi, 0, kend, D, col0, WID, meta_of(0));
         load_scores(0);
         __syncthreads();
         store_scores(S2_of(0));
@@ -185,7 +187,7 @@ flash_ema_bwd_kernel(FlashArgs a) {
     for (int bi = 0; bi < nb; ++bi) {
         const int cur = bi & 1;
         if (bi + 1 < nb) {
-            prod.load(a, b, cbi, bi + 1, kend, D, col0, WID);
+            prod.template load<VR>(a, b, cbi, bi + 1, kend, D, col0, WID, meta_of(bi + 1));
             load_scores(bi + 1);
         }
         const _Float16* cdec = cdec_of(cur);
@@ -271,7 +273,8 @@ flash_ema_bwd_kernel(FlashArgs a) {
             // dE: this lane's 4 steps summed in registers; the 4 row groups (other steps)
             // are reduce-scattered with v_permlane16/32_swap so that row g holds dim tile g
             // (DT = 4) or rows 0 and 2 hold tiles 0 and 1 (DT = 2); one atomic per lane.
-            const int64_t erow = ((int64_t)b * a.K + bi * SB + j) * D + col0 + hl * HD;
+            const int64_t slot_row = VR ? min(meta[j].u, e_rows_of(a) - 1) : (int64_t)b * a.K + bi * SB + j;
+            const int64_t erow = slot_row * D + col0 + hl * HD;
             if (DT == 4) {
                 const float vk = rows4_reduce_scatter(dEk[0], dEk[1 % DT], dEk[2 % DT], dEk[3 % DT]);
                 const float vv = rows4_reduce_scatter(dEv[0], dEv[1 % DT], dEv[2 % DT], dEv[3 % DT]);
@@ -374,8 +377,8 @@ static size_t bwd_lds_bytes() {
 }
 
 template <int HD, int NS, int SB>
-static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
-    FlashArgs a = a0;
+static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
+    FlashArgsV a = a0;
     a.head_groups = a.H / kBwdHeads;
     constexpr int NPAD = 32 * NS;
     constexpr int WID = kBwdHeads * HD;
@@ -393,25 +396,26 @@ static int launch_bwd(const FlashArgs& a0, hipStream_t st) {
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: hd=%d, N=%d needs %zu B of LDS", HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
     dim3 grid(a.B * ntb * a.head_groups);
-#define MB_BWD(MI, ME)                                                                      \
-    do {                                                                                    \
-        auto k = a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH>   \
-                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH>) \
-                        : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH>  \
-                                  : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH>); \
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
-        if (e != hipSuccess) {                                                              \
-            (void)hipGetLastError();                                                        \
-            return fail((int)e, "mb_flash_ema_bwd: LDS attribute: %s", hipGetErrorString(e)); \
-        }                                                                                   \
-        hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, a);                                \
+#define MB_BWD_PICK(MI, ME, VR)                                                                  \
+    (a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH, VR>             \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH, VR>)           \
+            : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH, VR>            \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH, VR>))
+    const FlashArgs& base = a;
+#define MB_BWD(MI, ME)                                                                            \
+    do {                                                                                          \
+        const int rc_ = vr ? launch_with_lds(MB_BWD_PICK(MI, ME, true), grid, nthr, lds, st, a,      \
+                                             "mb_flash_ema_bwd")                                  \
+                           : launch_with_lds(MB_BWD_PICK(MI, ME, false), grid, nthr, lds, st, base, \
+                                             "mb_flash_ema_bwd");                                 \
+        if (rc_) return rc_;                                                                      \
     } while (0)
     if (mi <= 1 && me <= 1) MB_BWD(1, 1);
     else if (mi <= 2 && me <= 1) MB_BWD(2, 1);
     else if (mi <= 2 && me <= 2) MB_BWD(2, 2);
     else return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: N=%d too wide", a.N);
 #undef MB_BWD
+#undef MB_BWD_PICK
     return check_launch("mb_flash_ema_bwd");
 }
 
@@ -429,7 +433,7 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
                                 int H, int L, int hd, int K, int N, int Np, int nc, int Br,
                                 int64_t V_total, int flags, const float* scores, float* dQ,
                                 float* dE_k, float* dE_v, float* dW_pe, void* stream) {
-    FlashArgs a{};
+    FlashArgsV a{};
     a.Q = Q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_sl = q_sl; a.q_sd = q_sd;
     a.dO = dO; a.x = x; a.x_sb = x_sb; a.x_sl = x_sl;
     a.Ek = E_k; a.Ev = E_v; a.W = W_pe; a.rhos = rhos; a.unique = unique; a.Cb = C_bounds;
@@ -439,8 +443,11 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     a.silu = (flags & MB_FLASH_SILU) ? 1 : 0;
     a.dQ = dQ; a.dEk = dE_k; a.dEv = dE_v; a.dW = dW_pe;
     a.S2in = scores;
+    const bool vr = (flags & MB_FLASH_VOCAB_ROWS) != 0;
+    a.e_rows = vr ? V_total : 0;
     int rc = flash_validate("mb_flash_ema_bwd", a, hd);
     if (rc) return rc;
+    MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_bwd: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
     if (H % kBwdHeads)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: H=%d must be a multiple of %d", H, kBwdHeads);
     if (B == 0 || L == 0) return MB_OK;
@@ -452,16 +459,17 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     const int64_t D = (int64_t)H * hd;
     if ((rc = zero_fill(dW_pe, (int64_t)N * D, st))) return rc;
     if (K > 0) {
-        if ((rc = zero_fill(dE_k, (int64_t)B * K * D, st))) return rc;
-        if ((rc = zero_fill(dE_v, (int64_t)B * K * D, st))) return rc;
+        const int64_t rows = vr ? V_total : (int64_t)B * K;
+        if ((rc = zero_fill(dE_k, rows * D, st))) return rc;
+        if ((rc = zero_fill(dE_v, rows * D, st))) return rc;
     }
     const int NS = (N + 31) / 32;
     if (hd == 64) {
-        if (NS == 1) return launch_bwd<64, 1, 4>(a, st);
-        if (NS == 2) return launch_bwd<64, 2, 4>(a, st);
-        return launch_bwd<64, 4, 1>(a, st);
+        if (NS == 1) return launch_bwd<64, 1, 4>(a, vr, st);
+        if (NS == 2) return launch_bwd<64, 2, 4>(a, vr, st);
+        return launch_bwd<64, 4, 1>(a, vr, st);
     }
-    if (NS == 1) return launch_bwd<32, 1, 4>(a, st);
-    if (NS == 2) return launch_bwd<32, 2, 4>(a, st);
-    return launch_bwd<32, 4, 2>(a, st);
+    if (NS == 1) return launch_bwd<32, 1, 4>(a, vr, st);
+    if (NS == 2) return launch_bwd<32, 2, 4>(a, vr, st);
+    return launch_bwd<32, 4, 2>(a, vr, st);
 }

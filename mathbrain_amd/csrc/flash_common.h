@@ -44,8 +44,8 @@ struct FlashArgs {
     int64_t q_sb, q_sh, q_sl, q_sd;
     const int64_t* x;
     int64_t x_sb, x_sl;
-    const float* Ek;  // [B, K, D]
-    const float* Ev;  // [B, K, D]
+    const float* Ek;  // [B, K, D], or [e_rows, D] indexed by token id (FlashArgsV)
+    const float* Ev;  // the same
     const float* W;   // [N, D]  (pe_proj.weight transposed)
     const float* rhos;
     const int64_t* unique;  // [B, K], -1 = padding
@@ -62,11 +62,37 @@ struct FlashArgs {
     const float* Oin;  // forward output, [B, H, L, hd] contiguous
     const float* LSEin;
     float* dQ;   // [B, H, L, hd] contiguous
-    float* dEk;  // [B, K, D], accumulated with atomics (zeroed by the host)
+    float* dEk;  // like Ek, accumulated with atomics (zeroed by the host)
     float* dEv;
     float* dW;   // [N, D], accumulated with atomics (zeroed by the host)
     int head_groups;  // backward: workgroups per (b, block) along heads
 };
+
+// Arguments of the kernels whose E_k / E_v (and dE_k / dE_v) rows are token ids into
+// [e_rows, D] vocabulary tables (their VR template parameter).  A separate type, so that
+// the other kernels keep their argument layout (and with it their code schedule).
+struct FlashArgsV : FlashArgs {
+    int64_t e_rows;
+};
+template <bool VR> struct FlashArgsOf { using type = FlashArgs; };
+template <> struct FlashArgsOf<true> { using type = FlashArgsV; };
+
+__device__ inline int64_t e_rows_of(const FlashArgs& a) { return (int64_t)a.B * a.K; }
+__device__ inline int64_t e_rows_of(const FlashArgsV& a) { return a.e_rows; }
+
+// Sets a kernel's dynamic LDS limit and launches it with its argument block.
+template <class Kern, class Args>
+static int launch_with_lds(Kern k, dim3 grid, int nthr, size_t lds, hipStream_t st,
+                           const Args& args, const char* who) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail((int)e, "%s: LDS attribute: %s", who, hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, args);
+    return MB_OK;
+}
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
@@ -147,6 +173,16 @@ struct Stage {
     }
 };
 
+// Row of slot (b, k), token id u, in E_k / E_v / dE_k / dE_v: b*K + k, or with VR
+// the token id (padding slots, -1, read row 0; ids are clamped to the table).  u comes from
+// the batch's slot info in LDS: a global read here would make the producer's other loads
+// wait with it (memory reads complete in order).
+template <bool VR, class A>
+__device__ inline int64_t e_row(const A& a, int b, int k, int64_t u) {
+    if (!VR) return (int64_t)b * a.K + k;
+    return min(max(u, (int64_t)0), e_rows_of(a) - 1);
+}
+
 struct BatchMeta {
     int64_t u;
     uint64_t mask;
@@ -219,8 +255,9 @@ struct Producer {
     float4 s[MAXI];
     float4 e[MAXE];
 
-    __device__ void load(const FlashArgs& a, int b, int cbi, int bi, int kend, int D, int col0,
-                         int width) {
+    template <bool VR, class A>
+    __device__ void load(const A& a, int b, int cbi, int bi, int kend, int D, int col0,
+                         int width, const BatchMeta* meta) {
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
 #pragma unroll
@@ -257,7 +294,7 @@ struct Producer {
                 const int k = bi * SB + j;
                 if (k < kend) {
                     const float* src =
-                        (which ? a.Ev : a.Ek) + ((int64_t)b * a.K + k) * D + col0 + c4 * 4;
+                        (which ? a.Ev : a.Ek) + e_row<VR>(a, b, k, VR ? meta[j].u : 0) * D + col0 + c4 * 4;
                     v = *reinterpret_cast<const float4*>(src);
                 }
             }

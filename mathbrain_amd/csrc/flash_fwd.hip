@@ -24,9 +24,10 @@ namespace mb {
 
 constexpr float kTau = 8.0f;
 
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU>
+// VR: E_k / E_v are vocabulary tables indexed by the slot's token id (MB_FLASH_VOCAB_ROWS).
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR>
 __global__ void __launch_bounds__(512, 1)
-flash_ema_fwd_kernel(FlashArgs a) {
+flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
     using S = Stage<NPAD, SB>;
@@ -113,7 +114,8 @@ flash_ema_fwd_kernel(FlashArgs a) {
     Producer<NPAD, SB, MAXI, MAXE> prod;
     if (nb > 0) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
-        prod.load(a, b, cbi, 0, kend, D, 0, D);
+        if (VR) __syncthreads();  // the load reads the batch's token ids
+        prod.template load<VR>(a, b, cbi, 0, kend, D, 0, D, meta_of(0));
         __syncthreads();
         prod.template store<false, S::CROW, S::TROW>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
@@ -122,7 +124,7 @@ flash_ema_fwd_kernel(FlashArgs a) {
 
     for (int bi = 0; bi < nb; ++bi) {
         const int cur = bi & 1;
-        if (bi + 1 < nb) prod.load(a, b, cbi, bi + 1, kend, D, 0, D);
+        if (bi + 1 < nb) prod.template load<VR>(a, b, cbi, bi + 1, kend, D, 0, D, meta_of(bi + 1));
         const _Float16* cdec = cdec_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
@@ -244,7 +246,7 @@ static size_t fwd_lds_bytes(int D) {
 }
 
 template <int HD, int NS, int SB>
-static int launch_fwd(const FlashArgs& a, hipStream_t st) {
+static int launch_fwd(const FlashArgsV& a, bool vr, hipStream_t st) {
     const int D = a.H * HD;
     const int nthr = 64 * a.H;
     constexpr int NPAD = 32 * NS;
@@ -255,17 +257,16 @@ static int launch_fwd(const FlashArgs& a, hipStream_t st) {
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: D=%d, N=%d needs %zu B of LDS", D, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
     dim3 grid(a.B * ntb);
-#define MB_FWD(MI, ME)                                                                      \
-    do {                                                                                    \
-        auto k = a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true>                   \
-                        : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false>;                 \
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),                 \
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
-        if (e != hipSuccess) {                                                              \
-            (void)hipGetLastError();                                                        \
-            return fail((int)e, "mb_flash_ema_fwd: LDS attribute: %s", hipGetErrorString(e)); \
-        }                                                                                   \
-        hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, a);                                \
+    const FlashArgs& base = a;
+#define MB_FWD(MI, ME)                                                                           \
+    do {                                                                                         \
+        const int rc_ = vr ? launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true>    \
+                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true>,  \
+                                             grid, nthr, lds, st, a, "mb_flash_ema_fwd")                      \
+                           : launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false>   \
+                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false>, \
+                                             grid, nthr, lds, st, base, "mb_flash_ema_fwd");                  \
+        if (rc_) return rc_;                                                                     \
     } while (0)
     const int me = (nvec + nthr - 1) / nthr;
     if (mi > 4 || me > 4)
@@ -308,7 +309,7 @@ extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
                                 int B, int H, int L, int hd, int K, int N, int Np, int nc, int Br,
                                 int64_t V_total, int flags, float* O, float* LSE, float* scores,
                                 void* stream) {
-    FlashArgs a{};
+    FlashArgsV a{};
     a.Q = Q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_sl = q_sl; a.q_sd = q_sd;
     a.x = x; a.x_sb = x_sb; a.x_sl = x_sl;
     a.Ek = E_k; a.Ev = E_v; a.W = W_pe; a.rhos = rhos; a.unique = unique; a.Cb = C_bounds;
@@ -317,19 +318,22 @@ extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     a.silu = (flags & MB_FLASH_SILU) ? 1 : 0;
     a.O = O; a.LSE = LSE;
     a.S2out = scores;
+    const bool vr = (flags & MB_FLASH_VOCAB_ROWS) != 0;
+    a.e_rows = vr ? V_total : 0;
     int rc = flash_validate("mb_flash_ema_fwd", a, hd);
     if (rc) return rc;
+    MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_fwd: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
     if (B == 0 || L == 0) return MB_OK;
     MB_REQUIRE(Q && x && rhos && unique && O && LSE && W_pe, "mb_flash_ema_fwd: null pointer");
     MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_fwd: null slot pointer");
     hipStream_t st = (hipStream_t)stream;
     const int NS = (N + 31) / 32;
     if (hd == 64) {
-        if (NS == 1) return launch_fwd<64, 1, 4>(a, st);
-        if (NS == 2) return launch_fwd<64, 2, 4>(a, st);
-        return launch_fwd<64, 4, 2>(a, st);
+        if (NS == 1) return launch_fwd<64, 1, 4>(a, vr, st);
+        if (NS == 2) return launch_fwd<64, 2, 4>(a, vr, st);
+        return launch_fwd<64, 4, 2>(a, vr, st);
     }
-    if (NS == 1) return launch_fwd<32, 1, 4>(a, st);
-    if (NS == 2) return launch_fwd<32, 2, 4>(a, st);
-    return launch_fwd<32, 4, 2>(a, st);
+    if (NS == 1) return launch_fwd<32, 1, 4>(a, vr, st);
+    if (NS == 2) return launch_fwd<32, 2, 4>(a, vr, st);
+    return launch_fwd<32, 4, 2>(a, vr, st);
 }

@@ -67,8 +67,25 @@ def _build_unique_index(x, device):
     return out, K_max
 
 
-def _flash_flags(use_silu, absent_mass):
-    return (_lib.MB_FLASH_SILU if use_silu else 0) | (_lib.MB_FLASH_ABSENT_MASS if absent_mass else 0)
+def _flash_flags(use_silu, absent_mass, vocab_rows=False):
+    return ((_lib.MB_FLASH_SILU if use_silu else 0) | (_lib.MB_FLASH_ABSENT_MASS if absent_mass else 0)
+            | (_lib.MB_FLASH_VOCAB_ROWS if vocab_rows else 0))
+
+
+def _slot_rows(E, B, K, D, V_total, what):
+    """E_k / E_v in fp32: [B, K, D] gathered slot rows, or a [V_total, D] vocabulary table
+    whose row unique[b, k] is slot (b, k)'s (returns the tensor and whether it is a table)."""
+    Ef = E.to(torch.float32)
+    if Ef.dim() == 2:
+        if Ef.shape != (V_total, D):
+            raise ValueError(f"{what}: a vocabulary table must be [V_total, H*hd] = {(V_total, D)}, "
+                             f"got {tuple(Ef.shape)}")
+        return Ef.contiguous(), True
+    Ef = Ef.reshape(B, K, D) if Ef.dim() == 4 and Ef.shape[:2] == (B, K) else Ef
+    if Ef.shape != (B, K, D):
+        raise ValueError(f"{what}: E_k/E_v must be [B, K_max, H*hd] = {(B, K, D)} or a "
+                         f"[V_total, H*hd] table, got {tuple(E.shape)}")
+    return Ef.contiguous(), False
 
 
 def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
@@ -79,9 +96,12 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
     (pe_proj.weight.t()); rhos [N]; unique_tensor [B, K_max] (-1 = padding); C_bounds
     from ``precompute_boundaries(x, unique_tensor, rhos, Br, c_init)``.  Float inputs are
     used in fp32, as the reference's ``custom_fwd(cast_inputs=float32)`` does.
+    E_k_active / E_v_active may instead be [V_total, H*hd] vocabulary tables (the
+    projections of every embedding row): slot (b, k) then reads row unique_tensor[b, k],
+    the same values the [B, K_max] gather would hold, without the gather.
 
     Returns (O [B, H, L, hd] fp32, LSE [B, H, L], C_bounds, E_k, E_v) with E_k/E_v viewed
-    [B, K_max, H, hd], as the reference does.  With ``absent_mass`` (the default) the
+    [B, K_max, H, hd], as the reference does (tables are returned as given, in fp32).  With ``absent_mass`` (the default) the
     softmax covers all V_total slots as the dense PyTorch reference
     (flash_ema_attention.py:76-77) does; ``absent_mass=False`` gives the Triton kernel's
     softmax over the valid slots only (triton_flash_ema.py:215-229).  With
@@ -97,10 +117,10 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
     N = rhos.shape[0]
     D = H * hd
     Qf = Q.to(torch.float32)
-    Ek = E_k_active.to(torch.float32).contiguous()
-    Ev = E_v_active.to(torch.float32).contiguous()
-    if Ek.shape != (B, K, D) or Ev.shape != (B, K, D):
-        raise ValueError(f"E_k/E_v must be [B, K_max, H*hd] = {(B, K, D)}, got {tuple(Ek.shape)}")
+    Ek, table = _slot_rows(E_k_active, B, K, D, int(V_total), "flash_ema_forward")
+    Ev, table_v = _slot_rows(E_v_active, B, K, D, int(V_total), "flash_ema_forward")
+    if table != table_v:
+        raise ValueError("flash_ema_forward: E_k and E_v must both be tables or both gathered rows")
     W = W_pe.to(torch.float32).contiguous()
     if W.shape[0] < N or W.shape[1] != D:
         raise ValueError(f"W_pe must be [N, H*hd] = {(N, D)}, got {tuple(W.shape)}")
@@ -118,9 +138,12 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
         _lib.call("mb_flash_ema_fwd", _lib.ptr(Qf), *Qf.stride(), _lib.ptr(xl), xl.stride(0),
                   xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W), _lib.ptr(rh),
                   _lib.ptr(uniq), _lib.ptr(Cb), B, H, L, hd, K, N, Cb.shape[3], Cb.shape[1],
-                  int(Br), int(V_total), _flash_flags(use_silu, absent_mass), _lib.ptr(O),
+                  int(Br), int(V_total), _flash_flags(use_silu, absent_mass, table), _lib.ptr(O),
                   _lib.ptr(LSE), _lib.ptr(S2), _lib.stream(dev))
-    out = (O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd))
+    if table:
+        out = (O, LSE, C_bounds, Ek, Ev)
+    else:
+        out = (O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd))
     return out + (S2,) if return_scores else out
 
 
@@ -128,9 +151,10 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
                        use_silu=True, Br=64, absent_mass=True, scores=None):
     """Gradients of flash_ema_forward (triton_flash_ema.py:586-650) in one fused HIP pass.
 
-    E_k / E_v are [B, K, H*hd] or [B, K, H, hd]; ``scores`` is the forward's optional
-    scores output (recomputed when None).  Returns (dQ [B,H,L,hd], dE_k [B,K,H*hd],
-    dE_v [B,K,H*hd], dW_pe [N, H*hd]), all fp32.
+    E_k / E_v are [B, K, H*hd] or [B, K, H, hd], or [V_total, H*hd] vocabulary tables (then
+    dE_k / dE_v are tables too: each row sums the gradients of every slot of that token);
+    ``scores`` is the forward's optional scores output (recomputed when None).  Returns
+    (dQ [B,H,L,hd], dE_k [B,K,H*hd], dE_v [B,K,H*hd], dW_pe [N, H*hd]), all fp32.
     """
     dev = _lib.require_gpu(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO,
                            what="flash_ema_backward")
@@ -143,8 +167,10 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
     if dOf.stride() != Qf.stride():
         Qf = Qf.contiguous()
         dOf = dOf.contiguous()
-    Ek = E_k.to(torch.float32).reshape(B, K, D).contiguous()
-    Ev = E_v.to(torch.float32).reshape(B, K, D).contiguous()
+    Ek, table = _slot_rows(E_k, B, K, D, int(V_total), "flash_ema_backward")
+    Ev, table_v = _slot_rows(E_v, B, K, D, int(V_total), "flash_ema_backward")
+    if table != table_v:
+        raise ValueError("flash_ema_backward: E_k and E_v must both be tables or both gathered rows")
     W = W_pe.to(torch.float32)[:N].contiguous()
     rh = rhos.detach().to(torch.float32).contiguous()
     uniq = unique_tensor.to(torch.int64).contiguous()
@@ -153,8 +179,8 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
     Of = O.to(torch.float32).contiguous()
     Lf = LSE.to(torch.float32).contiguous()
     dQ = torch.empty(B, H, L, hd, dtype=torch.float32, device=dev)
-    dEk = torch.empty(B, K, D, dtype=torch.float32, device=dev)
-    dEv = torch.empty(B, K, D, dtype=torch.float32, device=dev)
+    dEk = torch.empty(Ek.shape, dtype=torch.float32, device=dev)
+    dEv = torch.empty(Ev.shape, dtype=torch.float32, device=dev)
     dW = torch.empty(N, D, dtype=torch.float32, device=dev)
     if scores is not None and (scores.shape != (B, H, K, L) or scores.dtype != torch.float32
                                or not scores.is_contiguous()):
@@ -164,7 +190,7 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
                   xl.stride(0), xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W),
                   _lib.ptr(rh), _lib.ptr(uniq), _lib.ptr(Cb), _lib.ptr(Of), _lib.ptr(Lf), B, H, L,
                   hd, K, N, Cb.shape[3], Cb.shape[1], int(Br), int(V_total),
-                  _flash_flags(use_silu, absent_mass), _lib.ptr(scores), _lib.ptr(dQ),
+                  _flash_flags(use_silu, absent_mass, table), _lib.ptr(scores), _lib.ptr(dQ),
                   _lib.ptr(dEk), _lib.ptr(dEv), _lib.ptr(dW), _lib.stream(dev))
     return dQ, dEk, dEv, dW
 

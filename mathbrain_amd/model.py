@@ -70,7 +70,9 @@ class SlotAttentionLayer(nn.Module):
                 E_active=None):
         """``E_active`` optionally carries the gather E_slots[max(unique, 0)] that every layer
         of the reference recomputes (model.py:63-64); SlotTransformerLM gathers once for all
-        layers, so the embedding backward runs once on the layers' summed gradients."""
+        layers, so the embedding backward runs once on the layers' summed gradients.  A 2-D
+        ``E_active`` [V, D] is the embedding table itself: the projections then cover the
+        vocabulary and the attention reads each slot's row by its token id."""
         B, L, D = x_q.shape
         if unique_tensor is None or C_bounds is None:
             # model.py:88-99 runs the dense all-vocabulary reference here; it is the CPU
@@ -147,6 +149,9 @@ class SlotTransformerLM(nn.Module):
         self.final_norm = RMSNorm(d_model)
         self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
         self.lm_head.weight = self.embed.weight
+        # K/V rows from the projected vocabulary table (True), from the per-row slot gather
+        # (False), or whichever has fewer rows (None)
+        self.kv_table = None
 
     def forward(self, x, unique_slots=None, inverse_indices=None, c_base=None, doc_ids=None, pad_mask=None):
         device = x.device
@@ -180,8 +185,17 @@ class SlotTransformerLM(nn.Module):
             c_base_kv = None
         C_bounds = precompute_boundaries(x, unique_tensor, self.ema_rhos, 64, c_init=c_base_kv)
         # The slot rows every layer gathers (model.py:63-64) are the same: gather once, so that
-        # autograd sums the layers' gradients first and runs one embedding backward.
-        E_active = F.embedding(torch.clamp(unique_tensor, min=0), E_slots)
+        # autograd sums the layers' gradients first and runs one embedding backward.  When
+        # the slot lists hold more rows than the vocabulary (B * K_max > V), the layers
+        # instead project the embedding table itself (ln_kv, k_proj and v_proj act row by
+        # row, so row u of the projected table is what every slot of token u would gather)
+        # and the attention reads the slot rows from it by token id: fewer rows to
+        # normalise, project and cast, and no gather or scatter.
+        use_table = self.kv_table if self.kv_table is not None else x.shape[0] * K_max > E_slots.shape[0]
+        if use_table:
+            E_active = E_slots
+        else:
+            E_active = F.embedding(torch.clamp(unique_tensor, min=0), E_slots)
         for layer in self.layers:
             x_q = layer(x_q, x, E_slots, self.ema_rhos, C_seq, unique_tensor, K_max, C_bounds, E_active)
         x_q = self.final_norm(x_q)

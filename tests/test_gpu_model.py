@@ -101,3 +101,30 @@ def test_model_few_slots_pads_to_sixteen():
     want = omodel.lm_forward(p, x, 1, H, m.ema_rhos.cpu(), V, unique_slots=uniq, c_base=cb.double(),
                              pad_mask=pm)
     assert norm_err(out, want) < TOL_BF16
+
+
+@pytest.mark.parametrize("kv_table", [None, True, False])
+def test_model_vocab_table_path_vs_oracle(kv_table):
+    """A vocabulary smaller than B * K_max: the layers project the embedding table and the
+    attention reads slot rows by token id (kv_table None picks it here); forced either way
+    the logits and every gradient match the float64 oracle with the kernel's gate rounding."""
+    V, D, n_layers, H, N, B, L = 60, 128, 2, 4, 16, 3, 96
+    m = build(V, D, n_layers, H, N, seed=6).cuda()
+    m.kv_table = kv_table
+    x, uniq, cb, pm = batch(B, L, V, N, seed=7)
+    assert B * max(uniq.shape[1], 16) > V
+    g = torch.Generator().manual_seed(8)
+    R = torch.randn(B, L, V, generator=g)
+    logits = m(x.cuda(), uniq.cuda(), None, cb.cuda(), None, pm.cuda())
+    (logits * R.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    p = {k: v.detach().cpu().double().requires_grad_() for k, v in m.state_dict().items()
+         if k != "ema_rhos" and k != "lm_head.weight"}
+    want = omodel.lm_forward(p, x, n_layers, H, m.ema_rhos.cpu(), V, gate_round="f16",
+                             unique_slots=uniq, c_base=cb.double(), pad_mask=pm)
+    (want * R.double()).sum().backward()
+    assert norm_err(logits, want) < 1e-4
+    grads = dict(m.named_parameters())
+    for k, v in p.items():
+        tol = 1e-2 if k.endswith("pe_proj.weight") else 1e-4
+        assert norm_err(grads[k].grad, v.grad) < tol, (kv_table, k)
