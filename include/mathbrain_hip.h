@@ -339,6 +339,24 @@ int mb_factored_tok_bwd(const float *Q, const float *dO, const int64_t *x, int64
                         int hd, float *dQ, float *dEk_tok, float *dEv_tok, float *dG_b,
                         void *stream);
 
+/*
+ * RMSNorm.  Replaces RMSNorm.forward (mathbrain/model.py:11-19) and its autograd backward:
+ *
+ *   mb_rmsnorm_fwd:  rstd[r] = rsqrt(mean_d x[r,d]^2 + eps),  y[r,d] = w[d] * (x[r,d] * rstd[r])
+ *   mb_rmsnorm_bwd:  dx[r,d] = rstd (w[d] dy[r,d]) - rstd^3 / D * x[r,d] * sum_e w[e] dy[r,e] x[r,e]
+ *                    dw[d]   = sum_r dy[r,d] x[r,d] rstd[r]  (cleared by the call with a fill
+ *                    kernel, then accumulated with fp32 atomics: summation order not fixed)
+ *
+ *   x, dy, y, dx  [rows, D] fp32 contiguous;  w, dw [D] fp32;  rstd [rows] fp32 (written by
+ *                 the forward, read by the backward)
+ *
+ * Supported: 1 <= D <= 1024.
+ */
+int mb_rmsnorm_fwd(const float *x, const float *w, int64_t rows, int D, float eps, float *y,
+                   float *rstd, void *stream);
+int mb_rmsnorm_bwd(const float *x, const float *w, const float *dy, const float *rstd,
+                   int64_t rows, int D, float *dx, float *dw, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

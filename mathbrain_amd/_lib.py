@@ -49,6 +49,8 @@ SIGNATURES = {
                            _i, _i, _p, _i64, _i, _p], _i),
     "mb_factored_tok_fwd": ([_p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _p, _p], _i),
     "mb_factored_tok_bwd": ([_p, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p], _i),
+    "mb_rmsnorm_fwd": ([_p, _p, _i64, _i, _f, _p, _p, _p], _i),
+    "mb_rmsnorm_bwd": ([_p, _p, _p, _p, _i64, _i, _p, _p, _p], _i),
 }
 
 MB_FLASH_SILU = 1

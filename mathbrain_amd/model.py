@@ -4,9 +4,9 @@ Drop-in for mathbrain/model.py (:11-186): the same modules, parameter names, con
 arguments and forward signatures, so checkpoints and train.py's calls carry over.  The
 hot path runs in the HIP kernels: the query scan (``compute_query_ema_history``), the
 key-side chunk states (``precompute_boundaries``), the gating with pe_proj folded in
-(``fused_apply_symmetric_query_gating``) and flash-EMA attention (``FlashEMAFunction``).
-RMSNorm, SwiGLU, the slot K/V projections and the tied lm_head stay torch modules, as in
-the reference.  The reference's CPU branch (dense attention over the whole vocabulary,
+(``fused_apply_symmetric_query_gating``), flash-EMA attention (``FlashEMAFunction``) and
+RMSNorm (``rms_norm``, one fused pass per direction).  SwiGLU, the slot K/V projections and
+the tied lm_head stay torch modules, as in the reference.  The reference's CPU branch (dense attention over the whole vocabulary,
 model.py:88-99) is not a product path here: CPU tensors raise NotImplementedError.
 """
 import math
@@ -18,6 +18,7 @@ import torch.nn.functional as F
 from .ema_query import compute_query_ema_history
 from .flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
 from .fused_gating import fused_apply_symmetric_query_gating
+from .rmsnorm import rms_norm
 
 
 class RMSNorm(nn.Module):
@@ -29,8 +30,9 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x):
-        variance = x.pow(2).mean(-1, keepdim=True)
-        return self.weight * (x * torch.rsqrt(variance + self.eps))
+        # one fused HIP pass per direction (mb_rmsnorm_fwd / mb_rmsnorm_bwd) for
+        # weight * (x * rsqrt(mean(x^2) + eps))
+        return rms_norm(x, self.weight, self.eps)
 
 
 class SwiGLU(nn.Module):
