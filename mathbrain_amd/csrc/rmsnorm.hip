@@ -17,6 +17,7 @@ namespace {
 
 constexpr int kRmsThreads = 256;  // four rows (waves) per workgroup
 constexpr int kRmsMaxD = 1024;
+constexpr int kRmsBwdBlocks = 512;
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -151,9 +152,11 @@ extern "C" int mb_rmsnorm_bwd(const float* x, const float* w, const float* dy, c
     hipLaunchKernelGGL(rms_zero_kernel, dim3((D + 255) / 256), dim3(256), 0, st, dw, D);
     if (rows == 0) return check_launch("mb_rmsnorm_bwd");
     MB_REQUIRE(x && w && dy && rstd && dx, "mb_rmsnorm_bwd: null pointer argument");
-    // enough workgroups to fill the chip; each walks rows with a grid stride
+    // two workgroups per CU, each walking rows with a grid stride: every workgroup adds its
+    // D column sums to dw at the end, so more workgroups mean more atomics on the same D
+    // addresses (2048 workgroups: 65 us at 28 672 x 512, most of it those atomics)
     const int64_t want = (rows + kRmsThreads / 64 - 1) / (kRmsThreads / 64);
-    const dim3 grid((unsigned)std::min<int64_t>(want, 2048)), blk(kRmsThreads);
+    const dim3 grid((unsigned)std::min<int64_t>(want, kRmsBwdBlocks)), blk(kRmsThreads);
     switch (rms_per(D)) {
         case 1: hipLaunchKernelGGL(rms_bwd_kernel<1>, grid, blk, 0, st, x, w, dy, rstd, rows, D, dx, dw); break;
         case 2: hipLaunchKernelGGL(rms_bwd_kernel<2>, grid, blk, 0, st, x, w, dy, rstd, rows, D, dx, dw); break;
