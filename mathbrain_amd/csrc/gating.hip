@@ -306,9 +306,12 @@ __global__ void gate_zero_kernel(float* p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0.f;
 }
 
-static int gate_grid(int64_t rows) {
+// Workgroups walk row tiles with a grid stride.  The backward's workgroups each add their
+// 3 x D column sums with atomics at the end, on the same 3 x D addresses, and only two of
+// them fit on a CU at once (VGPRs): it runs on as many as are resident.
+static int gate_grid(int64_t rows, bool bwd) {
     const int64_t ntiles = (rows + kGateRows - 1) / kGateRows;
-    return (int)std::max<int64_t>(1, std::min<int64_t>(ntiles, 256 * 8));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(ntiles, bwd ? 256 * 2 : 256 * 8));
 }
 
 template <bool BWD>
@@ -316,7 +319,7 @@ static int gate_launch(const GateArgs& a, bool fused, bool silu, hipStream_t st)
     const int cpt = (a.D + kGateThreads - 1) / kGateThreads;
     const size_t lds = ((BWD ? 2 : 1) * (size_t)kGateRows * a.D + 2 * kGateRows +
                         (fused ? (size_t)kGateRows * a.N : 0)) * sizeof(float);
-    const dim3 grid(gate_grid(a.rows));
+    const dim3 grid(gate_grid(a.rows, BWD));
 #define MB_GATE_K(C, F, S) (BWD ? gating_bwd_kernel<C, F, S> : gating_fwd_kernel<C, F, S>)
 #define MB_GATE_CPT(C)                                                                          \
     do {                                                                                        \
