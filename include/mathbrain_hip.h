@@ -357,6 +357,24 @@ int mb_rmsnorm_fwd(const float *x, const float *w, int64_t rows, int D, float ep
 int mb_rmsnorm_bwd(const float *x, const float *w, const float *dy, const float *rstd,
                    int64_t rows, int D, float *dx, float *dw, void *stream);
 
+/* Element types of the entry points that take either. */
+#define MB_DTYPE_F32 0
+#define MB_DTYPE_BF16 1
+
+/*
+ * SwiGLU gate product.  Replaces the elementwise part of SwiGLU.forward
+ * (mathbrain/model.py:21-29), F.silu(w1(x)) * w3(x), and its autograd backward:
+ *
+ *   mb_swiglu_fwd:  m  = SiLU(a) * b
+ *   mb_swiglu_bwd:  da = dm * b * s (1 + a (1 - s)),  db = dm * SiLU(a),  s = sigmoid(a)
+ *
+ *   a = w1(x), b = w3(x), m, dm, da, db: n elements each, contiguous, all of one dtype
+ *   (MB_DTYPE_F32 or MB_DTYPE_BF16); evaluated in fp32, rounded once to the dtype.
+ */
+int mb_swiglu_fwd(const void *a, const void *b, int64_t n, int dtype, void *m, void *stream);
+int mb_swiglu_bwd(const void *a, const void *b, const void *dm, int64_t n, int dtype, void *da,
+                  void *db, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

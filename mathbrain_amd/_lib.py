@@ -51,11 +51,15 @@ SIGNATURES = {
     "mb_factored_tok_bwd": ([_p, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p], _i),
     "mb_rmsnorm_fwd": ([_p, _p, _i64, _i, _f, _p, _p, _p], _i),
     "mb_rmsnorm_bwd": ([_p, _p, _p, _p, _i64, _i, _p, _p, _p], _i),
+    "mb_swiglu_fwd": ([_p, _p, _i64, _i, _p, _p], _i),
+    "mb_swiglu_bwd": ([_p, _p, _p, _i64, _i, _p, _p, _p], _i),
 }
 
 MB_FLASH_SILU = 1
 MB_FLASH_ABSENT_MASS = 2
 MB_FLASH_VOCAB_ROWS = 4
+MB_DTYPE_F32 = 0
+MB_DTYPE_BF16 = 1
 
 _lib = None
 

@@ -5,8 +5,9 @@ arguments and forward signatures, so checkpoints and train.py's calls carry over
 hot path runs in the HIP kernels: the query scan (``compute_query_ema_history``), the
 key-side chunk states (``precompute_boundaries``), the gating with pe_proj folded in
 (``fused_apply_symmetric_query_gating``), flash-EMA attention (``FlashEMAFunction``) and
-RMSNorm (``rms_norm``, one fused pass per direction).  SwiGLU, the slot K/V projections and
-the tied lm_head stay torch modules, as in the reference.  The reference's CPU branch (dense attention over the whole vocabulary,
+RMSNorm (``rms_norm``) and SwiGLU's gate product (``swiglu_product``), one fused pass per
+direction each.  The linear layers (the slot K/V projections, the FFN and the tied lm_head)
+stay torch modules, as in the reference.  The reference's CPU branch (dense attention over the whole vocabulary,
 model.py:88-99) is not a product path here: CPU tensors raise NotImplementedError.
 """
 import math
@@ -19,6 +20,7 @@ from .ema_query import compute_query_ema_history
 from .flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
 from .fused_gating import fused_apply_symmetric_query_gating
 from .rmsnorm import rms_norm
+from .swiglu import swiglu_product
 
 
 class RMSNorm(nn.Module):
@@ -45,7 +47,8 @@ class SwiGLU(nn.Module):
         self.w3 = nn.Linear(dim, hidden_dim, bias=False)
 
     def forward(self, x):
-        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+        # silu(w1 x) * w3 x as one fused HIP pass per direction (mb_swiglu_fwd / _bwd)
+        return self.w2(swiglu_product(self.w1(x), self.w3(x)))
 
 
 class SlotAttentionLayer(nn.Module):
