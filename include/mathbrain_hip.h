@@ -369,7 +369,8 @@ int mb_rmsnorm_bwd(const float *x, const float *w, const float *dy, const float 
  *   mb_swiglu_bwd:  da = dm * b * s (1 + a (1 - s)),  db = dm * SiLU(a),  s = sigmoid(a)
  *
  *   a = w1(x), b = w3(x), m, dm, da, db: n elements each, contiguous, all of one dtype
- *   (MB_DTYPE_F32 or MB_DTYPE_BF16); evaluated in fp32, rounded once to the dtype.
+ *   (MB_DTYPE_F32 or MB_DTYPE_BF16), 32-byte aligned (vector loads; others are rejected);
+ *   evaluated in fp32, rounded once to the dtype.
  */
 int mb_swiglu_fwd(const void *a, const void *b, int64_t n, int dtype, void *m, void *stream);
 int mb_swiglu_bwd(const void *a, const void *b, const void *dm, int64_t n, int dtype, void *da,

@@ -142,6 +142,8 @@ extern "C" int mb_swiglu_fwd(const void* a, const void* b, int64_t n, int dtype,
         return fail(MB_ERR_UNSUPPORTED, "mb_swiglu_fwd: dtype %d (supported: MB_DTYPE_F32, MB_DTYPE_BF16)", dtype);
     if (n == 0) return MB_OK;
     MB_REQUIRE(a && b && m, "mb_swiglu_fwd: null pointer argument");
+    MB_REQUIRE((((uintptr_t)a | (uintptr_t)b | (uintptr_t)m) & 31) == 0,
+               "mb_swiglu_fwd: pointers must be 32-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     if (dtype == MB_DTYPE_F32)
         hipLaunchKernelGGL(swiglu_fwd_kernel<float>, swiglu_grid(n), dim3(kSwiThreads), 0, st,
@@ -159,6 +161,8 @@ extern "C" int mb_swiglu_bwd(const void* a, const void* b, const void* dm, int64
         return fail(MB_ERR_UNSUPPORTED, "mb_swiglu_bwd: dtype %d (supported: MB_DTYPE_F32, MB_DTYPE_BF16)", dtype);
     if (n == 0) return MB_OK;
     MB_REQUIRE(a && b && dm && da && db, "mb_swiglu_bwd: null pointer argument");
+    MB_REQUIRE((((uintptr_t)a | (uintptr_t)b | (uintptr_t)dm | (uintptr_t)da | (uintptr_t)db) & 31) == 0,
+               "mb_swiglu_bwd: pointers must be 32-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     if (dtype == MB_DTYPE_F32)
         hipLaunchKernelGGL(swiglu_bwd_kernel<float>, swiglu_grid(n), dim3(kSwiThreads), 0, st,
