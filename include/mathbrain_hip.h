@@ -357,6 +357,25 @@ int mb_rmsnorm_fwd(const float *x, const float *w, int64_t rows, int D, float ep
 int mb_rmsnorm_bwd(const float *x, const float *w, const float *dy, const float *rstd,
                    int64_t rows, int D, float *dx, float *dw, void *stream);
 
+/*
+ * LayerNorm (the model's ln_kv over the embedding rows, mathbrain/model.py:63-64):
+ *
+ *   mb_layernorm_fwd:  mean[r] = mean_d x[r,d],  rstd[r] = rsqrt(mean_d (x - mean)^2 + eps),
+ *                      y[r,d] = (x[r,d] - mean[r]) rstd[r] w[d] + b[d]
+ *   mb_layernorm_bwd:  with xh = (x - mean) rstd and g = dy w:
+ *                      dx = rstd (g - mean_d g - xh mean_d(g xh)),
+ *                      dw = sum_r dy xh,  db = sum_r dy  (cleared by the call with a fill
+ *                      kernel, then accumulated with fp32 atomics: summation order not fixed)
+ *
+ *   x, dy, y, dx [rows, D] fp32 contiguous;  w, b, dw, db [D] fp32;  mean, rstd [rows] fp32
+ *   (written by the forward, read by the backward).  Supported: 1 <= D <= 1024.
+ */
+int mb_layernorm_fwd(const float *x, const float *w, const float *b, int64_t rows, int D, float eps,
+                     float *y, float *mean, float *rstd, void *stream);
+int mb_layernorm_bwd(const float *x, const float *w, const float *dy, const float *mean,
+                     const float *rstd, int64_t rows, int D, float *dx, float *dw, float *db,
+                     void *stream);
+
 /* Element types of the entry points that take either. */
 #define MB_DTYPE_F32 0
 #define MB_DTYPE_BF16 1

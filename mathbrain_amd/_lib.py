@@ -51,6 +51,8 @@ SIGNATURES = {
     "mb_factored_tok_bwd": ([_p, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p], _i),
     "mb_rmsnorm_fwd": ([_p, _p, _i64, _i, _f, _p, _p, _p], _i),
     "mb_rmsnorm_bwd": ([_p, _p, _p, _p, _i64, _i, _p, _p, _p], _i),
+    "mb_layernorm_fwd": ([_p, _p, _p, _i64, _i, _f, _p, _p, _p, _p], _i),
+    "mb_layernorm_bwd": ([_p, _p, _p, _p, _p, _i64, _i, _p, _p, _p, _p], _i),
     "mb_swiglu_fwd": ([_p, _p, _i64, _i, _p, _p], _i),
     "mb_swiglu_bwd": ([_p, _p, _p, _i64, _i, _p, _p, _p], _i),
 }

@@ -69,19 +69,35 @@ rms_bwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
         acc[i] = 0.f;
     }
     const float invD = 1.0f / (float)D;
-    for (int64_t row = (int64_t)blockIdx.x * (kRmsThreads / 64) + wave; row < rows; row += nwaves) {
-        const float* xr = x + row * D;
-        const float* gr = dy + row * D;
-        const float r = rstd[row];
-        float xv[PER], gv[PER];
-        float dot = 0.f;
+    // rows are software-pipelined: the next row's loads are issued before this row's math
+    int64_t row = (int64_t)blockIdx.x * (kRmsThreads / 64) + wave;
+    float xn[PER], gn[PER], rn = 0.f;
+    auto fetch = [&](int64_t rr) {
+        const bool okr = rr < rows;
+        const float* xr = x + (okr ? rr : 0) * D;
+        const float* gr = dy + (okr ? rr : 0) * D;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int d = lane + 64 * i;
-            xv[i] = d < D ? xr[d] : 0.f;
-            gv[i] = d < D ? gr[d] : 0.f;
-            dot = __builtin_fmaf(wv[i] * gv[i], xv[i], dot);
+            const bool ok = okr && d < D;
+            xn[i] = ok ? xr[d] : 0.f;
+            gn[i] = ok ? gr[d] : 0.f;
         }
+        rn = okr ? rstd[rr] : 0.f;
+    };
+    fetch(row);
+    for (; row < rows; row += nwaves) {
+        float xv[PER], gv[PER];
+        const float r = rn;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            xv[i] = xn[i];
+            gv[i] = gn[i];
+        }
+        fetch(row + nwaves);
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) dot = __builtin_fmaf(wv[i] * gv[i], xv[i], dot);
         dot = wave_sum(dot);
         const float c = r * r * r * invD * dot;
         float* dxr = dx + row * D;

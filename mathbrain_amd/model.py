@@ -5,8 +5,8 @@ arguments and forward signatures, so checkpoints and train.py's calls carry over
 hot path runs in the HIP kernels: the query scan (``compute_query_ema_history``), the
 key-side chunk states (``precompute_boundaries``), the gating with pe_proj folded in
 (``fused_apply_symmetric_query_gating``), flash-EMA attention (``FlashEMAFunction``) and
-RMSNorm (``rms_norm``) and SwiGLU's gate product (``swiglu_product``), one fused pass per
-direction each.  The linear layers (the slot K/V projections, the FFN and the tied lm_head)
+RMSNorm (``rms_norm``), ln_kv (``layer_norm``) and SwiGLU's gate product
+(``swiglu_product``), one fused pass per direction each.  The linear layers (the slot K/V projections, the FFN and the tied lm_head)
 stay torch modules, as in the reference.  The reference's CPU branch (dense attention over the whole vocabulary,
 model.py:88-99) is not a product path here: CPU tensors raise NotImplementedError.
 """
@@ -19,6 +19,7 @@ import torch.nn.functional as F
 from .ema_query import compute_query_ema_history
 from .flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
 from .fused_gating import fused_apply_symmetric_query_gating
+from .layernorm import layer_norm
 from .rmsnorm import rms_norm
 from .swiglu import swiglu_product
 
@@ -88,7 +89,7 @@ class SlotAttentionLayer(nn.Module):
         # 1. slot K/V projections (model.py:63-68)
         if E_active is None:
             E_active = F.embedding(torch.clamp(unique_tensor, min=0), E_slots)
-        memory_base = self.ln_kv(E_active)
+        memory_base = layer_norm(E_active, self.ln_kv.weight, self.ln_kv.bias, self.ln_kv.eps)
         E_k_active = self.k_proj(memory_base)
         E_v_active = self.v_proj(memory_base)
         # 2. query gating (model.py:75)
