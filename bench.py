@@ -72,7 +72,7 @@ ATTENTION_CONFIGS = {
 
 
 def attention_case(seed=0, config="cfg2"):
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.synthetic import make_batch
     B, L, H, hd, N, V, pad = ATTENTION_CONFIGS[config]
     d = make_batch(B, L, V, N, 4096, seed=seed, pad_frac=pad)
     dev = torch.device("cuda", torch.cuda.current_device())
@@ -98,7 +98,7 @@ def attention_case(seed=0, config="cfg2"):
 
 
 def attention_step(c, timers=None):
-    from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
+    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
     Cb = precompute_boundaries(c["x"], c["unique"], c["rhos"], 64, c["c_base"])
     if timers is not None:
         timers["fwd"][0].record()
@@ -210,9 +210,9 @@ def run_attention(args):
 
 
 def run_scan(args):
-    from mathbrain_amd import _lib
-    from mathbrain_amd.ema_query import compute_query_ema_history
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain import _lib
+    from mathbrain.triton_ema_query import compute_query_ema_history
+    from mathbrain.synthetic import make_batch
     B, T, N, V = 56, 2048, 128, 50257
     d = make_batch(B, T, V, N, 8192, seed=3)
     dev = torch.device("cuda", torch.cuda.current_device())
@@ -274,7 +274,7 @@ def run_scan(args):
 
 
 def run_gating(args):
-    from mathbrain_amd import _lib
+    from mathbrain import _lib
     B, L, D, N = 56, 512, 512, 64
     dev = torch.device("cuda", torch.cuda.current_device())
     g = torch.Generator().manual_seed(0)
@@ -332,8 +332,8 @@ def run_gating(args):
 
 def run_model(args):
     import torch.nn.functional as F
-    from mathbrain_amd.model import SlotTransformerLM
-    from mathbrain_amd.synthetic import make_doc_batch
+    from mathbrain.model import SlotTransformerLM
+    from mathbrain.synthetic import make_doc_batch
     B, T, V, N, D, n_layers, H = 56, 512, 50257, 64, 512, 6, 8
     dev = torch.device("cuda", torch.cuda.current_device())
     torch.set_float32_matmul_precision("high")   # train.py:94-95
@@ -406,9 +406,9 @@ def run_corpus(args):
     """The corpus state scan of preprocess_corpus (mb_corpus_states) over a 64 M-token
     synthetic corpus (50257 ids, Zipf(1.1), lognormal documents of median 3000, N=64)."""
     import numpy as np
-    from mathbrain_amd import _lib
-    from mathbrain_amd.data import chain_order, corpus_states
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain import _lib
+    from mathbrain.data import chain_order, corpus_states
+    from mathbrain.synthetic import zipf_corpus
     T, V, N = 1 << 26, 50257, 64
     tokens, doc_ids = zipf_corpus(T, V, median_len=3000, seed=11)
     dev = torch.device("cuda", torch.cuda.current_device())
@@ -475,9 +475,9 @@ def run_batch(args):
     16 M-token synthetic corpus (50257 ids, lognormal documents of median 4000, N=64),
     slots expanded with each document's history and c_base gathered from the state rows."""
     import numpy as np
-    from mathbrain_amd import _lib
-    from mathbrain_amd.data import chunk_index, corpus_states, next_occurrence
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain import _lib
+    from mathbrain.data import chunk_index, corpus_states, next_occurrence
+    from mathbrain.synthetic import zipf_corpus
     T, V, N, B, block = 1 << 24, 50257, 64, 56, 512
     tokens, doc_ids = zipf_corpus(T, V, median_len=4000, seed=12)
     dev = torch.device("cuda", torch.cuda.current_device())
@@ -587,8 +587,8 @@ def run_factored(args):
     """The factored linear EMA (factored_ema_forward, fwd + bwd) at configuration 2's shapes:
     B=56, T=512, d_model 512, 8 heads x 64, N=64, V=50257, c_base over the history-expanded
     slots of a 4096-token warm-up per sequence."""
-    from mathbrain_amd.factored_ema import factored_ema_forward
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.factored_ema import factored_ema_forward
+    from mathbrain.synthetic import make_batch
     B, T, H, hd, N, V = 56, 512, 8, 64, 64, 50257
     D = H * hd
     d = make_batch(B, T, V, N, 4096, min_hl=1.0, max_hl=4096.0, seed=0)

@@ -90,6 +90,23 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
                            const float *c_init, int64_t c_init_stride_k, const int64_t *doc_ids,
                            float *C_bounds, int Np, void *stream);
 
+/*
+ * Sorted distinct ids of each row.  Replaces the body of _build_unique_index
+ * (mathbrain/triton_flash_ema.py:475-507):
+ *
+ *   out[b, 0:counts[b]]     = the distinct values of x[b, :] in increasing order
+ *   out[b, counts[b]:width] = -1
+ *
+ *   x       [B, L] int64, element strides (x_stride_b, x_stride_l)
+ *   out     [B, width] int64 contiguous output (a row's ids beyond width are dropped;
+ *           width >= L keeps all of them)
+ *   counts  [B] int32 output: distinct values per row
+ *
+ * Limits: L <= 8192 (a row is sorted in the LDS of one CU).
+ */
+int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int B, int L,
+                   int64_t *out, int width, int32_t *counts, void *stream);
+
 /* Flags of the flash-EMA entry points. */
 #define MB_FLASH_SILU 1        /* gate = SiLU(pre); otherwise the linear gate (use_silu=False) */
 #define MB_FLASH_ABSENT_MASS 2 /* softmax also over the V - K_b absent slots (score 0) */

@@ -6,6 +6,7 @@ torch's devices, memory and streams.  There is no fallback: if the library is
 missing every entry point raises, naming the build command.
 """
 import ctypes
+import functools
 import os
 
 import torch
@@ -29,6 +30,7 @@ SIGNATURES = {
     "mb_abi_version": ([], _i),
     "mb_ema_query_scan": ([_p, _i64, _i64, _i, _i, _p, _i, _i64, _p, _p, _i, _p, _p, _p, _p, _p], _i),
     "mb_ema_boundary_states": ([_p, _i64, _i64, _i, _i, _p, _i, _p, _i, _i, _p, _i64, _p, _p, _i, _p], _i),
+    "mb_unique_rows": ([_p, _i64, _i64, _i, _i, _p, _i, _p, _p], _i),
     "mb_flash_ema_fwd": ([_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p,
                           _i, _i, _i, _i, _i, _i, _i, _i, _i, _i64, _i, _p, _p, _p, _p], _i),
     "mb_flash_ema_bwd": ([_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p,
@@ -71,7 +73,7 @@ class HipKernelError(RuntimeError):
 
 
 class HipLibraryMissing(RuntimeError):
-    """libmathbrain_hip.so is not built (python -m mathbrain_amd.build)."""
+    """libmathbrain_hip.so is not built (python -m mathbrain.build)."""
 
 
 def lib():
@@ -79,8 +81,8 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise HipLibraryMissing(
-                f"{LIB_PATH} is missing; build it with `python -m mathbrain_amd.build` "
-                "(mathbrain_amd has no CPU fallback)")
+                f"{LIB_PATH} is missing; build it with `python -m mathbrain.build` "
+                "(mathbrain has no CPU fallback)")
         L = ctypes.CDLL(LIB_PATH)
         for name, (args, res) in SIGNATURES.items():
             fn = getattr(L, name)
@@ -110,7 +112,28 @@ def stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def require_gpu(*tensors, what="mathbrain_amd"):
+def traced_op(name, fake):
+    """Decorator: registers ``fn`` as the torch custom op ``mathbrain::<name>`` whose shape
+    function (for fake / meta tensors) is ``fake``, and returns a callable that runs ``fn``
+    directly in eager mode and the registered op while torch.compile traces.  A traced
+    graph then holds the op instead of breaking at the ctypes call, and eager calls skip
+    the dispatcher (about 50 us per call, measured).  ``fn`` takes tensors, optional
+    tensors, ints, floats and bools (annotated) and returns new tensors."""
+    def deco(fn):
+        op = torch.library.custom_op(f"mathbrain::{name}", fn, mutates_args=())
+        op.register_fake(fake)
+
+        @functools.wraps(fn)
+        def call(*args):
+            if torch.compiler.is_compiling():
+                return op(*args)
+            return fn(*args)
+        call.op = op
+        return call
+    return deco
+
+
+def require_gpu(*tensors, what="mathbrain"):
     """Every tensor must live on one ROCm GPU: the product has no CPU path."""
     dev = None
     for t in tensors:

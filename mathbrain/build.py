@@ -1,9 +1,9 @@
 """Builds libmathbrain_hip.so, the gfx950 C-ABI library, in-tree with hipcc.
 
-    python -m mathbrain_amd.build          # or mathbrain_amd.build.build()
+    python -m mathbrain.build          # or mathbrain.build.build()
 
 Every .hip file under csrc/ is compiled for gfx950 only (objects go to
-mathbrain_amd/_build/) and linked into mathbrain_amd/libmathbrain_hip.so.  The
+mathbrain/_build/) and linked into mathbrain/libmathbrain_hip.so.  The
 library links the HIP runtime by soname (libamdhip64.so.7); in a process that
 has imported torch it binds to the runtime torch already loaded, so it shares
 torch's device, allocator and streams.

@@ -450,19 +450,23 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_bwd: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
     if (H % kBwdHeads)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: H=%d must be a multiple of %d", H, kBwdHeads);
-    if (B == 0 || L == 0) return MB_OK;
-    MB_REQUIRE(Q && dO && x && rhos && unique && O && LSE && W_pe && dQ && dW_pe,
-               "mb_flash_ema_bwd: null pointer");
-    MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds && dE_k && dE_v), "mb_flash_ema_bwd: null slot pointer");
-    hipStream_t st = (hipStream_t)stream;
-    // dE_k, dE_v and dW_pe are accumulated with atomics; every dQ element is written once.
+    // dE_k, dE_v and dW_pe are accumulated with atomics, so they are cleared first -- also
+    // when there is no step to accumulate (B or L zero), which leaves them zero; every dQ
+    // element is written once.
     const int64_t D = (int64_t)H * hd;
+    const int64_t erows = K > 0 ? (vr ? V_total : (int64_t)B * K) : 0;
+    MB_REQUIRE(dW_pe, "mb_flash_ema_bwd: null dW_pe");
+    MB_REQUIRE(erows == 0 || (dE_k && dE_v), "mb_flash_ema_bwd: null dE_k / dE_v");
+    hipStream_t st = (hipStream_t)stream;
     if ((rc = zero_fill(dW_pe, (int64_t)N * D, st))) return rc;
-    if (K > 0) {
-        const int64_t rows = vr ? V_total : (int64_t)B * K;
-        if ((rc = zero_fill(dE_k, rows * D, st))) return rc;
-        if ((rc = zero_fill(dE_v, rows * D, st))) return rc;
+    if (erows > 0) {
+        if ((rc = zero_fill(dE_k, erows * D, st))) return rc;
+        if ((rc = zero_fill(dE_v, erows * D, st))) return rc;
     }
+    if (B == 0 || L == 0) return MB_OK;
+    MB_REQUIRE(Q && dO && x && rhos && unique && O && LSE && W_pe && dQ,
+               "mb_flash_ema_bwd: null pointer");
+    MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_bwd: null slot pointer");
     const int NS = (N + 31) / 32;
     if (hd == 64) {
         if (NS == 1) return launch_bwd<64, 1, 4>(a, vr, st);

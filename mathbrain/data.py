@@ -37,12 +37,12 @@ def _device(device):
     if device is None:
         if not torch.cuda.is_available():
             raise NotImplementedError(
-                "mathbrain_amd.data builds samples on an MI355X GPU; none is visible "
+                "mathbrain.data builds samples on an MI355X GPU; none is visible "
                 "(this implementation has no CPU path)")
         return torch.device("cuda", torch.cuda.current_device())
     device = torch.device(device)
     if device.type != "cuda":
-        raise NotImplementedError(f"mathbrain_amd.data: device {device} is not a GPU; "
+        raise NotImplementedError(f"mathbrain.data: device {device} is not a GPU; "
                                   "this implementation has no CPU path")
     return device
 

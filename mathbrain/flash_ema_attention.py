@@ -11,7 +11,7 @@ the O(L V N D) work, and it is differentiable (the reference's in-place state up
 blocks autograd).  pe_proj must have no bias, as in the model (model.py:44): with a bias
 absent slots would not gate to zero.
 """
-from .flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
+from .triton_flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
 
 
 def flash_ema_forward(Q, x, E_k_slots, E_v_slots, rhos, pe_proj, n_heads, use_silu=True):

@@ -16,9 +16,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ema_query import compute_query_ema_history
-from .flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
-from .fused_gating import fused_apply_symmetric_query_gating
+from .triton_ema_query import compute_query_ema_history
+from .triton_flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
+from .triton_fused_gating import fused_apply_symmetric_query_gating
 from .layernorm import layer_norm
 from .rmsnorm import rms_norm
 from .swiglu import swiglu_product
@@ -57,7 +57,8 @@ class SlotAttentionLayer(nn.Module):
     (model.py:32-102): memory = ln_kv(E[slots]), K = k_proj(memory), V = v_proj(memory),
     keys and values gated by SiLU(pe_proj(C)) inside the flash-EMA kernel."""
 
-    def __init__(self, d_model: int, n_heads: int, dropout: float, n_scales: int, use_silu: bool = True):
+    def __init__(self, d_model: int, n_heads: int, dropout: float, n_scales: int, use_silu: bool = True,
+                 absent_mass: bool = True):
         super().__init__()
         assert d_model % n_heads == 0
         self.n_heads = n_heads
@@ -71,6 +72,9 @@ class SlotAttentionLayer(nn.Module):
         self.ln_q = nn.LayerNorm(d_model)
         self.resid_dropout = nn.Dropout(dropout)
         self.use_silu = use_silu
+        # softmax over all V slots (the dense PyTorch reference) or over the valid slots only
+        # (the reference's Triton kernel): see FlashEMAFunction
+        self.absent_mass = absent_mass
 
     def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None,
                 E_active=None):
@@ -101,7 +105,8 @@ class SlotAttentionLayer(nn.Module):
         Q_mha = Q_t.view(B, L, H, hd).transpose(1, 2)
         W_pe_t = self.pe_proj.weight.t()
         out_mha = FlashEMAFunction.apply(Q_mha, x, E_k_active, E_v_active, W_pe_t, rhos,
-                                         E_slots.shape[0], unique_tensor, K_max, C_bounds, self.use_silu)
+                                         E_slots.shape[0], unique_tensor, K_max, C_bounds, self.use_silu,
+                                         64, self.absent_mass)
         out = out_mha.transpose(1, 2).reshape(B, L, D)
         out = self.o_proj(out)
         return self.resid_dropout(out)
@@ -110,10 +115,10 @@ class SlotAttentionLayer(nn.Module):
 class SlotTransformerBlock(nn.Module):
     """model.py:105-116."""
 
-    def __init__(self, d_model, n_heads, d_ff, dropout, n_scales, use_silu=True):
+    def __init__(self, d_model, n_heads, d_ff, dropout, n_scales, use_silu=True, absent_mass=True):
         super().__init__()
         self.attn_norm = RMSNorm(d_model)
-        self.attn = SlotAttentionLayer(d_model, n_heads, dropout, n_scales, use_silu)
+        self.attn = SlotAttentionLayer(d_model, n_heads, dropout, n_scales, use_silu, absent_mass)
         self.ffn_norm = RMSNorm(d_model)
         self.ffn = SwiGLU(d_model, d_ff)
 
@@ -137,7 +142,7 @@ class SlotTransformerLM(nn.Module):
     """
 
     def __init__(self, vocab_size, d_model, n_layers, n_heads, N=16, dropout=0.1, use_silu=True,
-                 ema_dropout=0.0, min_hl=1.0, max_hl=2048.0):
+                 ema_dropout=0.0, min_hl=1.0, max_hl=2048.0, absent_mass=True):
         super().__init__()
         self.vocab_size = vocab_size
         self.d_model = d_model
@@ -149,7 +154,7 @@ class SlotTransformerLM(nn.Module):
         self.embed = nn.Embedding(vocab_size, d_model)
         d_ff = 256 * ((int(8 * d_model / 3) + 255) // 256)
         self.layers = nn.ModuleList([
-            SlotTransformerBlock(d_model, n_heads, d_ff, dropout, self.n_scales, use_silu)
+            SlotTransformerBlock(d_model, n_heads, d_ff, dropout, self.n_scales, use_silu, absent_mass)
             for _ in range(n_layers)
         ])
         self.final_norm = RMSNorm(d_model)
@@ -167,11 +172,11 @@ class SlotTransformerLM(nn.Module):
                 "(the reference's CPU path is its dense PyTorch fallback)")
         E_slots = self.embed.weight
         x_q = self.embed(x)
-        # scans hoisted once for all layers (model.py:157, 162-180)
-        C_seq = compute_query_ema_history(x, self.ema_rhos, self.vocab_size, c_base, unique_slots)
-        if self.ema_dropout > 0 and self.training:
-            C_seq = F.dropout(C_seq, p=self.ema_dropout, training=True)
         if unique_slots is not None and pad_mask is not None:
+            # -1 marks the collate padding on both sides.  The reference passes the padded
+            # list (pad id 0) to the query scan (model.py:157), where a padding entry can
+            # overwrite a real token 0's carried row with zeros while the key side keeps it
+            # (model.py:167-180); with the masked list the two sides agree.
             unique_tensor = unique_slots.masked_fill(~pad_mask, -1)
             # K_max: the slot list's width (at least 16).  The reference reads back the largest
             # valid count instead (model.py:169, a host sync every step) and cuts the list
@@ -179,6 +184,7 @@ class SlotTransformerLM(nn.Module):
             # skip a row's trailing padding slots either way.
             K_max = max(unique_tensor.shape[1], 16)
             c_base_kv = c_base[:, :K_max, :] if c_base is not None else None
+            C_seq = compute_query_ema_history(x, self.ema_rhos, self.vocab_size, c_base, unique_tensor)
             if unique_tensor.shape[1] < K_max:
                 # fewer than 16 slots in every row: pad the slot list to the 16 the
                 # reference's K_max floor asks for (model.py:170), with -1
@@ -187,8 +193,13 @@ class SlotTransformerLM(nn.Module):
                 if c_base_kv is not None:
                     c_base_kv = F.pad(c_base_kv, (0, 0, 0, pad))
         else:
-            unique_tensor, K_max = _build_unique_index(x, device)
+            C_seq = compute_query_ema_history(x, self.ema_rhos, self.vocab_size, c_base, unique_slots)
+            # each row's distinct tokens padded to the row length (model.py:177 reads the
+            # largest count back instead; the extra -1 slots are skipped by the kernels)
+            unique_tensor, K_max = _build_unique_index(x, device, width=x.shape[1])
             c_base_kv = None
+        if self.ema_dropout > 0 and self.training:
+            C_seq = F.dropout(C_seq, p=self.ema_dropout, training=True)
         C_bounds = precompute_boundaries(x, unique_tensor, self.ema_rhos, 64, c_init=c_base_kv)
         # The slot rows every layer gathers (model.py:63-64) are the same: gather once, so that
         # autograd sums the layers' gradients first and runs one embedding backward.  When

@@ -3,7 +3,7 @@
 CPU restatement of the reference's Per-Slot EMA hot path.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
 anything from this package, and only to check or to time the reference
-algorithm beside the HIP path.  Nothing in ``mathbrain_amd`` imports it; the
+algorithm beside the HIP path.  Nothing in ``mathbrain`` imports it; the
 product fails loudly when its HIP library is missing instead of falling back
 here.
 

@@ -46,8 +46,16 @@ def unique_index(x):
 
 
 def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_base=None,
-               pad_mask=None, use_silu=True, attention="sparse", gate_round=None):
-    """Logits [B, L, V] of SlotTransformerLM.forward (model.py:144-186)."""
+               pad_mask=None, use_silu=True, attention="sparse", gate_round=None,
+               absent_mass=True, mask_query_keys=True, t_eval=None):
+    """Logits [B, L, V] of SlotTransformerLM.forward (model.py:144-186).
+
+    ``absent_mass`` picks the attention's softmax (all V slots, or the valid slots only as
+    the reference's Triton kernel computes it).  ``mask_query_keys=False`` reproduces the
+    reference's query scan on the 0-padded slot list (model.py:157).  With ``t_eval`` the
+    logits are [B, len(t_eval), V] at those positions only: K/V come from the embedding
+    table and the counter states, not from other positions' hidden states, so every
+    position's logits depend on its own row and the states alone (exact)."""
     B, L = x.shape
     E = p["embed.weight"]
     dt = E.dtype
@@ -55,7 +63,19 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
     H = n_heads
     hd = D // H
     x_q = E[x]                                                          # :149
-    C_seq = torch.from_numpy(scan.query_scan(x, rhos, vocab_size, c_base, unique_slots)).to(dt)  # :157
+    keys = unique_slots
+    if unique_slots is not None and pad_mask is not None and mask_query_keys:
+        # the collate padding masked to -1 on the query side too (the reference passes the
+        # 0-padded list, model.py:157, which can overwrite token 0's carried row)
+        keys = unique_slots.masked_fill(~pad_mask, -1)
+    C_seq = torch.from_numpy(scan.query_scan(x, rhos, vocab_size, c_base, keys)).to(dt)  # :157
+    steps = list(range(L)) if t_eval is None else [int(t) for t in t_eval]
+    if t_eval is not None:
+        if attention != "sparse":
+            raise ValueError("t_eval needs the sparse attention")
+        x_q = x_q[:, steps]
+        C_seq = C_seq[:, steps]
+    Le = len(steps)
     if unique_slots is not None and pad_mask is not None:               # :163-174
         unique = unique_slots.masked_fill(~pad_mask, -1)
         K_max = max(int(pad_mask.sum(1).max()), 16)
@@ -79,10 +99,18 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
             mem = F.layer_norm(E_active, (D,), g("attn.ln_kv.weight"), g("attn.ln_kv.bias"))
             Ek = mem @ g("attn.k_proj.weight").t()                      # :67
             Ev = mem @ g("attn.v_proj.weight").t()                      # :68
-            Q_mha = Q_t.reshape(B, L, H, hd).transpose(1, 2)            # :81
-            O = att.sparse(Q_mha, x, Ek, Ev, g("attn.pe_proj.weight").t(), rhos.to(dt), vocab_size,
-                           unique, cb, use_silu=use_silu, absent_mass=True, gate_round=gate_round)
-            out = O.transpose(1, 2).reshape(B, L, D)                    # :87
+            Q_full = Q_t
+            if t_eval is not None:   # rows of the other steps are never read
+                Q_full = Q_t.new_zeros(B, L, D).index_copy(1, torch.tensor(steps), Q_t)
+            Q_mha = Q_full.reshape(B, L, H, hd).transpose(1, 2)          # :81
+            Wt = g("attn.pe_proj.weight").t()
+            if t_eval is None:
+                O = att.sparse(Q_mha, x, Ek, Ev, Wt, rhos.to(dt), vocab_size, unique, cb,
+                               use_silu=use_silu, absent_mass=absent_mass, gate_round=gate_round)
+            else:
+                O = _SampledAttention.apply(Q_mha, Ek, Ev, Wt, x, rhos.to(dt), vocab_size, unique,
+                                            cb, use_silu, absent_mass, gate_round, steps)
+            out = O.transpose(1, 2).reshape(B, Le, D)                   # :87
         elif attention == "dense":
             mem = F.layer_norm(E, (D,), g("attn.ln_kv.weight"), g("attn.ln_kv.bias"))   # :92
             Eks = mem @ g("attn.k_proj.weight").t()                     # :93
@@ -97,3 +125,30 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
         x_q = h
     x_q = rmsnorm(x_q, p["final_norm.weight"])                          # :185
     return x_q @ E.t()                                                  # :186, tied lm_head
+
+
+class _SampledAttention(torch.autograd.Function):
+    """attention.sparse evaluated at ``steps`` only, with the reference's closed-form
+    gradients (attention.sparse_backward_formulas, itself checked equal to autograd in
+    float64) as its backward, so no per-step autograd graph is kept.  Q [B, H, L, hd] (rows
+    of other steps unused); returns O [B, H, len(steps), hd]."""
+
+    @staticmethod
+    def forward(ctx, Q, Ek, Ev, Wt, x, rhos, V, unique, cb, use_silu, absent_mass, gate_round, steps):
+        with torch.no_grad():
+            O = att.sparse(Q, x, Ek, Ev, Wt, rhos, V, unique, cb, use_silu=use_silu,
+                           absent_mass=absent_mass, gate_round=gate_round, t_eval=steps)
+        ctx.save_for_backward(Q, Ek, Ev, Wt)
+        ctx.rest = (x, rhos, V, unique, cb, use_silu, absent_mass, gate_round, steps)
+        return O
+
+    @staticmethod
+    def backward(ctx, dO_e):
+        Q, Ek, Ev, Wt = ctx.saved_tensors
+        x, rhos, V, unique, cb, use_silu, absent_mass, gate_round, steps = ctx.rest
+        dO = Q.new_zeros(Q.shape)
+        dO[:, :, steps] = dO_e
+        dQ, dEk, dEv, dW = att.sparse_backward_formulas(
+            Q, x, Ek, Ev, Wt, rhos, V, unique, dO, cb, use_silu=use_silu, absent_mass=absent_mass,
+            gate_round=gate_round, t_eval=steps)
+        return (dQ, dEk.reshape(Ek.shape), dEv.reshape(Ev.shape), dW[: Wt.shape[0]]) + (None,) * 9

@@ -72,7 +72,7 @@ def scan_case():
 
 
 def attention_case():
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.synthetic import make_batch
     from oracle import attention as att
     B, L, V, H, hd, N = 2, 40, 120, 4, 32, 16
     d = make_batch(B, L, V, N, 48, seed=77, min_hl=2.0, max_hl=256.0)

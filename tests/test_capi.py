@@ -22,9 +22,9 @@ def declared_symbols():
 @pytest.fixture(scope="module")
 def lib():
     import torch  # noqa: F401  (the library binds to torch's HIP runtime)
-    from mathbrain_amd import _lib
+    from mathbrain import _lib
     if not os.path.exists(_lib.LIB_PATH):
-        from mathbrain_amd import build
+        from mathbrain import build
         build.build()
     return ctypes.CDLL(_lib.LIB_PATH)
 
@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_binding_table_matches_header():
-    from mathbrain_amd import _lib
+    from mathbrain import _lib
     assert set(_lib.SIGNATURES) == declared_symbols()
 
 
@@ -53,7 +53,7 @@ def test_abi_version_and_error_string(lib):
 
 def test_argument_errors_need_no_gpu(lib):
     """Argument checks run on the host before any launch and report through mb_last_error."""
-    from mathbrain_amd import _lib
+    from mathbrain import _lib
     L = _lib.lib()
     rc = L.mb_ema_query_scan(None, 0, 1, 1, 4, None, 0, 10, None, None, 0, None, None, None, None, None)
     assert rc == _lib.MB_ERR_INVALID_ARGUMENT
@@ -67,14 +67,14 @@ def test_argument_errors_need_no_gpu(lib):
 
 def test_cpu_tensors_are_rejected():
     import torch
-    from mathbrain_amd.ema_query import compute_query_ema_history
+    from mathbrain.triton_ema_query import compute_query_ema_history
     with pytest.raises(NotImplementedError, match="no CPU path"):
         compute_query_ema_history(torch.zeros(1, 4, dtype=torch.long), torch.ones(2), 10)
 
 
 def test_data_and_factored_argument_errors_need_no_gpu(lib):
     """The data-pipeline and factored entry points check sizes and workspace on the host."""
-    from mathbrain_amd import _lib
+    from mathbrain import _lib
     L = _lib.lib()
     assert L.mb_corpus_states_workspace(0, 64) == 0
     assert L.mb_corpus_states_workspace(1024, 64) == 1024 // 1024 * 64 * 3 * 4
@@ -100,7 +100,7 @@ def test_data_and_factored_argument_errors_need_no_gpu(lib):
 
 def test_factored_and_data_cpu_tensors_are_rejected():
     import torch
-    from mathbrain_amd.factored_ema import factored_ema_forward
+    from mathbrain.factored_ema import factored_ema_forward
     with pytest.raises(NotImplementedError, match="no CPU path"):
         factored_ema_forward(torch.zeros(1, 4, 8), torch.zeros(1, 4, dtype=torch.long),
                              torch.zeros(5, 8), torch.zeros(5, 8), torch.ones(2), torch.zeros(2, 8), 2)

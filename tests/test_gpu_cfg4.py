@@ -57,7 +57,7 @@ _DATA = {}
 
 def data():
     if not _DATA:
-        from mathbrain_amd.synthetic import make_batch
+        from mathbrain.synthetic import make_batch
         _DATA.update(make_batch(B, L, V, N, 4096, seed=44, pad_frac=0.1))
         assert int(_DATA["pad_len"].max()) > 0
     return _DATA
@@ -92,7 +92,7 @@ def masked_dO(seed, rows=None, steps=None):
 
 def run(w, x=None, unique=None, c_base=None, dO=None, stored_scores=False):
     """Boundary states, forward and (with dO) backward on the GPU; CPU results."""
-    from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
+    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
     d = data()
     x = d["x"] if x is None else x
     unique = d["unique"] if unique is None else unique

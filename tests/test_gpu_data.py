@@ -1,5 +1,5 @@
 """Parity of the device data pipeline (mb_corpus_states, mb_slot_lists, mb_slot_batch
-behind mathbrain_amd/data.py) with the CPU oracle of mathbrain/data.py: the corpus
+behind mathbrain/data.py) with the CPU oracle of mathbrain/data.py: the corpus
 states, the written files, every sample dict and collated batch, and the reference's
 own scenarios run end to end.  Integers, ids and masks bit-exact; float32 states and
 c_base to 1e-5 relative (each is a product or sum of powers of rho evaluated in another
@@ -30,14 +30,14 @@ def _close(got, want, rtol=RTOL, atol=1e-30):
 
 
 def _states(tokens, doc_ids, rhos):
-    from mathbrain_amd.data import corpus_states
+    from mathbrain.data import corpus_states
     return corpus_states(torch.from_numpy(np.asarray(tokens, np.int32)).cuda(),
                          torch.from_numpy(np.asarray(doc_ids, np.int32)).cuda(),
                          torch.from_numpy(np.asarray(rhos, np.float32)).cuda()).cpu().numpy()
 
 
 def _corpus_dir(docs, N, lo, hi):
-    from mathbrain_amd.data import preprocess_corpus
+    from mathbrain.data import preprocess_corpus
     d = tempfile.mkdtemp(prefix="mb_data_")
     preprocess_corpus(docs, d, N=N, min_hl=lo, max_hl=hi)
     return d
@@ -79,7 +79,7 @@ def _same_batch(got, want):
 
 @pytest.mark.parametrize("N", [1, 4, 16, 64, 100, 128])
 def test_gpu_corpus_states_match_oracle(N):
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.synthetic import zipf_corpus
     tokens, doc_ids = zipf_corpus(20000, 3000, median_len=700, seed=N)
     rhos = od.rhos_for(N, 1.0, 2048.0)
     print(f"corpus states T=20000 N={N}", flush=True)
@@ -113,7 +113,7 @@ def test_gpu_corpus_states_resets():
 
 def test_gpu_corpus_states_large_spot_check():
     # 4 M tokens of a 50257-id Zipf corpus: 400 positions against the float64 closed form
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.synthetic import zipf_corpus
     T, N = (1 << 22) + 17, 64
     tokens, doc_ids = zipf_corpus(T, 50257, median_len=3000, seed=7)
     rhos = od.rhos_for(N, 1.0, 2048.0)
@@ -132,7 +132,7 @@ def test_gpu_corpus_states_large_spot_check():
 
 def test_gpu_preprocess_corpus_files():
     # the reference's file format (data.py:242-320) with the reference's content
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.synthetic import zipf_corpus
     tokens, doc_ids = zipf_corpus(6000, 500, median_len=400, seed=3)
     docs = _docs_from(tokens, doc_ids)
     d = _corpus_dir(docs, 16, 1.0, 1024.0)
@@ -150,14 +150,14 @@ def test_gpu_preprocess_corpus_files():
 # ---- samples and batches ---------------------------------------------------------------------
 
 def _dataset(docs, N, lo, hi, block):
-    from mathbrain_amd.data import WikiTextMMapDataset
+    from mathbrain.data import WikiTextMMapDataset
     d = _corpus_dir(docs, N, lo, hi)
     return WikiTextMMapDataset(d, block_size=block, rhos=torch.from_numpy(od.rhos_for(N, lo, hi)))
 
 
 @pytest.mark.parametrize("seed,block", [(0, 4), (1, 17), (2, 64)])
 def test_gpu_dataset_items_match_oracle(seed, block):
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.synthetic import zipf_corpus
     tokens, doc_ids = zipf_corpus(3000, 200, median_len=300, seed=seed)
     ds = _dataset(_docs_from(tokens, doc_ids), 8, 1.0, 256.0, block)
     item = _oracle_for(ds)
@@ -168,7 +168,7 @@ def test_gpu_dataset_items_match_oracle(seed, block):
 
 @pytest.mark.parametrize("B", [1, 5, 17])
 def test_gpu_get_batch_matches_oracle_collate(B):
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.synthetic import zipf_corpus
     tokens, doc_ids = zipf_corpus(8000, 700, median_len=900, seed=10 + B)
     ds = _dataset(_docs_from(tokens, doc_ids), 12, 1.0, 512.0, 50)
     item = _oracle_for(ds)
@@ -181,7 +181,7 @@ def test_gpu_get_batch_matches_oracle_collate(B):
 
 def test_gpu_batch_zipf_full_vocab():
     # a configuration-2-like batch: 56 chunks of 512 + 1 tokens over 50257 ids, N = 64
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.synthetic import zipf_corpus
     tokens, doc_ids = zipf_corpus(300000, 50257, median_len=4000, seed=21)
     ds = _dataset(_docs_from(tokens, doc_ids), 64, 1.0, 4096.0, 512)
     item = _oracle_for(ds)
@@ -195,7 +195,7 @@ def test_gpu_batch_zipf_full_vocab():
 def test_gpu_reference_scenarios():
     from torch.utils.data import DataLoader
 
-    from mathbrain_amd.data import dynamic_collate_fn
+    from mathbrain.data import dynamic_collate_fn
     # tests/test_data_pipeline.py:61-103: c_base of token 1 in the continuation chunk
     ds = _dataset([[1, 2, 3] * 5], 2, 1.0, 4.0, 8)
     r = od.rhos_for(2, 1.0, 4.0)
@@ -229,8 +229,8 @@ def test_gpu_reference_scenarios():
 
 
 def test_gpu_slot_loader_matches_get_batch():
-    from mathbrain_amd.data import SlotBatchLoader, TokenBudgetSampler, dynamic_collate_fn
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.data import SlotBatchLoader, TokenBudgetSampler, dynamic_collate_fn
+    from mathbrain.synthetic import zipf_corpus
     tokens, doc_ids = zipf_corpus(5000, 400, median_len=500, seed=5)
     ds = _dataset(_docs_from(tokens, doc_ids), 8, 1.0, 256.0, 40)
     sampler = TokenBudgetSampler(ds, token_budget=400, shuffle=False)
@@ -248,8 +248,8 @@ def test_gpu_slot_loader_matches_get_batch():
 
 def test_gpu_batch_feeds_the_model():
     # the collated batch goes straight into SlotTransformerLM as train.py passes it
-    from mathbrain_amd.model import SlotTransformerLM
-    from mathbrain_amd.synthetic import zipf_corpus
+    from mathbrain.model import SlotTransformerLM
+    from mathbrain.synthetic import zipf_corpus
     tokens, doc_ids = zipf_corpus(4000, 300, median_len=600, seed=9)
     ds = _dataset(_docs_from(tokens, doc_ids), 16, 1.0, 1024.0, 64)
     chunks, us, pm, inv, cb, K, doc = ds.get_batch(list(range(min(6, len(ds)))))

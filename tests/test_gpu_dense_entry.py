@@ -23,7 +23,7 @@ def rel(a, b):
 
 
 def test_gpu_dense_entry_point_matches_dense_oracle():
-    from mathbrain_amd.flash_ema_attention import flash_ema_forward
+    from mathbrain.flash_ema_attention import flash_ema_forward
     B, L, D, H, N, V = 2, 128, 128, 4, 16, 1000
     g = torch.Generator().manual_seed(0)
     x = torch.randint(0, V, (B, L), generator=g)
@@ -50,7 +50,7 @@ def test_gpu_dense_entry_point_matches_dense_oracle():
 
 
 def test_gpu_dense_entry_rejects_a_gate_bias():
-    from mathbrain_amd.flash_ema_attention import flash_ema_forward
+    from mathbrain.flash_ema_attention import flash_ema_forward
     pe = torch.nn.Linear(4, 32).cuda()
     with pytest.raises(NotImplementedError, match="bias"):
         flash_ema_forward(torch.zeros(1, 8, 32).cuda(), torch.zeros(1, 8, dtype=torch.long).cuda(),
@@ -59,7 +59,7 @@ def test_gpu_dense_entry_rejects_a_gate_bias():
 
 
 def test_gpu_query_scan_pt_name():
-    from mathbrain_amd.ema_query import compute_query_ema_history_pt
+    from mathbrain.triton_ema_query import compute_query_ema_history_pt
     rng = np.random.default_rng(3)
     x = rng.integers(0, 20, (2, 50))
     rh = np.array([0.9, 0.6, 0.3], np.float32)

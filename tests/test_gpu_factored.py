@@ -1,5 +1,5 @@
 """Parity of the HIP factored linear EMA (mb_factored_* behind
-mathbrain_amd/factored_ema.py) with the CPU oracle of factored_ema.py (oracle/factored.py,
+mathbrain/factored_ema.py) with the CPU oracle of factored_ema.py (oracle/factored.py,
 float64): outputs and the gradients of Q, E_k, E_v and W_pe, with and without c_base, at
 tile edges and at the model's head shape, plus the layer.  Tolerance (fp32 kernels against
 float64): 1e-4 relative, norm-wise (max |diff| / max |ref|)."""
@@ -39,7 +39,7 @@ def make(B, L, V, H, hd, N, K, seed, cbase=True, scale=0.5):
 
 
 def run_both(args, kw, dO_seed=99):
-    from mathbrain_amd.factored_ema import factored_ema_forward
+    from mathbrain.factored_ema import factored_ema_forward
     Q, x, Ek, Ev, rhos, W, H = args
     leaves = [t.clone().requires_grad_(True) for t in (Q, Ek, Ev, W)]
     want = of.closed_form(leaves[0], x, leaves[1], leaves[2], rhos, leaves[3], H, **kw)
@@ -84,7 +84,7 @@ def test_gpu_factored_model_shape():
 
 def test_gpu_factored_matches_loop_restatement():
     # the step-by-step restatement of factored_ema.py:22-96 (not only its closed form)
-    from mathbrain_amd.factored_ema import factored_ema_forward
+    from mathbrain.factored_ema import factored_ema_forward
     (Q, x, Ek, Ev, rhos, W, H), kw = make(2, 70, 30, 2, 32, 6, 12, seed=11)
     want = of.loop_forward(Q, x, Ek, Ev, rhos, W, H, **kw)
     f = lambda t: t.to(torch.float32).cuda()
@@ -97,7 +97,7 @@ def test_gpu_factored_matches_loop_restatement():
 def test_gpu_factored_layer_matches_reference_composition():
     # FactoredLinearEMALayer (factored_ema.py:99-146) against the same composition with the
     # oracle in float64
-    from mathbrain_amd.factored_ema import FactoredLinearEMALayer
+    from mathbrain.factored_ema import FactoredLinearEMALayer
     torch.manual_seed(0)
     B, L, V, D, H, N, K = 2, 48, 40, 128, 2, 8, 10
     layer = FactoredLinearEMALayer(D, H, 0.0, N).cuda()

@@ -36,7 +36,7 @@ def norm_err(got, want):
 
 def make_case(B, L, V, H, hd, N, warmup=0, seed=0, uniform=False, min_hl=1.0, max_hl=4096.0,
               qs=1.0, es=0.5, ws=0.3, Br=64, pad_slots=0):
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.synthetic import make_batch
     d = make_batch(B, L, V, N, warmup, seed=seed, uniform=uniform, min_hl=min_hl, max_hl=max_hl)
     g = torch.Generator().manual_seed(seed + 1)
     unique, c_base = d["unique"], d["c_base"]
@@ -64,7 +64,7 @@ def make_case(B, L, V, H, hd, N, warmup=0, seed=0, uniform=False, min_hl=1.0, ma
 
 
 def gpu_forward(c, use_silu=True, absent_mass=True):
-    from mathbrain_amd.flash_ema import flash_ema_forward
+    from mathbrain.triton_flash_ema import flash_ema_forward
     cu = lambda t: t.cuda()
     O, LSE, *_ = flash_ema_forward(cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]), cu(c["W"]),
                                    cu(c["rhos"]), c["V"], cu(c["unique"]), c["K"], cu(c["Cb"]),
@@ -163,7 +163,7 @@ def test_fwd_row_without_slots():
 
 
 def test_fwd_rejects_unsupported_shapes():
-    from mathbrain_amd._lib import HipKernelError
+    from mathbrain._lib import HipKernelError
     c = make_case(1, 16, 50, 4, 32, 16, warmup=0, seed=1)
     c["Q"] = torch.randn(1, 4, 16, 48)
     c["E_k"] = torch.randn(1, c["K"], 192)
@@ -177,7 +177,7 @@ def test_fwd_rejects_unsupported_shapes():
 
 def gpu_backward(c, dO, use_silu=True, absent_mass=True, stored_scores=True):
     """Backward through the C ABI, with the forward's stored scores or recomputing them."""
-    from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward
+    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward
     cu = lambda t: t.cuda()
     O, LSE, _, _, _, S2 = flash_ema_forward(
         cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]), cu(c["W"]), cu(c["rhos"]), c["V"],
@@ -264,7 +264,7 @@ def test_bwd_flags(use_silu, absent_mass, stored_scores):
 
 def test_fwd_scores_output():
     """The optional scores output is s * log2(e) = LSE-consistent log-softmax numerators."""
-    from mathbrain_amd.flash_ema import flash_ema_forward
+    from mathbrain.triton_flash_ema import flash_ema_forward
     c = make_case(2, 50, 120, 4, 32, 16, warmup=40, seed=8, pad_slots=3)
     cu = lambda t: t.cuda()
     O, LSE, _, _, _, S2 = flash_ema_forward(cu(c["Q"]), cu(c["x"]), cu(c["E_k"]), cu(c["E_v"]),
@@ -280,8 +280,8 @@ def test_fwd_scores_output():
 
 
 def test_autograd_function_matches_direct_calls():
-    from mathbrain_amd import flash_ema
-    from mathbrain_amd.flash_ema import FlashEMAFunction
+    from mathbrain import triton_flash_ema as flash_ema
+    from mathbrain.triton_flash_ema import FlashEMAFunction
     c = make_case(2, 64, 300, 8, 64, 64, warmup=200, seed=5)
     g = torch.Generator().manual_seed(9)
     dO = torch.randn(c["Q"].shape, generator=g)
@@ -309,7 +309,7 @@ def test_vocab_table_rows_match_gathered_rows(pad_slots):
     one variant and not the other, so the two agree to the gate's fp16 rounding (1e-4 here,
     measured 9e-6), not bit for bit, and both stay within the kernel-rounding bar of the
     oracle."""
-    from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward
+    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward
     c = make_case(3, 90, 40, 8, 64, 16, warmup=60, seed=31, pad_slots=pad_slots)
     g = torch.Generator().manual_seed(32)
     D = c["W"].shape[1]
@@ -353,7 +353,7 @@ def test_vocab_table_rows_match_gathered_rows(pad_slots):
 
 
 def test_vocab_table_shape_is_checked():
-    from mathbrain_amd.flash_ema import flash_ema_forward
+    from mathbrain.triton_flash_ema import flash_ema_forward
     c = make_case(2, 40, 30, 8, 64, 16, seed=33)
     cu = lambda t: t.cuda()
     bad = torch.randn(c["V"] + 1, c["W"].shape[1]).cuda()

@@ -1,0 +1,141 @@
+"""Parity at the full shapes of configurations 2 and 5, on the launches the benchmarks time.
+
+Configuration 2 (one flash-EMA layer, B=56, T=512, 8 x 64 heads, N=64, V=50257, Zipf(1.1)
+tokens, c_base from a 4096-token warm-up, half-lives 1..4096, N(0, 0.02) weights): the
+whole batch goes through the boundary scan, forward and backward kernels in one launch
+each; dO is nonzero only on two sequences (the one with most slots and one more), so that
+every gradient, dW_pe summed over the batch included, equals what the exact float64 oracle
+computes for those two sequences at all 512 steps.  Tolerance 2e-2 norm-wise (the bf16
+bar: the gate GEMM takes fp16 operands and the dW_pe product bf16 ones).
+
+Configuration 5 (SlotTransformerLM training step: 6 layers, d_model 512, 8 x 64 heads,
+N=64, V=50257, B=56, T=512, synthetic lognormal documents with carried c_base, history-
+expanded slot lists): the full batch forward and backward, with the loss restricted to 64
+positions of two sequences; logits there and every parameter gradient against the model
+oracle evaluated at those positions only (exact: keys and values come from the embedding
+table and the counter states, never from other positions' hidden states).  Bars: 2e-2
+against the exact float64 oracle; 1e-4 against the oracle with the kernel's gate rounding
+(1e-2 for pe_proj.weight, whose attention part is contracted from bf16 operands).
+"""
+import pytest
+import torch
+
+from oracle import attention as att
+from oracle import model as omodel
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-2
+
+
+def norm_err(got, want):
+    got = got.detach().double().cpu()
+    want = want.detach().double().cpu()
+    return float((got - want).abs().max() / want.abs().max().clamp(min=1e-300))
+
+
+def test_cfg2_full_batch_two_sequences_all_steps():
+    from mathbrain.synthetic import make_batch
+    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
+    B, L, H, HD, N, V = 56, 512, 8, 64, 64, 50257
+    D = H * HD
+    d = make_batch(B, L, V, N, 4096, seed=2)
+    K = d["unique"].shape[1]
+    rows = [int(d["counts"].argmax()), 17]
+    print(f"cfg2 full batch: K_max {K}, sum K_b {int(d['counts'].sum())}, rows {rows}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    Q = torch.randn(B, H, L, HD, generator=g) * 0.02
+    Ek = torch.randn(B, K, D, generator=g) * 0.02
+    Ev = torch.randn(B, K, D, generator=g) * 0.02
+    W = torch.randn(N, D, generator=g) * 0.02
+    dO = torch.zeros(B, H, L, HD)
+    dO[rows] = torch.randn(len(rows), H, L, HD, generator=g)
+    cu = lambda t: t.cuda()
+    xg, ug, rg = cu(d["x"]), cu(d["unique"]), cu(d["rhos"])
+    Cb = precompute_boundaries(xg, ug, rg, 64, cu(d["c_base"]))
+    O, LSE, *_ = flash_ema_forward(cu(Q), xg, cu(Ek), cu(Ev), cu(W), rg, V, ug, K, Cb)
+    dQ, dEk, dEv, dW = flash_ema_backward(cu(Q), xg, cu(Ek), cu(Ev), cu(W), rg, V, ug, Cb, O, LSE,
+                                          cu(dO))
+    torch.cuda.synchronize()
+    assert torch.isfinite(O).all() and torch.isfinite(LSE).all()
+    others = [b for b in range(B) if b not in rows]
+    for t in (dQ, dEk, dEv):
+        assert torch.count_nonzero(t[others]) == 0
+    f = torch.float64
+    r = torch.tensor(rows)
+    args = (Q[r].to(f), d["x"][r], Ek[r].to(f), Ev[r].to(f), W.to(f), d["rhos"].to(f), V, d["unique"][r])
+    Ow, LSEw = att.sparse(*args, d["c_base"][r].to(f), return_lse=True)
+    gw = att.sparse_backward_formulas(*args, dO[r].to(f), d["c_base"][r].to(f))
+    errs = {"O": norm_err(O[r], Ow), "LSE": norm_err(LSE[r], LSEw), "dQ": norm_err(dQ[r], gw[0]),
+            "dE_k": norm_err(dEk[r], gw[1]), "dE_v": norm_err(dEv[r], gw[2]), "dW_pe": norm_err(dW, gw[3])}
+    print("cfg2 full batch vs float64 oracle: " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert max(errs.values()) < TOL_BF16, errs
+
+
+_CFG5 = {}
+
+
+def cfg5():
+    """The configuration-5 model (random init, seed 0) and one synthetic document batch."""
+    if not _CFG5:
+        from mathbrain.model import SlotTransformerLM
+        from mathbrain.synthetic import make_doc_batch
+        V, D, NL, H, N, B, T = 50257, 512, 6, 8, 64, 56, 512
+        torch.manual_seed(0)
+        m = SlotTransformerLM(V, D, NL, H, N=N, dropout=0.0, min_hl=1.0, max_hl=4096.0)
+        d = make_doc_batch(B, T, V, N, min_hl=1.0, max_hl=4096.0, seed=5)
+        assert torch.allclose(m.ema_rhos, d["rhos"])
+        _CFG5.update(model=m, data=d, dims=(V, D, NL, H, N, B, T))
+    return _CFG5
+
+
+def _cfg5_gpu_run(rows, steps, R):
+    """Full-batch forward + backward of the loss sum over (rows x steps) of logits * R."""
+    c = cfg5()
+    m, d = c["model"], c["data"]
+    m = m.cuda()
+    m.zero_grad(set_to_none=True)
+    pm = d["unique"] >= 0
+    logits = m(d["x"].cuda(), d["unique"].cuda(), None, d["c_base"].cuda(), None, pm.cuda())
+    sel = logits[torch.tensor(rows).cuda()][:, torch.tensor(steps).cuda()]
+    (sel * R.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    grads = {k: p.grad.detach().cpu() for k, p in m.named_parameters()}
+    out = sel.detach().cpu()
+    del logits, sel
+    m.cpu()
+    torch.cuda.empty_cache()
+    return out, grads
+
+
+@pytest.mark.parametrize("gate_round,tol", [(None, TOL_BF16), ("f16", 1e-4)])
+def test_cfg5_full_model_sampled_positions(gate_round, tol):
+    c = cfg5()
+    m, d = c["model"], c["data"]
+    V, D, NL, H, N, B, T = c["dims"]
+    lens = d["lengths"]
+    rows = [int(d["counts"].argmax()), int(torch.argsort(lens, descending=True)[1])]
+    if rows[0] == rows[1]:
+        rows[1] = int(torch.argsort(lens, descending=True)[2])
+    n = int(min(lens[rows[0]], lens[rows[1]]))
+    g = torch.Generator().manual_seed(6)
+    steps = sorted(torch.randperm(n, generator=g)[:64].tolist())
+    R = torch.randn(len(rows), len(steps), V, generator=g)
+    print(f"cfg5: K_max {d['unique'].shape[1]}, rows {rows} (K_b {[int(d['counts'][r]) for r in rows]}), "
+          f"{len(steps)} steps, gate_round={gate_round}", flush=True)
+    got, grads = _cfg5_gpu_run(rows, steps, R)
+    r = torch.tensor(rows)
+    f = torch.float64
+    p = {k: v.detach().to(f).requires_grad_() for k, v in m.state_dict().items()
+         if k not in ("ema_rhos", "lm_head.weight")}
+    want = omodel.lm_forward(p, d["x"][r], NL, H, m.ema_rhos, V, unique_slots=d["unique"][r],
+                             c_base=d["c_base"][r].to(f), pad_mask=d["unique"][r] >= 0,
+                             gate_round=gate_round, t_eval=steps)
+    (want * R.to(f)).sum().backward()
+    errs = {"logits": norm_err(got, want)}
+    errs.update({k: norm_err(grads[k], v.grad) for k, v in p.items()})
+    worst = sorted(errs.items(), key=lambda kv: -kv[1])[:4]
+    print(f"cfg5 gate_round={gate_round}: logits {errs['logits']:.2e}; worst {worst}")
+    for k, e in errs.items():
+        bar = tol if (gate_round is None or not k.endswith("pe_proj.weight")) else 1e-2
+        assert e < bar, (k, e)

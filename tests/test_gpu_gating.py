@@ -25,7 +25,7 @@ def norm_err(got, want):
 
 
 def case(B, L, D, N, V=500, seed=0, ws=0.02):
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.synthetic import make_batch
     d = make_batch(B, L, V, N, 256, seed=seed)
     C = torch.from_numpy(oscan.query_scan(d["x"], d["rhos"], V, d["c_base"], d["unique"])).float()
     g = torch.Generator().manual_seed(seed + 1)
@@ -52,7 +52,7 @@ def oracle_grads(c, use_silu):
 @pytest.mark.parametrize("D,N", [(128, 16), (512, 64), (384, 128), (1000, 7)])
 @pytest.mark.parametrize("use_silu", [True, False])
 def test_folded_projection_fwd_bwd(D, N, use_silu):
-    from mathbrain_amd.fused_gating import GatedQueryFunction
+    from mathbrain.triton_fused_gating import GatedQueryFunction
     c = case(2, 67, D, N, seed=D + N)
     want_y, want_g = oracle_grads(c, use_silu)
     x_q = c["x_q"].cuda().requires_grad_()
@@ -73,7 +73,7 @@ def test_folded_projection_fwd_bwd(D, N, use_silu):
 def test_fused_gating_function_matches_reference_formulas(use_silu):
     """FusedGatingFunction keeps the reference autograd signature: gradients of
     (x_q, p_pre, bias, ln_w, ln_b) equal the reference kernel's closed form."""
-    from mathbrain_amd.fused_gating import FusedGatingFunction
+    from mathbrain.triton_fused_gating import FusedGatingFunction
     c = case(3, 41, 512, 64, seed=7)
     dt = torch.float64
     p_pre = c["C"] @ c["W"].t()
@@ -93,7 +93,7 @@ def test_fused_gating_function_matches_reference_formulas(use_silu):
 def test_module_entry_point_and_strided_rows():
     """fused_apply_symmetric_query_gating with the model's modules, a strided x_q view and
     a single row; equals the reference CPU branch composed from torch modules."""
-    from mathbrain_amd.fused_gating import fused_apply_symmetric_query_gating
+    from mathbrain.triton_fused_gating import fused_apply_symmetric_query_gating
     D, N = 256, 32
     c = case(2, 33, D, N, seed=3)
     pe = nn.Linear(N, D, bias=False)
@@ -116,7 +116,7 @@ def test_module_entry_point_and_strided_rows():
 
 
 def test_empty_rows():
-    from mathbrain_amd.fused_gating import GatedQueryFunction
+    from mathbrain.triton_fused_gating import GatedQueryFunction
     x = torch.zeros(0, 5, 64, device="cuda", requires_grad=True)
     y = GatedQueryFunction.apply(x, torch.zeros(0, 5, 8, device="cuda"),
                                  torch.zeros(8, 64, device="cuda"), torch.ones(64, device="cuda"),

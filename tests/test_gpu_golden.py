@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _hip_scan(x, rhos, V, c_init=None, keys=None, doc=None):
-    from mathbrain_amd.ema_query import compute_query_ema_history
+    from mathbrain.triton_ema_query import compute_query_ema_history
     cu = lambda a: None if a is None else torch.as_tensor(a).cuda()
     return compute_query_ema_history(cu(x), cu(rhos), V, cu(c_init), cu(keys), cu(doc)).cpu().numpy()
 
@@ -27,7 +27,7 @@ def test_gpu_reference_kats():
 
 
 def test_gpu_scan_fixture():
-    from mathbrain_amd.flash_ema import precompute_boundaries
+    from mathbrain.triton_flash_ema import precompute_boundaries
     f = np.load(os.path.join(GOLD, "scan_small.npz"))
     C = _hip_scan(f["x"], f["rhos"], int(f["x"].max()) + 1, f["c_init"], f["keys"], f["doc"])
     np.testing.assert_allclose(C, f["C_seq"], rtol=1e-5, atol=1e-30)
@@ -38,7 +38,7 @@ def test_gpu_scan_fixture():
 
 
 def test_gpu_attention_fixture():
-    from mathbrain_amd.flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
+    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
     f = {k: torch.from_numpy(v).cuda() for k, v in np.load(os.path.join(GOLD, "attention_small.npz")).items()}
     V = int(f["V"])
     K = f["unique"].shape[1]
@@ -57,7 +57,7 @@ def test_gpu_data_fixture():
     # the device data pipeline against the committed corpus: states, chunk list, one batch
     import tempfile
 
-    from mathbrain_amd.data import WikiTextMMapDataset, corpus_states
+    from mathbrain.data import WikiTextMMapDataset, corpus_states
     f = np.load(os.path.join(GOLD, "data_small.npz"))
     st = corpus_states(torch.from_numpy(f["tokens"]).cuda(), torch.from_numpy(f["doc_ids"]).cuda(),
                        torch.from_numpy(f["rhos"]).cuda())
@@ -77,7 +77,7 @@ def test_gpu_data_fixture():
 
 
 def test_gpu_factored_fixture():
-    from mathbrain_amd.factored_ema import factored_ema_forward
+    from mathbrain.factored_ema import factored_ema_forward
     f = {k: torch.from_numpy(v).cuda() for k, v in np.load(os.path.join(GOLD, "factored_small.npz")).items()}
     leaves = [f[k].clone().requires_grad_(True) for k in ("Q", "E_k", "E_v", "W")]
     O = factored_ema_forward(leaves[0], f["x"], leaves[1], leaves[2], f["rhos"], leaves[3], int(f["H"]),

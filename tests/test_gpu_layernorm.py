@@ -1,5 +1,5 @@
 """LayerNorm on the HIP kernels (mb_layernorm_fwd / mb_layernorm_bwd behind
-mathbrain_amd/layernorm.py, the model's ln_kv) against F.layer_norm evaluated by torch
+mathbrain/layernorm.py, the model's ln_kv) against F.layer_norm evaluated by torch
 autograd in float64: output, dx, dweight and dbias, norm-wise (max |diff| / max |ref|)
 within 1e-5 (fp32 kernels), at widths around the 64-lane tiles, ragged row counts and the
 model's vocabulary-table shape."""
@@ -21,7 +21,7 @@ def rel(a, b):
 @pytest.mark.parametrize("shape", [(5, 3), (3, 63), (7, 64), (2, 3, 100), (9, 128), (6, 1000),
                                    (5, 1024), (50257, 512)])
 def test_layernorm_matches_torch_float64(shape):
-    from mathbrain_amd.layernorm import layer_norm
+    from mathbrain.layernorm import layer_norm
     g = torch.Generator().manual_seed(sum(shape))
     D = shape[-1]
     x = torch.randn(*shape, generator=g, dtype=torch.float64) * 2 + 0.5
@@ -43,8 +43,8 @@ def test_layernorm_matches_torch_float64(shape):
 
 
 def test_layernorm_rejects_wide_rows_and_cpu_tensors():
-    from mathbrain_amd import _lib
-    from mathbrain_amd.layernorm import layer_norm
+    from mathbrain import _lib
+    from mathbrain.layernorm import layer_norm
     with pytest.raises(_lib.HipKernelError):
         layer_norm(torch.randn(2, 1025, device="cuda"), torch.ones(1025, device="cuda"),
                    torch.zeros(1025, device="cuda"), 1e-5)

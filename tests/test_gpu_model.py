@@ -28,13 +28,13 @@ def norm_err(got, want):
 
 
 def build(V=500, D=128, n_layers=2, H=4, N=16, seed=0, **kw):
-    from mathbrain_amd.model import SlotTransformerLM
+    from mathbrain.model import SlotTransformerLM
     torch.manual_seed(seed)
     return SlotTransformerLM(V, D, n_layers, H, N=N, dropout=0.0, max_hl=1024.0, **kw)
 
 
 def batch(B, L, V, N, seed, warmup=200):
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.synthetic import make_batch
     d = make_batch(B, L, V, N, warmup, seed=seed, max_hl=1024.0)
     return d["x"], d["unique"], d["c_base"], d["unique"] >= 0
 
@@ -128,3 +128,112 @@ def test_model_vocab_table_path_vs_oracle(kv_table):
     for k, v in p.items():
         tol = 1e-2 if k.endswith("pe_proj.weight") else 1e-4
         assert norm_err(grads[k].grad, v.grad) < tol, (kv_table, k)
+
+
+@pytest.mark.parametrize("absent_mass", [True, False])
+def test_model_absent_mass_switch_vs_oracle(absent_mass):
+    """SlotTransformerLM(absent_mass=...) threads the softmax choice into every layer's
+    attention: all V slots (the dense reference) or the valid slots only (the reference's
+    Triton kernel); logits and gradients match the oracle under each, and the two differ."""
+    V, D, n_layers, H, N, B, L = 400, 128, 2, 4, 16, 2, 64
+    torch.manual_seed(11)
+    from mathbrain.model import SlotTransformerLM
+    m = SlotTransformerLM(V, D, n_layers, H, N=N, dropout=0.0, max_hl=1024.0,
+                          absent_mass=absent_mass).cuda()
+    x, uniq, cb, pm = batch(B, L, V, N, seed=12)
+    g = torch.Generator().manual_seed(13)
+    R = torch.randn(B, L, V, generator=g)
+    logits = m(x.cuda(), uniq.cuda(), None, cb.cuda(), None, pm.cuda())
+    (logits * R.cuda()).sum().backward()
+    p = {k: v.detach().cpu().double().requires_grad_() for k, v in m.state_dict().items()
+         if k != "ema_rhos" and k != "lm_head.weight"}
+    kw = dict(unique_slots=uniq, c_base=cb.double(), pad_mask=pm)
+    # every step evaluated through the closed-form backward, which takes the dW_pe product
+    # from bf16 operands as the kernel does (without the absent mass p is ~V/K_b times
+    # larger, so that rounding shows in pe_proj.weight's gradient)
+    want = omodel.lm_forward(p, x, n_layers, H, m.ema_rhos.cpu(), V, gate_round="f16",
+                             absent_mass=absent_mass, t_eval=list(range(L)), **kw)
+    (want * R.double()).sum().backward()
+    assert norm_err(logits, want) < 1e-4
+    grads = dict(m.named_parameters())
+    for k, v in p.items():
+        tol = 1e-2 if k.endswith("pe_proj.weight") else 1e-4
+        assert norm_err(grads[k].grad, v.grad) < tol, (absent_mass, k)
+    other = omodel.lm_forward({k: v.detach() for k, v in p.items()}, x, n_layers, H,
+                              m.ema_rhos.cpu(), V, gate_round="f16", absent_mass=not absent_mass, **kw)
+    assert norm_err(other, want) > 1e-2
+
+
+def test_model_collated_batch_with_token_zero_history():
+    """A batch from the data pipeline (slot lists padded with id 0, as the reference's
+    collate pads them) whose chunks carry token 0 in their history: the query side and the
+    key side both keep token 0's carried c_base (the padding is masked to -1 before the
+    query scan), and logits match the oracle with the same masking."""
+    import numpy as np
+    from mathbrain.data import WikiTextMMapDataset, preprocess_corpus
+    import tempfile
+    rng = np.random.default_rng(21)
+    V = 50
+    docs = []
+    for _ in range(8):
+        n = int(rng.integers(200, 320))
+        d = rng.integers(1, V, n)
+        d[rng.integers(0, 100, 6)] = 0             # token 0 in the history ...
+        d[rng.integers(128, n, 6)] = 0             # ... and again inside later chunks
+        docs.append(d.tolist())
+    tmp = tempfile.mkdtemp(prefix="mb_h4_")
+    preprocess_corpus(docs, tmp, N=16, min_hl=1.0, max_hl=1024.0)
+    from mathbrain.synthetic import rhos_from_half_lives
+    ds = WikiTextMMapDataset(tmp, 64, rhos_from_half_lives(16, 1.0, 1024.0))
+    late = [i for i in range(len(ds)) if ds._cs[i] - ds._cds[i] >= 128][:6]
+    chunks, us, pm, inv, cb, K, doc = ds.get_batch(late)
+    pmc = pm.bool().cpu()
+    usc = us.cpu()
+    xc = chunks.cpu()
+    inside = doc.cpu() != -1                       # chunk positions (the collate pads with 0)
+    hit = [bool(((xc[b] == 0) & inside[b]).any() and not pmc[b].all()) for b in range(usc.shape[0])]
+    assert any(hit), "a padded row must hold token 0 in its chunk and history"
+    torch.manual_seed(22)
+    from mathbrain.model import SlotTransformerLM
+    m = SlotTransformerLM(V, 64, 1, 2, N=16, dropout=0.0, max_hl=1024.0).cuda()
+    x = chunks[:, :-1]
+    logits = m(x, unique_slots=us, inverse_indices=inv[:, :-1], c_base=cb, doc_ids=doc[:, :-1],
+               pad_mask=pm)
+    p = {k: v.detach().cpu().double() for k, v in m.state_dict().items()
+         if k != "ema_rhos" and k != "lm_head.weight"}
+    want = omodel.lm_forward(p, x.cpu(), 1, 2, m.ema_rhos.cpu(), V, unique_slots=usc,
+                             c_base=cb.cpu().double(), pad_mask=pmc, gate_round="f16")
+    assert norm_err(logits, want) < 1e-4
+    stale = omodel.lm_forward(p, x.cpu(), 1, 2, m.ema_rhos.cpu(), V, unique_slots=usc,
+                              c_base=cb.cpu().double(), pad_mask=pmc, gate_round="f16",
+                              mask_query_keys=False)
+    moved = norm_err(stale, want)
+    print(f"0-padded query keys would move the logits by {moved:.2e}")
+    assert moved > 1e-7
+
+
+def test_model_traces_without_graph_breaks():
+    """torch._dynamo sees every HIP entry point as a registered op (mathbrain::*), so the
+    model's forward traces into one graph and a compiled step matches eager."""
+    import torch._dynamo
+    V, D, H, N, B, L = 300, 128, 4, 16, 2, 48
+    m = build(V, D, 2, H, N, seed=31).cuda()
+    x, uniq, cb, pm = batch(B, L, V, N, seed=32)
+    args = (x.cuda(), uniq.cuda(), None, cb.cuda(), None, pm.cuda())
+    torch._dynamo.reset()
+    ex = torch._dynamo.explain(m)(*args)
+    reasons = [str(r.reason)[:300] for r in ex.break_reasons]
+    print(f"graphs {ex.graph_count}, breaks {ex.graph_break_count}: {reasons}")
+    assert ex.graph_break_count == 0, reasons
+    ops = {str(n.target) for g in ex.graphs for n in g.graph.nodes if n.op == "call_function"}
+    assert any("mathbrain" in o for o in ops), ops
+    ref = m(*args)
+    (ref.float() ** 2).mean().backward()
+    gref = {k: p.grad.clone() for k, p in m.named_parameters()}
+    m.zero_grad()
+    cm = torch.compile(m, backend="eager")
+    out = cm(*args)
+    (out.float() ** 2).mean().backward()
+    assert norm_err(out, ref) < 1e-6
+    for k, p in m.named_parameters():
+        assert norm_err(p.grad, gref[k]) < 1e-5, k

@@ -1,5 +1,5 @@
 """RMSNorm on the HIP kernels (mb_rmsnorm_fwd / mb_rmsnorm_bwd behind
-mathbrain_amd/rmsnorm.py) against the reference's expression
+mathbrain/rmsnorm.py) against the reference's expression
 weight * (x * rsqrt(mean(x^2) + eps)) (mathbrain/model.py:17-19) evaluated by torch autograd
 in float64: output, dx and dweight, norm-wise (max |diff| / max |ref|) within 1e-5 (fp32
 kernels), at widths below, at and between the 64-lane tiles, ragged row counts and the
@@ -27,7 +27,7 @@ def reference(x, w, eps):
 @pytest.mark.parametrize("shape", [(5, 3), (3, 63), (7, 64), (2, 3, 100), (9, 128), (4, 7, 512),
                                    (6, 1000), (5, 1024), (56 * 16, 512)])
 def test_rmsnorm_matches_reference_expression(shape):
-    from mathbrain_amd.rmsnorm import rms_norm
+    from mathbrain.rmsnorm import rms_norm
     g = torch.Generator().manual_seed(sum(shape))
     D = shape[-1]
     x = torch.randn(*shape, generator=g, dtype=torch.float64) * 3
@@ -50,7 +50,7 @@ def test_rmsnorm_matches_reference_expression(shape):
 
 def test_rmsnorm_tiny_values_use_eps():
     # rows of zeros: rstd = eps^-1/2, y = 0, dx = rstd * w * dy
-    from mathbrain_amd.rmsnorm import rms_norm
+    from mathbrain.rmsnorm import rms_norm
     x = torch.zeros(3, 128, device="cuda", requires_grad=True)
     w = torch.full((128,), 2.0, device="cuda", requires_grad=True)
     y = rms_norm(x, w, 1e-6)
@@ -62,8 +62,8 @@ def test_rmsnorm_tiny_values_use_eps():
 
 
 def test_rmsnorm_rejects_wide_rows_and_cpu_tensors():
-    from mathbrain_amd import _lib
-    from mathbrain_amd.rmsnorm import rms_norm
+    from mathbrain import _lib
+    from mathbrain.rmsnorm import rms_norm
     with pytest.raises(_lib.HipKernelError):
         rms_norm(torch.randn(2, 1025, device="cuda"), torch.ones(1025, device="cuda"), 1e-6)
     with pytest.raises(NotImplementedError):

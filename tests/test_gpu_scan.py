@@ -27,7 +27,7 @@ def _dev(t):
 
 
 def _scan(x, rhos, V, c_init=None, keys=None, doc=None, **kw):
-    from mathbrain_amd.ema_query import compute_query_ema_history
+    from mathbrain.triton_ema_query import compute_query_ema_history
     return compute_query_ema_history(_dev(x), _dev(rhos), V,
                                      None if c_init is None else _dev(c_init),
                                      None if keys is None else _dev(keys),
@@ -79,7 +79,7 @@ def test_gpu_scan_doc_ids_and_strided_x():
     keys = np.stack([rng.permutation(V)[:10] for _ in range(B)])
     c_init = rng.random((B, 10, N)).astype(np.float32)
     xt = _dev(full)[:, :-1]  # non-contiguous view, as train.py passes tokens[:, :-1]
-    from mathbrain_amd.ema_query import compute_query_ema_history
+    from mathbrain.triton_ema_query import compute_query_ema_history
     got = compute_query_ema_history(xt, _dev(rhos), V, _dev(c_init), _dev(keys), _dev(doc)).cpu().numpy()
     want = oscan.query_scan(full[:, :-1], rhos, V, c_init, keys, doc)
     _close(got, want)
@@ -160,7 +160,7 @@ def test_gpu_scan_more_tokens_than_lds_state(L, V, N, docs):
 
 
 def test_gpu_scan_too_long_raises():
-    from mathbrain_amd._lib import HipKernelError
+    from mathbrain._lib import HipKernelError
     with pytest.raises(HipKernelError, match="unsupported"):
         _scan(np.zeros((1, 8193), np.int64), np.array([0.5], np.float32), 10)
 
@@ -168,7 +168,7 @@ def test_gpu_scan_too_long_raises():
 def test_gpu_scan_cfg3_full_size():
     """Config 3 at full size: B=56, T=2048, N=128, V=50257, c_base from an 8192-token
     Zipf(1.1) warm-up -- every output element against the oracle, plus the final state."""
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.synthetic import make_batch
     d = make_batch(56, 2048, 50257, 128, 8192, seed=3)
     C, state, stamps = _scan(d["x"].numpy(), d["rhos"].numpy(), 50257, d["c_base"].numpy(),
                              d["unique"].numpy(), return_state=True)
@@ -219,7 +219,7 @@ def test_gpu_scan_chained_chunks_equal_single_pass():
 
 @pytest.mark.parametrize("Br", [1, 16, 64, 100])
 def test_gpu_boundary_vs_oracle(Br):
-    from mathbrain_amd.flash_ema import precompute_boundaries
+    from mathbrain.triton_flash_ema import precompute_boundaries
     rng = np.random.default_rng(Br)
     B, L, V, N, K = 3, 333, 50, 12, 40
     x = rng.integers(0, V, size=(B, L))
@@ -235,7 +235,7 @@ def test_gpu_boundary_vs_oracle(Br):
 
 
 def test_gpu_boundary_doc_ids_and_padded_c_init():
-    from mathbrain_amd.flash_ema import precompute_boundaries
+    from mathbrain.triton_flash_ema import precompute_boundaries
     rng = np.random.default_rng(9)
     B, L, V, N, K = 2, 200, 20, 4, 20
     x = rng.integers(0, V, size=(B, L))
@@ -249,8 +249,8 @@ def test_gpu_boundary_doc_ids_and_padded_c_init():
 
 
 def test_gpu_boundary_cfg2_zipf():
-    from mathbrain_amd.flash_ema import precompute_boundaries
-    from mathbrain_amd.synthetic import make_batch
+    from mathbrain.triton_flash_ema import precompute_boundaries
+    from mathbrain.synthetic import make_batch
     d = make_batch(4, 512, 50257, 64, 4096, seed=1)
     got = precompute_boundaries(d["x"].cuda(), d["unique"].cuda(), d["rhos"].cuda(), 64,
                                 d["c_base"].cuda()).cpu().numpy()

@@ -1,5 +1,5 @@
 """SwiGLU's gate product on the HIP kernels (mb_swiglu_fwd / mb_swiglu_bwd behind
-mathbrain_amd/swiglu.py) against the reference's F.silu(a) * b (mathbrain/model.py:21-29)
+mathbrain/swiglu.py) against the reference's F.silu(a) * b (mathbrain/model.py:21-29)
 evaluated by torch autograd in float64 on the same input values: output and both input
 gradients, norm-wise (max |diff| / max |ref|).  fp32 inputs: 1e-6.  bf16 inputs (autocast):
 the kernels evaluate in fp32 and round once to bf16, so the bar is bf16's rounding, 8e-3
@@ -21,7 +21,7 @@ def rel(a, b):
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-6), (torch.bfloat16, 8e-3)])
 @pytest.mark.parametrize("shape", [(1,), (7,), (3, 9), (5, 1536), (4096, 1537)])
 def test_swiglu_product_matches_reference(shape, dtype, tol):
-    from mathbrain_amd.swiglu import swiglu_product
+    from mathbrain.swiglu import swiglu_product
     g = torch.Generator().manual_seed(len(shape) * 100 + shape[-1])
     a = (torch.randn(*shape, generator=g) * 3).to(dtype)
     b = torch.randn(*shape, generator=g).to(dtype)
@@ -42,7 +42,7 @@ def test_swiglu_product_matches_reference(shape, dtype, tol):
 
 
 def test_swiglu_empty_and_cpu():
-    from mathbrain_amd.swiglu import swiglu_product
+    from mathbrain.swiglu import swiglu_product
     e = torch.empty(0, 16, device="cuda")
     assert swiglu_product(e, e).shape == (0, 16)
     with pytest.raises(NotImplementedError):
@@ -51,7 +51,7 @@ def test_swiglu_empty_and_cpu():
 
 def test_swiglu_offset_views():
     # contiguous views that start 1 element into their storage (not 32-byte aligned)
-    from mathbrain_amd.swiglu import swiglu_product
+    from mathbrain.swiglu import swiglu_product
     g = torch.Generator().manual_seed(5)
     base_a = torch.randn(1 + 40 * 24, generator=g).to(torch.bfloat16)
     base_b = torch.randn(1 + 40 * 24, generator=g).to(torch.bfloat16)

@@ -1,5 +1,5 @@
 """Pins the CPU oracle of the data pipeline (oracle/data.py) and checks the host-side
-bookkeeping of mathbrain_amd/data.py against it (no GPU needed).
+bookkeeping of mathbrain/data.py against it (no GPU needed).
 
 Known answers are the reference's own (tests/test_pipeline_thorough.py,
 tests/test_data_pipeline.py, tests/test_history_expansion.py); the rest are the closed
@@ -182,11 +182,11 @@ def test_block_size_invariance():
             assert np.allclose(C + 1.0, states[c[0]:c[1]], rtol=1e-5, atol=1e-5)
 
 
-# ---- host bookkeeping of mathbrain_amd.data against the oracle ------------------------------
+# ---- host bookkeeping of mathbrain.data against the oracle ------------------------------
 
 @pytest.mark.parametrize("seed,block", [(0, 3), (1, 16), (2, 64), (3, 1)])
 def test_chunk_index_matches_oracle(seed, block):
-    from mathbrain_amd import data as md
+    from mathbrain import data as md
     rng = np.random.default_rng(seed)
     docs = random_docs(rng, 30, 150, 50) + [[5]] + random_docs(rng, 3, 4, 5)
     _, doc_ids = corpus(docs)
@@ -197,13 +197,13 @@ def test_chunk_index_matches_oracle(seed, block):
 
 
 def test_chunk_index_rejects_split_documents():
-    from mathbrain_amd import data as md
+    from mathbrain import data as md
     with pytest.raises(ValueError):
         md.chunk_index(np.array([0, 0, 1, 1, 0, 0], np.int32), 4)
 
 
 def test_token_budget_sampler_matches_oracle():
-    from mathbrain_amd import data as md
+    from mathbrain import data as md
 
     class Lens:
         def __init__(self, n):
@@ -223,7 +223,7 @@ def test_token_budget_sampler_matches_oracle():
 
 
 def test_dynamic_collate_matches_oracle():
-    from mathbrain_amd import data as md
+    from mathbrain import data as md
     rng = np.random.default_rng(5)
     docs = random_docs(rng, 6, 60, 12)
     tokens, doc_ids, rhos, states, pos, chunks, starts, item = build(docs, 4, 1.0, 32.0, 9)
@@ -238,7 +238,7 @@ def test_dynamic_collate_matches_oracle():
 
 
 def test_device_calls_need_a_gpu():
-    from mathbrain_amd import data as md
+    from mathbrain import data as md
     if torch.cuda.is_available():
         pytest.skip("a GPU is visible")
     with pytest.raises(NotImplementedError):

@@ -42,7 +42,7 @@ def test_dense_cpu_path_equals_sparse_device_path(use_silu):
 
 
 def test_product_model_has_no_cpu_path():
-    from mathbrain_amd.model import SlotTransformerLM
+    from mathbrain.model import SlotTransformerLM
     m = SlotTransformerLM(50, 64, 1, 2, N=4, dropout=0.0)
     with pytest.raises(NotImplementedError):
         m(torch.randint(0, 50, (1, 8)))
