@@ -195,16 +195,16 @@ def test_model_collated_batch_with_token_zero_history():
     assert any(hit), "a padded row must hold token 0 in its chunk and history"
     torch.manual_seed(22)
     from mathbrain.model import SlotTransformerLM
-    m = SlotTransformerLM(V, 64, 1, 2, N=16, dropout=0.0, max_hl=1024.0).cuda()
+    m = SlotTransformerLM(V, 128, 1, 4, N=16, dropout=0.0, max_hl=1024.0).cuda()
     x = chunks[:, :-1]
     logits = m(x, unique_slots=us, inverse_indices=inv[:, :-1], c_base=cb, doc_ids=doc[:, :-1],
                pad_mask=pm)
     p = {k: v.detach().cpu().double() for k, v in m.state_dict().items()
          if k != "ema_rhos" and k != "lm_head.weight"}
-    want = omodel.lm_forward(p, x.cpu(), 1, 2, m.ema_rhos.cpu(), V, unique_slots=usc,
+    want = omodel.lm_forward(p, x.cpu(), 1, 4, m.ema_rhos.cpu(), V, unique_slots=usc,
                              c_base=cb.cpu().double(), pad_mask=pmc, gate_round="f16")
     assert norm_err(logits, want) < 1e-4
-    stale = omodel.lm_forward(p, x.cpu(), 1, 2, m.ema_rhos.cpu(), V, unique_slots=usc,
+    stale = omodel.lm_forward(p, x.cpu(), 1, 4, m.ema_rhos.cpu(), V, unique_slots=usc,
                               c_base=cb.cpu().double(), pad_mask=pmc, gate_round="f16",
                               mask_query_keys=False)
     moved = norm_err(stale, want)
