@@ -4,8 +4,8 @@
  * Every entry point takes device pointers, plain sizes and strides, and a HIP stream
  * (hipStream_t passed as void*; NULL = the null stream).  Nothing here allocates:
  * callers pass every output buffer, and the one call that needs device scratch
- * (mb_corpus_states) takes it as a workspace argument.  Calls are asynchronous on
- * the stream.
+ * (mb_corpus_states) takes it as a workspace argument, or, in its _noalloc variant, uses
+ * a fixed scratch array inside the library.  Calls are asynchronous on the stream.
  *
  * Return value: MB_OK (0) on success; a negative MB_ERR_* code for an argument the call
  * rejects before launching anything; a positive hipError_t code when the HIP runtime
@@ -259,6 +259,18 @@ int mb_gating_bwd(const float *dy, const float *x_q, int64_t xq_row_stride, cons
 int64_t mb_corpus_states_workspace(int64_t T, int N);
 int mb_corpus_states(const int64_t *order, const int64_t *chain, int64_t T, const float *rhos,
                      int N, float *states, void *work, int64_t work_bytes, void *stream);
+
+/*
+ * mb_corpus_states without a workspace argument: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * mb_corpus_states; the scratch is a 32 MiB device array inside the library (one per GPU,
+ * held until the process ends), so mb_corpus_states_workspace(T, N) must not exceed
+ * 32 MiB (about 44 M tokens at N = 64): larger calls return MB_ERR_WORKSPACE.  The call
+ * allocates nothing.  Calls that overlap on one GPU share that scratch and race.
+ */
+int mb_corpus_states_noalloc(const int64_t *order, const int64_t *chain, int64_t T,
+                             const float *rhos, int N, float *states, void *stream);
 
 /*
  * Slot lists of a batch of chunks (first half of the batch builder).  Replaces the slot

@@ -42,6 +42,7 @@ SIGNATURES = {
                        _p, _p, _p, _p, _p], _i),
     "mb_corpus_states_workspace": ([_i64, _i], _i64),
     "mb_corpus_states": ([_p, _p, _i64, _p, _i, _p, _p, _i64, _p], _i),
+    "mb_corpus_states_noalloc": ([_p, _p, _i64, _p, _i, _p, _p], _i),
     "mb_slot_lists": ([_p, _p, _i64, _i64, _p, _p, _p, _i, _p, _p, _p, _p, _p], _i),
     "mb_slot_batch": ([_p, _p, _p, _p, _i, _i64, _i64, _p, _p, _p, _i, _p, _p, _p, _p, _i, _i,
                        _p, _p, _p, _p, _p, _p, _p], _i),

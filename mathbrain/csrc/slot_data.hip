@@ -4,6 +4,7 @@
 // (data.py:93-148, 207-232).  The corpus (tokens, document ids, the next-occurrence
 // index and the [T, N] states) stays resident in HBM; a batch is three small launches.
 #include <climits>
+#include <mutex>
 
 #include "common.h"
 
@@ -341,29 +342,47 @@ int64_t units_for(int64_t T) { return (T + kUnit - 1) / kUnit; }
 
 using namespace mb;
 
-extern "C" int64_t mb_corpus_states_workspace(int64_t T, int N) {
-    if (T <= 0 || N <= 0) return 0;
-    return units_for(T) * (int64_t)N * 3 * (int64_t)sizeof(float);
+// Device scratch of mb_corpus_states_noalloc.  Each GPU the library runs on holds its own
+// copy from module load until the process ends; host code reaches it only through the
+// address hipGetSymbolAddress returns on that device (the array's name in host code is a
+// stand-in, not a device address).
+constexpr int64_t kNoAllocScratchBytes = 32ll << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace mb {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// The current device's address of `scratch`, looked up once per device (with that device
+// current) and kept.
+int scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail((int)e, "mb_corpus_states_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(MB_ERR_UNSUPPORTED, "mb_corpus_states_noalloc: device %d beyond %d", dev, kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail((int)(e != hipSuccess ? e : hipErrorInvalidSymbol),
+                        "mb_corpus_states_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MB_OK;
 }
 
-extern "C" int mb_corpus_states(const int64_t* order, const int64_t* chain, int64_t T,
-                                const float* rhos, int N, float* states, void* work,
-                                int64_t work_bytes, void* stream) {
-    MB_REQUIRE(T >= 0, "mb_corpus_states: negative T=%lld", (long long)T);
-    MB_REQUIRE(N >= 1 && N <= kMaxRates, "mb_corpus_states: N=%d must be in [1, %d]", N, kMaxRates);
-    MB_REQUIRE(T <= INT_MAX, "mb_corpus_states: T=%lld exceeds the int32 position range",
-               (long long)T);
-    if (T == 0) return MB_OK;
-    MB_REQUIRE(order && chain && rhos && states,
-               "mb_corpus_states: order, chain, rhos and states must be non-null");
-    const int64_t need = mb_corpus_states_workspace(T, N);
-    if (!work || work_bytes < need)
-        return fail(MB_ERR_WORKSPACE, "mb_corpus_states: workspace of %lld B given, %lld B needed",
-                    (long long)work_bytes, (long long)need);
+// The three passes of mb_corpus_states over a workspace of mb_corpus_states_workspace bytes.
+int corpus_states_run(const int64_t* order, const int64_t* chain, int64_t T, const float* rhos,
+                      int N, float* states, void* work, hipStream_t st) {
     const int64_t nu = units_for(T);
     float* agg = (float*)work;
     float* s_in = agg + nu * 2 * N;
-    hipStream_t st = (hipStream_t)stream;
     const dim3 ugrid((unsigned)((nu + kUnitWaves - 1) / kUnitWaves));
     const dim3 ublock(64 * kUnitWaves);
     if (N <= 64) {
@@ -385,6 +404,53 @@ extern "C" int mb_corpus_states(const int64_t* order, const int64_t* chain, int6
                            rhos, N, nu, nullptr, s_in, states);
     }
     return check_launch("mb_corpus_states (state rows)");
+}
+
+}  // namespace
+}  // namespace mb
+
+extern "C" int64_t mb_corpus_states_workspace(int64_t T, int N) {
+    if (T <= 0 || N <= 0) return 0;
+    return units_for(T) * (int64_t)N * 3 * (int64_t)sizeof(float);
+}
+
+extern "C" int mb_corpus_states(const int64_t* order, const int64_t* chain, int64_t T,
+                                const float* rhos, int N, float* states, void* work,
+                                int64_t work_bytes, void* stream) {
+    MB_REQUIRE(T >= 0, "mb_corpus_states: negative T=%lld", (long long)T);
+    MB_REQUIRE(N >= 1 && N <= kMaxRates, "mb_corpus_states: N=%d must be in [1, %d]", N, kMaxRates);
+    MB_REQUIRE(T <= INT_MAX, "mb_corpus_states: T=%lld exceeds the int32 position range",
+               (long long)T);
+    if (T == 0) return MB_OK;
+    MB_REQUIRE(order && chain && rhos && states,
+               "mb_corpus_states: order, chain, rhos and states must be non-null");
+    const int64_t need = mb_corpus_states_workspace(T, N);
+    if (!work || work_bytes < need)
+        return fail(MB_ERR_WORKSPACE, "mb_corpus_states: workspace of %lld B given, %lld B needed",
+                    (long long)work_bytes, (long long)need);
+    return corpus_states_run(order, chain, T, rhos, N, states, work, (hipStream_t)stream);
+}
+
+extern "C" int mb_corpus_states_noalloc(const int64_t* order, const int64_t* chain, int64_t T,
+                                        const float* rhos, int N, float* states, void* stream) {
+    MB_REQUIRE(T >= 0, "mb_corpus_states_noalloc: negative T=%lld", (long long)T);
+    MB_REQUIRE(N >= 1 && N <= kMaxRates, "mb_corpus_states_noalloc: N=%d must be in [1, %d]", N,
+               kMaxRates);
+    MB_REQUIRE(T <= INT_MAX, "mb_corpus_states_noalloc: T=%lld exceeds the int32 position range",
+               (long long)T);
+    const int64_t need = mb_corpus_states_workspace(T, N);
+    if (need > kNoAllocScratchBytes)
+        return fail(MB_ERR_WORKSPACE,
+                    "mb_corpus_states_noalloc: T=%lld at N=%d needs %lld B of scratch, more than the "
+                    "%lld B this entry point holds per GPU (use mb_corpus_states with a workspace)",
+                    (long long)T, N, (long long)need, (long long)kNoAllocScratchBytes);
+    if (T == 0) return MB_OK;
+    MB_REQUIRE(order && chain && rhos && states,
+               "mb_corpus_states_noalloc: order, chain, rhos and states must be non-null");
+    void* work = nullptr;
+    int rc = scratch_address(&work);
+    if (rc) return rc;
+    return corpus_states_run(order, chain, T, rhos, N, states, work, (hipStream_t)stream);
 }
 
 extern "C" int mb_slot_lists(const int32_t* tokens, const int32_t* next_pos, int64_t T, int64_t V,
