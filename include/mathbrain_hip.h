@@ -112,6 +112,10 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
 #define MB_FLASH_ABSENT_MASS 2 /* softmax also over the V - K_b absent slots (score 0) */
 #define MB_FLASH_VOCAB_ROWS 4  /* E_k, E_v (dE_k, dE_v) are [V_total, H*hd] tables indexed by
                                   the slot's token id instead of [B, K, H*hd] gathered rows */
+#define MB_FLASH_FP32 8        /* fp32 mode: the gate GEMM takes fp16 hi + lo operand pairs (three
+                                  products, ~2^-22 relative) and the dW_pe product bf16 hi + lo
+                                  pairs (~2^-16); otherwise fp16 gate and bf16 dW_pe operands.
+                                  Needs N <= 64. */
 
 /*
  * Flash-EMA gated cross-attention forward.  Replaces flash_ema_forward and its kernel

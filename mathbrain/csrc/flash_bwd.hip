@@ -48,7 +48,12 @@ static int zero_fill(float* p, int64_t n, hipStream_t st) {
 // a wave holds, so the two half-waves of a head swap their dpre tiles through LDS and each
 // multiplies all 32 steps into its own half of the tiles [NTW th, NTW th + NTW).
 // VR: E_k / E_v and dE_k / dE_v are vocabulary tables indexed by the slot's token id.
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NTW, bool XH, bool VR>
+// PREC (MB_FLASH_FP32): the gate GEMM takes fp16 hi + lo operand pairs (W_lo c_hi + W_hi
+// c_lo + W_hi c_hi) and the dW_pe product bf16 hi + lo pairs (dpre_lo c_hi + dpre_hi c_lo
+// + dpre_hi c_hi), both with fp32 accumulation; the producer writes the lo tiles beside
+// the hi ones and W_lo's fragments sit beside W_hi's in LDS.
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NTW, bool XH, bool VR,
+          bool PREC = false>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     constexpr int NPAD = 32 * NS;
@@ -58,9 +63,10 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     // (TT) when more than one slot shares a batch or when every wave reads both halves' steps
     // (XH); otherwise the copy costs more on the producer's critical path than the per-wave
     // fp16 -> bf16 conversion it saves (measured), and the waves convert instead.
-    constexpr bool TT = SB > 1 || XH;
+    constexpr bool TT = SB > 1 || XH || PREC;
     static_assert(!XH || SB == 1, "the dpre exchange buffer is reused slot after slot");
-    using S = Stage<NPAD, SB, TT>;
+    static_assert(!(XH && PREC), "the fp32 mode takes N <= 64");
+    using S = Stage<NPAD, SB, TT, PREC>;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int D = a.H * HD;
@@ -78,13 +84,14 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     static_assert(SCN <= 2 * kBwdHeads * 64, "one staged score per thread");
     const int stage_bytes = (int)S::bytes(WID) + SCN * 4;
     f16x8* wfr = reinterpret_cast<f16x8*>(smem + 2 * stage_bytes);
-    BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + kBwdHeads * DT * NS * 64);
+    f16x8* wfl = wfr + kBwdHeads * DT * NS * 64;  // PREC: the W_lo fragments
+    BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + (PREC ? 2 : 1) * kBwdHeads * DT * NS * 64);
     int64_t* win = reinterpret_cast<int64_t*>(metas + kMetaRing * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
     bf16x4* xbuf = reinterpret_cast<bf16x4*>(kinfo + 4);  // XH: [head][half][DT][64 lanes]
 #define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
-#define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CDEC * 2)
+#define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CTOFF)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
 #define S2_of(i) (E_of(i) + SB * 2 * WID)
 #define meta_of(batch) (metas + ((batch) % kMetaRing) * SB)
@@ -111,13 +118,17 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             const int n = min(32 * ns + 8 * (ln >> 4) + e, a.N - 1);
             w[e] = a.W[(int64_t)n * D + (hg * kBwdHeads + hh) * HD + 16 * dt + (ln & 15)];
         }
-        f16x8 v;
+        f16x8 v, vl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int n = 32 * ns + 8 * (ln >> 4) + e;
-            v[e] = (_Float16)(n < a.N ? w[e] * kLog2e : 0.f);
+            float ws = n < a.N ? w[e] * kLog2e : 0.f;
+            if (PREC) asm volatile("" : "+v"(ws));  // hi and lo of one float32 product
+            v[e] = (_Float16)ws;
+            vl[e] = (_Float16)(ws - (float)v[e]);
         }
         wfr[f] = v;
+        if (PREC) wfl[f] = vl;
     }
     flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
     const int kend = kinfo[1];
@@ -179,7 +190,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         load_scores(0);
         __syncthreads();
         store_scores(S2_of(0));
-        prod.template store<TT, S::CROW, S::TROW>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0), E_of(0), WID);
+        prod.template store<TT, S::CROW, S::TROW, PREC, S::CDEC, S::CT>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0), E_of(0), WID);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -210,10 +221,24 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                 ek[dt] = E[(j * 2 + 0) * WID + hl * HD + 16 * dt + c16];
                 ev[dt] = E[(j * 2 + 1) * WID + hl * HD + 16 * dt + c16];
             }
+            f16x8 cfl[NS];
+            if (PREC) {
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns)
+                    cfl[ns] = *reinterpret_cast<const f16x8*>(crow + S::CDEC + c16 * S::CROW + 32 * ns + 8 * g);
+            }
             f32x4 g2[DT], sg[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 f32x4 accg = {0.f, 0.f, 0.f, 0.f};
+                if (PREC) {  // small terms first
+#pragma unroll
+                    for (int ns = 0; ns < NS; ++ns)
+                        accg = mfma16x16x32(cf[ns], wfl[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
+#pragma unroll
+                    for (int ns = 0; ns < NS; ++ns)
+                        accg = mfma16x16x32(cfl[ns], wfr[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
+                }
 #pragma unroll
                 for (int ns = 0; ns < NS; ++ns)
                     accg = mfma16x16x32(cf[ns], wfr[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
@@ -248,7 +273,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             //   dE_k += xq g, dE_v += yd g, dQ += ds g e_k,
             //   dpre = (xq e_k + yd e_v) SiLU'(pre),  SiLU' = sig + g (1 - sig).
             float dEk[DT], dEv[DT];
-            bf16x4 dpre[DT];
+            bf16x4 dpre[DT], dprel[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 dEk[dt] = 0.f;
@@ -267,7 +292,9 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                         const float sig = sg[dt][i];
                         dsil = __builtin_fmaf(gv, __builtin_fmaf(-kLn2, sig, kLn2), sig);
                     }
-                    dpre[dt][i] = (__bf16)(av * dsil);
+                    const float dv = av * dsil;
+                    dpre[dt][i] = (__bf16)dv;
+                    if (PREC) dprel[dt][i] = (__bf16)(dv - (float)dpre[dt][i]);
                 }
             }
             // dE: this lane's 4 steps summed in registers; the 4 row groups (other steps)
@@ -327,13 +354,22 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt) {
                     const bf16x4 cb4 = cop(th, nt);
+                    if (PREC) {  // small terms first; the lo tile sits S::CT entries after the hi one
+                        const __bf16* ccol = cdecT_of(cur) + S::CT + (j * NPAD + c16) * S::TROW + 16 * th + 4 * g;
+                        const bf16x4 cl4 = *reinterpret_cast<const bf16x4*>(ccol + 16 * nt * S::TROW);
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt) {
+                            dWacc[dt][nt] = mfma16x16x16(dprel[dt], cb4, dWacc[dt][nt]);
+                            dWacc[dt][nt] = mfma16x16x16(dpre[dt], cl4, dWacc[dt][nt]);
+                        }
+                    }
 #pragma unroll
                     for (int dt = 0; dt < DT; ++dt) dWacc[dt][nt] = mfma16x16x16(dpre[dt], cb4, dWacc[dt][nt]);
                 }
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<TT, S::CROW, S::TROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), cdecT_of(cur ^ 1),
+            prod.template store<TT, S::CROW, S::TROW, PREC, S::CDEC, S::CT>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), cdecT_of(cur ^ 1),
                                                 E_of(cur ^ 1), WID);
             store_scores(S2_of(cur ^ 1));
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
@@ -368,15 +404,15 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #undef meta_of
 }
 
-template <int HD, int NS, int SB, bool XH>
+template <int HD, int NS, int SB, bool XH, bool PREC>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
-    return 2 * (Stage<32 * NS, SB, (SB > 1 || XH)>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
-           (size_t)kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
+    return 2 * (Stage<32 * NS, SB, (SB > 1 || XH || PREC), PREC>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
+           (size_t)(PREC ? 2 : 1) * kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16 + (XH ? (size_t)kBwdHeads * 2 * (HD / 16) * 64 * 8 : 0);
 }
 
-template <int HD, int NS, int SB>
+template <int HD, int NS, int SB, bool PREC = false>
 static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     FlashArgsV a = a0;
     a.head_groups = a.H / kBwdHeads;
@@ -391,16 +427,16 @@ static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     constexpr int NTW = NT < 256 / HD ? NT : 256 / HD;
     constexpr bool XH = NT > NTW;
     static_assert(NT == NTW || NT == 2 * NTW, "at most two half-waves per head");
-    const size_t lds = bwd_lds_bytes<HD, NS, SB, XH>();
+    const size_t lds = bwd_lds_bytes<HD, NS, SB, XH, PREC>();
     if (lds > 160 * 1024)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: hd=%d, N=%d needs %zu B of LDS", HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
     dim3 grid(a.B * ntb * a.head_groups);
 #define MB_BWD_PICK(MI, ME, VR)                                                                  \
-    (a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH, VR>             \
-                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH, VR>)           \
-            : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH, VR>            \
-                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH, VR>))
+    (a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH, VR, PREC>       \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH, VR, PREC>)     \
+            : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH, VR, PREC>      \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH, VR, PREC>))
     const FlashArgs& base = a;
 #define MB_BWD(MI, ME)                                                                            \
     do {                                                                                          \
@@ -468,6 +504,12 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
                "mb_flash_ema_bwd: null pointer");
     MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_bwd: null slot pointer");
     const int NS = (N + 31) / 32;
+    if (flags & MB_FLASH_FP32) {
+        // hi + lo operand tiles and both W fragment sets in LDS: one slot per batch
+        if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
+        if (hd == 64) return NS == 1 ? launch_bwd<64, 1, 1, true>(a, vr, st) : launch_bwd<64, 2, 1, true>(a, vr, st);
+        return NS == 1 ? launch_bwd<32, 1, 1, true>(a, vr, st) : launch_bwd<32, 2, 1, true>(a, vr, st);
+    }
     if (hd == 64) {
         if (NS == 1) return launch_bwd<64, 1, 4>(a, vr, st);
         if (NS == 2) return launch_bwd<64, 2, 4>(a, vr, st);

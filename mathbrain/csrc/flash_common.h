@@ -158,15 +158,20 @@ __device__ inline int xcd_major(int bid, int G) {
 
 // LDS carve-up of the per-batch staging buffers: cdec (fp16), with BF the transposed bf16
 // copy cdecT ([SB][NPAD][TROW], steps contiguous, for the backward's dW_pe product), then E.
-template <int NPAD, int SB, bool BF = false>
+// With PR (the fp32 gate mode) each counter tile has a second, "lo" tile right after it:
+// cdec_lo = fp16(c - cdec) and cdecT_lo = bf16(c - cdecT), so that hi + lo carries the
+// counter to ~2^-22 (fp16 pair) or ~2^-16 (bf16 pair) relative.
+template <int NPAD, int SB, bool BF = false, bool PR = false>
 struct Stage {
     static constexpr int CROW = NPAD + 8;  // 16-bit entries per cdec row (16 B pad against conflicts)
     static constexpr int CDEC = SB * kTB * CROW;  // entries per tile
+    static constexpr int NT = PR ? 2 : 1;         // tiles of each kind (hi, lo)
     // cdecT row: kTB steps + 4 entries of padding, so that 16 rates x 4 step groups read by
     // one wave start on 64 distinct LDS banks
     static constexpr int TROW = kTB + 4;
     static constexpr int CT = BF ? SB * NPAD * TROW : 0;
-    static constexpr int EOFF = (CDEC + CT) * 2;  // byte offset of E
+    static constexpr int CTOFF = NT * CDEC * 2;          // byte offset of cdecT
+    static constexpr int EOFF = (NT * CDEC + NT * CT) * 2;  // byte offset of E
     // width: embedding columns staged per slot
     __host__ __device__ static size_t bytes(int width) {
         return (size_t)EOFF + (size_t)SB * 2 * width * 4;
@@ -303,8 +308,9 @@ struct Producer {
     }
 
     // Builds cdec ([SB][kTB][CROW], fp16), with BF also cdecT ([SB][NPAD][TROW], bf16), and E
-    // ([SB][2][width]) of the batch into the staging buffer.
-    template <bool BF, int CROW, int TROW>
+    // ([SB][2][width]) of the batch into the staging buffer.  With PR also the lo tiles,
+    // CLO entries after cdec and CTLO entries after cdecT (see Stage).
+    template <bool BF, int CROW, int TROW, bool PR = false, int CLO = 0, int CTLO = 0>
     __device__ void store(int t0, int cb, const float* powt, const BatchMeta* meta,
                           _Float16* cdec, __bf16* cdecT, float* E, int width) {
         const int tid = threadIdx.x;
@@ -320,7 +326,7 @@ struct Producer {
             const float4 sv = make_float4(fminf(s[ii].x, kCMax), fminf(s[ii].y, kCMax),
                                           fminf(s[ii].z, kCMax), fminf(s[ii].w, kCMax));
             const uint64_t mask = meta[j].mask;
-            bf16x4 tb[4];
+            bf16x4 tb[4], tl4[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tl = 4 * tq + r;
@@ -337,13 +343,34 @@ struct Producer {
                     c2 += q.z;
                     c3 += q.w;
                 }
+                if (PR) {
+                    // hi and lo come from one materialised float32 counter: a conversion the
+                    // compiler fused with the last add would round hi from a different value
+                    asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
+                }
                 f16x4 w;
                 w[0] = (_Float16)c0;
                 w[1] = (_Float16)c1;
                 w[2] = (_Float16)c2;
                 w[3] = (_Float16)c3;
                 *reinterpret_cast<f16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
-                if (BF) {  // bf16 of the gate's fp16 counter (the gate and dW_pe see one c_dec)
+                if (PR) {  // the fp16 rounding remainder
+                    f16x4 wl;
+                    wl[0] = (_Float16)(c0 - (float)w[0]);
+                    wl[1] = (_Float16)(c1 - (float)w[1]);
+                    wl[2] = (_Float16)(c2 - (float)w[2]);
+                    wl[3] = (_Float16)(c3 - (float)w[3]);
+                    *reinterpret_cast<f16x4*>(cdec + CLO + (j * kTB + tl) * CROW + n0) = wl;
+                }
+                if (BF && PR) {  // bf16 hi + lo of the float32 counter
+                    const float cv[4] = {c0, c1, c2, c3};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const __bf16 h = (__bf16)cv[q];
+                        tb[q][r] = h;
+                        tl4[q][r] = (__bf16)(cv[q] - (float)h);
+                    }
+                } else if (BF) {  // bf16 of the gate's fp16 counter (the gate and dW_pe see one c_dec)
                     tb[0][r] = (__bf16)(float)w[0];
                     tb[1][r] = (__bf16)(float)w[1];
                     tb[2][r] = (__bf16)(float)w[2];
@@ -352,8 +379,11 @@ struct Producer {
             }
             if (BF) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
+                for (int q = 0; q < 4; ++q) {
                     *reinterpret_cast<bf16x4*>(cdecT + (j * NPAD + n0 + q) * TROW + 4 * tq) = tb[q];
+                    if (PR)
+                        *reinterpret_cast<bf16x4*>(cdecT + CTLO + (j * NPAD + n0 + q) * TROW + 4 * tq) = tl4[q];
+                }
             }
         }
         const int nvec = SB * 2 * (width / 4);

@@ -25,12 +25,16 @@ namespace mb {
 constexpr float kTau = 8.0f;
 
 // VR: E_k / E_v are vocabulary tables indexed by the slot's token id (MB_FLASH_VOCAB_ROWS).
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR>
+// PREC (MB_FLASH_FP32): the gate GEMM carries both operands as fp16 hi + lo pairs,
+//   pre = W_lo c_hi + W_hi c_lo + W_hi c_hi  (three MFMAs, fp32 accumulation),
+// which leaves ~2^-22 relative error per product instead of fp16's 2^-11; W_lo waits in
+// LDS (W_hi stays in registers) and the producer writes a c_lo tile beside c_hi.
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR, bool PREC = false>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
-    using S = Stage<NPAD, SB>;
+    using S = Stage<NPAD, SB, false, PREC>;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int D = a.H * HD;
@@ -48,6 +52,7 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
     int64_t* win = reinterpret_cast<int64_t*>(metas + 3 * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
+    f16x8* wlo = reinterpret_cast<f16x8*>(kinfo + 4);  // PREC: [head][dt][ns][lane]
 #define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
 #define meta_of(batch) (metas + ((batch) % 3) * SB)
@@ -81,12 +86,19 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int ns = 0; ns < NS; ++ns)
+            for (int ns = 0; ns < NS; ++ns) {
+                f16x8 lo;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int n = 32 * ns + 8 * g + e;
-                    wf[dt][ns][e] = (_Float16)(n < a.N ? wraw[dt][ns][e] * kLog2e : 0.f);
+                    float ws = n < a.N ? wraw[dt][ns][e] * kLog2e : 0.f;
+                    if (PREC) asm volatile("" : "+v"(ws));  // hi and lo of one float32 product
+                    wf[dt][ns][e] = (_Float16)ws;
+                    lo[e] = (_Float16)(ws - (float)wf[dt][ns][e]);
                 }
+                // this wave's head's W_lo fragments, read back in the slot loop
+                if (PREC) wlo[((h * DT + dt) * NS + ns) * 64 + lane] = lo;
+            }
     }
 
     // Queries of this lane's steps, pre-scaled by 1/sqrt(hd).
@@ -117,7 +129,7 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
         if (VR) __syncthreads();  // the load reads the batch's token ids
         prod.template load<VR>(a, b, cbi, 0, kend, D, 0, D, meta_of(0));
         __syncthreads();
-        prod.template store<false, S::CROW, S::TROW>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
+        prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -145,14 +157,29 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
             }
             f32x4 gt[2][DT];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
+            for (int tt = 0; tt < 2; ++tt) {
+                f16x8 cl[NS];
+                if (PREC) {
+#pragma unroll
+                    for (int ns = 0; ns < NS; ++ns)
+                        cl[ns] = *reinterpret_cast<const f16x8*>(
+                            cdec + S::CDEC + (j * kTB + 16 * tt + c16) * S::CROW + 32 * ns + 8 * g);
+                }
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    if (PREC) {  // small terms first
+#pragma unroll
+                        for (int ns = 0; ns < NS; ++ns)
+                            acc = mfma16x16x32(wlo[((h * DT + dt) * NS + ns) * 64 + lane], cf[tt][ns], acc);
+#pragma unroll
+                        for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cl[ns], acc);
+                    }
 #pragma unroll
                     for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cf[tt][ns], acc);
                     gt[tt][dt] = acc;
                 }
+            }
             float s[2];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
@@ -211,7 +238,7 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<false, S::CROW, S::TROW>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+            prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
                                               E_of(cur ^ 1), D);
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
@@ -239,20 +266,20 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
 #undef meta_of
 }
 
-template <int HD, int NS, int SB>
-static size_t fwd_lds_bytes(int D) {
-    return 2 * Stage<32 * NS, SB>::bytes(D) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
-           65 * 32 * NS * 4 + 16;
+template <int HD, int NS, int SB, bool PREC>
+static size_t fwd_lds_bytes(int D, int H) {
+    return 2 * Stage<32 * NS, SB, false, PREC>::bytes(D) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
+           65 * 32 * NS * 4 + 16 + (PREC ? (size_t)H * (HD / 16) * NS * 64 * 16 : 0);
 }
 
-template <int HD, int NS, int SB>
+template <int HD, int NS, int SB, bool PREC = false>
 static int launch_fwd(const FlashArgsV& a, bool vr, hipStream_t st) {
     const int D = a.H * HD;
     const int nthr = 64 * a.H;
     constexpr int NPAD = 32 * NS;
     const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
     const int nvec = SB * 2 * (D / 4);
-    const size_t lds = fwd_lds_bytes<HD, NS, SB>(D);
+    const size_t lds = fwd_lds_bytes<HD, NS, SB, PREC>(D, a.H);
     if (lds > 160 * 1024)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: D=%d, N=%d needs %zu B of LDS", D, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
@@ -260,11 +287,11 @@ static int launch_fwd(const FlashArgsV& a, bool vr, hipStream_t st) {
     const FlashArgs& base = a;
 #define MB_FWD(MI, ME)                                                                           \
     do {                                                                                         \
-        const int rc_ = vr ? launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true>    \
-                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true>,  \
+        const int rc_ = vr ? launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true, PREC>    \
+                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true, PREC>,  \
                                              grid, nthr, lds, st, a, "mb_flash_ema_fwd")                      \
-                           : launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false>   \
-                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false>, \
+                           : launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false, PREC>   \
+                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false, PREC>, \
                                              grid, nthr, lds, st, base, "mb_flash_ema_fwd");                  \
         if (rc_) return rc_;                                                                     \
     } while (0)
@@ -328,6 +355,12 @@ extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_fwd: null slot pointer");
     hipStream_t st = (hipStream_t)stream;
     const int NS = (N + 31) / 32;
+    if (flags & MB_FLASH_FP32) {
+        // hi + lo operand tiles and the W_lo fragments in LDS: two slots per batch
+        if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
+        if (hd == 64) return NS == 1 ? launch_fwd<64, 1, 4, true>(a, vr, st) : launch_fwd<64, 2, 2, true>(a, vr, st);
+        return NS == 1 ? launch_fwd<32, 1, 4, true>(a, vr, st) : launch_fwd<32, 2, 2, true>(a, vr, st);
+    }
     if (hd == 64) {
         if (NS == 1) return launch_fwd<64, 1, 4>(a, vr, st);
         if (NS == 2) return launch_fwd<64, 2, 4>(a, vr, st);

@@ -58,7 +58,7 @@ class SlotAttentionLayer(nn.Module):
     keys and values gated by SiLU(pe_proj(C)) inside the flash-EMA kernel."""
 
     def __init__(self, d_model: int, n_heads: int, dropout: float, n_scales: int, use_silu: bool = True,
-                 absent_mass: bool = True):
+                 absent_mass: bool = True, precision: str = "bf16"):
         super().__init__()
         assert d_model % n_heads == 0
         self.n_heads = n_heads
@@ -75,6 +75,8 @@ class SlotAttentionLayer(nn.Module):
         # softmax over all V slots (the dense PyTorch reference) or over the valid slots only
         # (the reference's Triton kernel): see FlashEMAFunction
         self.absent_mass = absent_mass
+        # the attention's gate operands: fp16 ("bf16" mode) or fp16 hi + lo pairs ("fp32")
+        self.precision = precision
 
     def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None,
                 E_active=None):
@@ -106,7 +108,7 @@ class SlotAttentionLayer(nn.Module):
         W_pe_t = self.pe_proj.weight.t()
         out_mha = FlashEMAFunction.apply(Q_mha, x, E_k_active, E_v_active, W_pe_t, rhos,
                                          E_slots.shape[0], unique_tensor, K_max, C_bounds, self.use_silu,
-                                         64, self.absent_mass)
+                                         64, self.absent_mass, self.precision)
         out = out_mha.transpose(1, 2).reshape(B, L, D)
         out = self.o_proj(out)
         return self.resid_dropout(out)
@@ -115,10 +117,11 @@ class SlotAttentionLayer(nn.Module):
 class SlotTransformerBlock(nn.Module):
     """model.py:105-116."""
 
-    def __init__(self, d_model, n_heads, d_ff, dropout, n_scales, use_silu=True, absent_mass=True):
+    def __init__(self, d_model, n_heads, d_ff, dropout, n_scales, use_silu=True, absent_mass=True,
+                 precision="bf16"):
         super().__init__()
         self.attn_norm = RMSNorm(d_model)
-        self.attn = SlotAttentionLayer(d_model, n_heads, dropout, n_scales, use_silu, absent_mass)
+        self.attn = SlotAttentionLayer(d_model, n_heads, dropout, n_scales, use_silu, absent_mass, precision)
         self.ffn_norm = RMSNorm(d_model)
         self.ffn = SwiGLU(d_model, d_ff)
 
@@ -142,7 +145,7 @@ class SlotTransformerLM(nn.Module):
     """
 
     def __init__(self, vocab_size, d_model, n_layers, n_heads, N=16, dropout=0.1, use_silu=True,
-                 ema_dropout=0.0, min_hl=1.0, max_hl=2048.0, absent_mass=True):
+                 ema_dropout=0.0, min_hl=1.0, max_hl=2048.0, absent_mass=True, attn_precision="bf16"):
         super().__init__()
         self.vocab_size = vocab_size
         self.d_model = d_model
@@ -154,7 +157,8 @@ class SlotTransformerLM(nn.Module):
         self.embed = nn.Embedding(vocab_size, d_model)
         d_ff = 256 * ((int(8 * d_model / 3) + 255) // 256)
         self.layers = nn.ModuleList([
-            SlotTransformerBlock(d_model, n_heads, d_ff, dropout, self.n_scales, use_silu, absent_mass)
+            SlotTransformerBlock(d_model, n_heads, d_ff, dropout, self.n_scales, use_silu, absent_mass,
+                                 attn_precision)
             for _ in range(n_layers)
         ])
         self.final_norm = RMSNorm(d_model)

@@ -107,9 +107,18 @@ def _build_unique_index(x, device, width=None):
     return ids[:, :K_max].contiguous().to(x.dtype), K_max
 
 
-def _flash_flags(use_silu, absent_mass, vocab_rows=False):
+PRECISIONS = ("bf16", "fp32")
+
+
+def _fp32(precision):
+    if precision not in PRECISIONS:
+        raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
+    return precision == "fp32"
+
+
+def _flash_flags(use_silu, absent_mass, vocab_rows=False, fp32=False):
     return ((_lib.MB_FLASH_SILU if use_silu else 0) | (_lib.MB_FLASH_ABSENT_MASS if absent_mass else 0)
-            | (_lib.MB_FLASH_VOCAB_ROWS if vocab_rows else 0))
+            | (_lib.MB_FLASH_VOCAB_ROWS if vocab_rows else 0) | (_lib.MB_FLASH_FP32 if fp32 else 0))
 
 
 def _slot_rows(E, B, K, D, V_total, what):
@@ -129,7 +138,7 @@ def _slot_rows(E, B, K, D, V_total, what):
 
 
 def _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br,
-              absent_mass, return_scores):
+              absent_mass, return_scores, fp32=False):
     dev = _lib.require_gpu(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds,
                            what="flash_ema_forward")
     B, H, L, hd = Q.shape
@@ -158,12 +167,13 @@ def _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_
         _lib.call("mb_flash_ema_fwd", _lib.ptr(Qf), *Qf.stride(), _lib.ptr(xl), xl.stride(0),
                   xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W), _lib.ptr(rh),
                   _lib.ptr(uniq), _lib.ptr(Cb), B, H, L, hd, K, N, Cb.shape[3], Cb.shape[1],
-                  int(Br), int(V_total), _flash_flags(use_silu, absent_mass, table), _lib.ptr(O),
+                  int(Br), int(V_total), _flash_flags(use_silu, absent_mass, table, fp32), _lib.ptr(O),
                   _lib.ptr(LSE), _lib.ptr(S2), _lib.stream(dev))
     return O, LSE, S2, Ek, Ev, table
 
 
-def _fwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br, absent_mass):
+def _fwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br, absent_mass,
+              fp32):
     B, H, L, hd = Q.shape
     return Q.new_empty((B, H, L, hd), dtype=torch.float32), Q.new_empty((B, H, L), dtype=torch.float32)
 
@@ -172,15 +182,16 @@ def _fwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_
 def flash_ema_fwd(Q: torch.Tensor, x: torch.Tensor, E_k: torch.Tensor, E_v: torch.Tensor,
                   W_pe: torch.Tensor, rhos: torch.Tensor, unique_tensor: torch.Tensor,
                   C_bounds: torch.Tensor, V_total: int, use_silu: bool, Br: int,
-                  absent_mass: bool) -> tuple[torch.Tensor, torch.Tensor]:
+                  absent_mass: bool, fp32: bool) -> tuple[torch.Tensor, torch.Tensor]:
     """(O, LSE) of flash_ema_forward (one mb_flash_ema_fwd launch)."""
     O, LSE = _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br,
-                       absent_mass, False)[:2]
+                       absent_mass, False, fp32)[:2]
     return O, LSE
 
 
 def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
-                      C_bounds, use_silu=True, Br=64, absent_mass=True, return_scores=False):
+                      C_bounds, use_silu=True, Br=64, absent_mass=True, return_scores=False,
+                      precision="bf16"):
     """Gated flash-EMA attention forward (triton_flash_ema.py:529-568).
 
     Q [B, H, L, hd]; x [B, L]; E_k_active / E_v_active [B, K_max, H*hd]; W_pe [N, H*hd]
@@ -198,27 +209,31 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
     kernel's softmax over the valid slots only (triton_flash_ema.py:215-229).  With
     ``return_scores`` a sixth element holds the scores * log2(e) as [B, H, K_max, L]
     (what ``flash_ema_backward(scores=...)`` consumes instead of recomputing them).
+    ``precision``: "bf16" (default) feeds the gate GEMM fp16 operands; "fp32" feeds it fp16
+    hi + lo pairs (three products, ~2^-22 relative, N <= 64), the mode to use where scores
+    are large enough that the softmax amplifies operand rounding.
     """
+    fp32 = _fp32(precision)
     B, H, L, hd = Q.shape
     K = unique_tensor.shape[1]
     if K != K_max:
         raise ValueError(f"unique_tensor has {K} slots but K_max={K_max}")
     if not return_scores:
         O, LSE = flash_ema_fwd(Q, x, E_k_active, E_v_active, W_pe, rhos, unique_tensor, C_bounds,
-                               int(V_total), bool(use_silu), int(Br), bool(absent_mass))
+                               int(V_total), bool(use_silu), int(Br), bool(absent_mass), fp32)
         Ek, Ev = E_k_active.to(torch.float32), E_v_active.to(torch.float32)
         if Ek.dim() == 2:
             return O, LSE, C_bounds, Ek, Ev
         return O, LSE, C_bounds, Ek.reshape(B, K, H, hd), Ev.reshape(B, K, H, hd)
     O, LSE, S2, Ek, Ev, table = _fwd_impl(Q, x, E_k_active, E_v_active, W_pe, rhos, unique_tensor,
-                                          C_bounds, V_total, use_silu, Br, absent_mass, True)
+                                          C_bounds, V_total, use_silu, Br, absent_mass, True, fp32)
     if table:
         return O, LSE, C_bounds, Ek, Ev, S2
     return O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd), S2
 
 
 def _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total, use_silu,
-              Br, absent_mass, scores):
+              Br, absent_mass, scores, fp32=False):
     dev = _lib.require_gpu(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO,
                            what="flash_ema_backward")
     B, H, L, hd = Q.shape
@@ -253,13 +268,13 @@ def _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V
                   xl.stride(0), xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W),
                   _lib.ptr(rh), _lib.ptr(uniq), _lib.ptr(Cb), _lib.ptr(Of), _lib.ptr(Lf), B, H, L,
                   hd, K, N, Cb.shape[3], Cb.shape[1], int(Br), int(V_total),
-                  _flash_flags(use_silu, absent_mass, table), _lib.ptr(scores), _lib.ptr(dQ),
+                  _flash_flags(use_silu, absent_mass, table, fp32), _lib.ptr(scores), _lib.ptr(dQ),
                   _lib.ptr(dEk), _lib.ptr(dEv), _lib.ptr(dW), _lib.stream(dev))
     return dQ, dEk, dEv, dW
 
 
 def _bwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total, use_silu,
-              Br, absent_mass):
+              Br, absent_mass, fp32):
     B, H, L, hd = Q.shape
     D = H * hd
     rows = (E_k.shape[0], D) if E_k.dim() == 2 else (B, unique_tensor.shape[1], D)
@@ -272,27 +287,30 @@ def _bwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V
 def flash_ema_bwd(Q: torch.Tensor, x: torch.Tensor, E_k: torch.Tensor, E_v: torch.Tensor,
                   W_pe: torch.Tensor, rhos: torch.Tensor, unique_tensor: torch.Tensor,
                   C_bounds: torch.Tensor, O: torch.Tensor, LSE: torch.Tensor, dO: torch.Tensor,
-                  V_total: int, use_silu: bool, Br: int,
-                  absent_mass: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+                  V_total: int, use_silu: bool, Br: int, absent_mass: bool,
+                  fp32: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dQ, dE_k, dE_v, dW_pe) of flash_ema_backward (fills and one mb_flash_ema_bwd launch)."""
     return _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total,
-                     use_silu, Br, absent_mass, None)
+                     use_silu, Br, absent_mass, None, fp32)
 
 
 def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bounds, O, LSE, dO,
-                       use_silu=True, Br=64, absent_mass=True, scores=None):
+                       use_silu=True, Br=64, absent_mass=True, scores=None, precision="bf16"):
     """Gradients of flash_ema_forward (triton_flash_ema.py:586-650) in one fused HIP pass.
 
     E_k / E_v are [B, K, H*hd] or [B, K, H, hd], or [V_total, H*hd] vocabulary tables (then
     dE_k / dE_v are tables too: each row sums the gradients of every slot of that token);
     ``scores`` is the forward's optional scores output (recomputed when None).  Returns
     (dQ [B,H,L,hd], dE_k [B,K,H*hd], dE_v [B,K,H*hd], dW_pe [N, H*hd]), all fp32.
+    ``precision`` as in flash_ema_forward ("fp32" also takes the dW_pe product from bf16
+    hi + lo pairs of both operands).
     """
+    fp32 = _fp32(precision)
     if scores is None:
         return flash_ema_bwd(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO,
-                             int(V_total), bool(use_silu), int(Br), bool(absent_mass))
+                             int(V_total), bool(use_silu), int(Br), bool(absent_mass), fp32)
     return _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total,
-                     use_silu, Br, absent_mass, scores)
+                     use_silu, Br, absent_mass, scores, fp32)
 
 
 # With SAVE_SCORES, FlashEMAFunction keeps the forward's scores ([B, H, K_max, L] fp32,
@@ -305,20 +323,22 @@ SAVE_SCORES = False
 
 class FlashEMAFunction(torch.autograd.Function):
     """Autograd entry point with the reference's 12 arguments (triton_flash_ema.py:571-650)
-    and one more: apply(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
-    K_max, C_bounds, use_silu=True, Br=64, absent_mass=True) -> O [B, H, L, hd].  Inputs are
+    and two more: apply(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
+    K_max, C_bounds, use_silu=True, Br=64, absent_mass=True, precision="bf16") -> O [B, H, L, hd].  Inputs are
     used in fp32 (the reference's custom_fwd(cast_inputs=float32)); gradients flow to Q,
     E_k_active, E_v_active, W_pe.  ``absent_mass=True`` (the default) is the softmax over
     all V_total slots of the dense PyTorch reference; False reproduces the reference's
-    Triton kernel, which drops the absent slots' mass (triton_flash_ema.py:215-229)."""
+    Triton kernel, which drops the absent slots' mass (triton_flash_ema.py:215-229).
+    ``precision`` picks the gate GEMM's operands (see flash_ema_forward)."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float32)
     def forward(ctx, Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
-                C_bounds, use_silu=True, Br=64, absent_mass=True):
+                C_bounds, use_silu=True, Br=64, absent_mass=True, precision="bf16"):
         keep_scores = SAVE_SCORES and not torch.compiler.is_compiling()
         res = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
-                                K_max, C_bounds, use_silu, Br, absent_mass, return_scores=keep_scores)
+                                K_max, C_bounds, use_silu, Br, absent_mass, return_scores=keep_scores,
+                                precision=precision)
         O, LSE, C_bounds, E_k, E_v = res[:5]
         ctx.save_for_backward(Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE,
                               res[5] if keep_scores else None)
@@ -326,6 +346,7 @@ class FlashEMAFunction(torch.autograd.Function):
         ctx.use_silu = use_silu
         ctx.Br = Br
         ctx.absent_mass = absent_mass
+        ctx.precision = precision
         ctx.W_rows = W_pe.shape[0]
         return O
 
@@ -335,7 +356,8 @@ class FlashEMAFunction(torch.autograd.Function):
         Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE, S2 = ctx.saved_tensors
         dQ, dEk, dEv, dW = flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, ctx.V_total,
                                               unique_tensor, C_bounds, O, LSE, dO.contiguous(),
-                                              ctx.use_silu, ctx.Br, ctx.absent_mass, scores=S2)
+                                              ctx.use_silu, ctx.Br, ctx.absent_mass, scores=S2,
+                                              precision=ctx.precision)
         if ctx.W_rows > dW.shape[0]:  # W_pe passed with padded rows: their gradient is 0
             dW = torch.cat([dW, dW.new_zeros(ctx.W_rows - dW.shape[0], dW.shape[1])])
-        return dQ, None, dEk, dEv, dW, None, None, None, None, None, None, None, None
+        return dQ, None, dEk, dEv, dW, None, None, None, None, None, None, None, None, None

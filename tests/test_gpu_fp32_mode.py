@@ -1,0 +1,116 @@
+"""The fp32 mode of the flash-EMA attention (MB_FLASH_FP32, precision="fp32"): the gate GEMM
+takes fp16 hi + lo operand pairs (three products) and the dW_pe product bf16 hi + lo pairs,
+everything else is fp32.  Checked against the exact float64 oracle at the task's fp32-mode
+tolerance, 1e-4 norm-wise (max|got - want| / max|want|), for O, LSE and all four gradients:
+at configuration 1's shapes and scales, at the large test scales (queries N(0,1),
+embeddings N(0,0.25), W_pe N(0,0.09): scores ~100, where the default mode's 16-bit gate
+operands move O by a percent), at N = 64 with 8 x 64 heads, on a configuration-2 slice, with
+both flags, and through the vocabulary-table rows."""
+import pytest
+import torch
+
+from oracle import attention as att
+from tests.test_gpu_flash import CFG, make_case, norm_err
+
+pytestmark = pytest.mark.gpu
+
+TOL_FP32 = 1e-4
+
+
+def run(c, dO, precision="fp32", use_silu=True, absent_mass=True, table=None):
+    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward
+    cu = lambda t: t.cuda()
+    Ek, Ev = (c["E_k"], c["E_v"]) if table is None else table
+    O, LSE, *_ = flash_ema_forward(cu(c["Q"]), cu(c["x"]), cu(Ek), cu(Ev), cu(c["W"]), cu(c["rhos"]),
+                                   c["V"], cu(c["unique"]), c["K"], cu(c["Cb"]), use_silu=use_silu,
+                                   Br=c["Br"], absent_mass=absent_mass, precision=precision)
+    grads = flash_ema_backward(cu(c["Q"]), cu(c["x"]), cu(Ek), cu(Ev), cu(c["W"]), cu(c["rhos"]), c["V"],
+                               cu(c["unique"]), cu(c["Cb"]), O, LSE, cu(dO), use_silu=use_silu,
+                               Br=c["Br"], absent_mass=absent_mass, precision=precision)
+    torch.cuda.synchronize()
+    return [O.cpu(), LSE.cpu()] + [t.cpu() for t in grads]
+
+
+def exact(c, dO, use_silu=True, absent_mass=True):
+    dt = torch.float64
+    args = (c["Q"].to(dt), c["x"], c["E_k"].to(dt), c["E_v"].to(dt), c["W"].to(dt), c["rhos"].to(dt),
+            c["V"], c["unique"])
+    O, LSE = att.sparse(*args, c["c_base"].to(dt), use_silu=use_silu, absent_mass=absent_mass,
+                        return_lse=True)
+    g = att.sparse_backward_formulas(*args, dO.to(dt), c["c_base"].to(dt), use_silu=use_silu,
+                                     absent_mass=absent_mass)
+    return [O, LSE] + list(g)
+
+
+NAMES = ("O", "LSE", "dQ", "dE_k", "dE_v", "dW_pe")
+
+
+def check(c, seed=0, use_silu=True, absent_mass=True, table=None, bf16_worse=False):
+    g = torch.Generator().manual_seed(seed + 5)
+    dO = torch.randn(c["Q"].shape, generator=g)
+    got = run(c, dO, "fp32", use_silu, absent_mass, table)
+    want = exact(c, dO, use_silu, absent_mass)
+    errs = {n: norm_err(a, b) for n, a, b in zip(NAMES, got, want)}
+    msg = ", ".join(f"{k} {v:.2e}" for k, v in errs.items())
+    if bf16_worse:
+        fast = {n: norm_err(a, b) for n, a, b in zip(NAMES, run(c, dO, "bf16", use_silu, absent_mass, table), want)}
+        msg += " | bf16 mode: " + ", ".join(f"{k} {v:.2e}" for k, v in fast.items())
+        assert max(fast.values()) > 10 * max(errs.values()), msg
+    print(msg)
+    assert max(errs.values()) < TOL_FP32, msg
+
+
+def test_fp32_cfg1_own_scales():
+    """Configuration 1: B=2, T=128, 4 x 32 heads, N=16, V=1000, c_base zero, N(0, 0.02)."""
+    check(make_case(2, 128, 1000, 4, 32, 16, uniform=True, min_hl=4, max_hl=1024, **CFG))
+
+
+def test_fp32_cfg1_large_scales():
+    check(make_case(2, 128, 1000, 4, 32, 16, warmup=512, seed=3, min_hl=4, max_hl=1024), bf16_worse=True)
+
+
+@pytest.mark.parametrize("N", [16, 33, 64])
+def test_fp32_rates_heads64(N):
+    check(make_case(2, 96, 500, 8, 64, N, warmup=256, seed=N), seed=N)
+
+
+def test_fp32_cfg2_slice():
+    check(make_case(1, 256, 50257, 8, 64, 64, warmup=4096, seed=12, **CFG))
+
+
+@pytest.mark.parametrize("use_silu", [True, False])
+@pytest.mark.parametrize("absent_mass", [True, False])
+def test_fp32_flags(use_silu, absent_mass):
+    check(make_case(2, 64, 90, 4, 32, 16, warmup=50, seed=31), 7, use_silu, absent_mass)
+
+
+def test_fp32_ragged_length_and_padding_slots():
+    check(make_case(2, 77, 120, 8, 64, 16, warmup=80, seed=21, pad_slots=9), 9)
+
+
+def test_fp32_vocab_table_rows():
+    """E_k / E_v as [V, D] tables read by token id (the model's kv_table path)."""
+    c = make_case(2, 80, 70, 4, 64, 32, warmup=100, seed=51)
+    g = torch.Generator().manual_seed(52)
+    D = c["E_k"].shape[2]
+    tk, tv = torch.randn(c["V"], D, generator=g) * 0.5, torch.randn(c["V"], D, generator=g) * 0.5
+    rows = c["unique"].clamp(min=0)
+    c["E_k"], c["E_v"] = tk[rows], tv[rows]
+    dO = torch.randn(c["Q"].shape, generator=g)
+    got = run(c, dO, table=(tk, tv))
+    want = exact(c, dO)
+    # the table gradients sum every slot of a token: scatter the oracle's slot gradients
+    for i in (3, 4):
+        w = torch.zeros(c["V"], D, dtype=torch.float64)
+        w.index_add_(0, rows.reshape(-1), (want[i].reshape(-1, D) * (c["unique"] >= 0).reshape(-1, 1)))
+        want[i] = w
+    errs = {n: norm_err(a, b) for n, a, b in zip(NAMES, got, want)}
+    print(errs)
+    assert max(errs.values()) < TOL_FP32, errs
+
+
+def test_fp32_rejects_more_than_64_rates():
+    from mathbrain._lib import HipKernelError
+    c = make_case(1, 16, 50, 4, 32, 128, warmup=0, seed=1)
+    with pytest.raises(HipKernelError, match="N <= 64"):
+        run(c, torch.zeros(c["Q"].shape))

@@ -143,3 +143,41 @@ def test_cfg5_full_model_sampled_positions():
     print(f"cfg5 vs the kernel-rounding oracle: logits {errs['logits']:.2e}; worst {worst}")
     for k, e in errs.items():
         assert e < TOL_BF16, (k, e)
+
+
+def test_cfg5_full_model_fp32_mode_exact():
+    """The same batch and positions with the attention's fp32 mode (fp16 hi + lo gate
+    operands, bf16 hi + lo dW_pe operands) against the exact float64 model: the bf16 bar,
+    2e-2, for logits and every parameter gradient."""
+    c = cfg5()
+    m, d = c["model"], c["data"]
+    V, D, NL, H, N, B, T = c["dims"]
+    for layer in m.layers:
+        layer.attn.precision = "fp32"
+    try:
+        lens = d["lengths"]
+        rows = [int(d["counts"].argmax()), int(torch.argsort(lens, descending=True)[1])]
+        if rows[0] == rows[1]:
+            rows[1] = int(torch.argsort(lens, descending=True)[2])
+        n = int(min(lens[rows[0]], lens[rows[1]]))
+        g = torch.Generator().manual_seed(6)
+        steps = sorted(torch.randperm(n, generator=g)[:64].tolist())
+        R = torch.randn(len(rows), len(steps), V, generator=g)
+        got, grads = _cfg5_gpu_run(rows, steps, R)
+    finally:
+        for layer in m.layers:
+            layer.attn.precision = "bf16"
+    r = torch.tensor(rows)
+    f = torch.float64
+    p = {k: v.detach().to(f).requires_grad_() for k, v in m.state_dict().items()
+         if k not in ("ema_rhos", "lm_head.weight")}
+    want = omodel.lm_forward(p, d["x"][r], NL, H, m.ema_rhos, V, unique_slots=d["unique"][r],
+                             c_base=d["c_base"][r].to(f), pad_mask=d["unique"][r] >= 0,
+                             gate_round=None, t_eval=steps)
+    (want * R.to(f)).sum().backward()
+    errs = {"logits": norm_err(got, want)}
+    errs.update({k: norm_err(grads[k], v.grad) for k, v in p.items()})
+    worst = sorted(errs.items(), key=lambda kv: -kv[1])[:4]
+    print(f"cfg5 fp32 mode vs the exact oracle: logits {errs['logits']:.2e}; worst {worst}")
+    for k, e in errs.items():
+        assert e < TOL_BF16, (k, e)
