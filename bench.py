@@ -57,11 +57,25 @@ TRAFFIC_BYTES = {
     "cfg2": 13261.7e6,
     "cfg4": 45724.7e6,
     "corpus": 19654.0e6,   # the three mb_corpus_states launches (profiles/corpus_states_64M_tokens.md)
+    "scan": 109.2e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
+    "gating": 387.3e6,     # gating_fwd_kernel + gating_bwd_kernel (profiles/gating_cfg2_rows.md)
 }
 
 
 def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def _cpu_model():
+    """The host CPU's model name (what lscpu prints), from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 ATTENTION_CONFIGS = {
@@ -97,18 +111,18 @@ def attention_case(seed=0, config="cfg2"):
     return c
 
 
-def attention_step(c, timers=None):
+def attention_step(c, timers=None, precision="bf16"):
     from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
     Cb = precompute_boundaries(c["x"], c["unique"], c["rhos"], 64, c["c_base"])
     if timers is not None:
         timers["fwd"][0].record()
     O, LSE, *_ = flash_ema_forward(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
-                                   c["unique"], c["K"], Cb)
+                                   c["unique"], c["K"], Cb, precision=precision)
     if timers is not None:
         timers["fwd"][1].record()
         timers["bwd"][0].record()
     grads = flash_ema_backward(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
-                               c["unique"], Cb, O, LSE, c["dO"])
+                               c["unique"], Cb, O, LSE, c["dO"], precision=precision)
     if timers is not None:
         timers["bwd"][1].record()
     return grads
@@ -143,15 +157,44 @@ def cpu_baseline_attention(c, seconds=12.0):
         if elapsed > seconds:
             break
     return {"value": done / elapsed, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": _cpu_model(),
             "sample": (f"sequences 0..{len(slots) - 1} of the batch (K_b = {min(slots)}..{max(slots)} "
                        f"slots), all {L} steps each, forward + reference backward formulas in "
                        f"torch fp32 on {cores} threads; {elapsed:.1f} s")}
 
 
+def cpu_baseline_dense_forward(c, steps=12):
+    """The reference's dense all-vocabulary CPU forward (flash_ema_attention.py:19-85, the
+    oracle's restatement) on the first `steps` steps of one sequence.  Its work per step is
+    the same at every step and for every sequence (decay, gate and attend over all V slots),
+    so tokens/s is extrapolated from that sample to the whole batch; it has no backward (the
+    reference's in-place update blocks autograd)."""
+    from oracle import attention as att
+    d = c["cpu"]
+    H, hd, N, V = c["H"], c["hd"], c["N"], c["V"]
+    D = H * hd
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(321)
+    Q = torch.randn(1, steps, D, generator=g) * 0.02
+    Ek = torch.randn(V, D, generator=g) * 0.02
+    Ev = torch.randn(V, D, generator=g) * 0.02
+    Wp = torch.randn(D, N, generator=g) * 0.02
+    att.dense(Q[:, :1], d["x"][:1, :1], Ek, Ev, d["rhos"], Wp, H)   # warm-up step
+    t = time.perf_counter()
+    att.dense(Q, d["x"][:1, :steps], Ek, Ev, d["rhos"], Wp, H)
+    sec = time.perf_counter() - t
+    return {"value": round(steps / sec, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": _cpu_model(), "extrapolated": True,
+            "sample": (f"dense all-vocabulary forward only (V={V}, fp32, {cores} threads), the first "
+                       f"{steps} steps of sequence 0 in {sec:.1f} s; per-step work is constant, so the "
+                       f"rate is extrapolated to the B={c['B']}, T={c['L']} batch")}
+
+
 def run_attention(args):
     c = attention_case(config="cfg4" if args.workload == "cfg4" else "cfg2")
     for _ in range(args.warmup):
-        attention_step(c)
+        attention_step(c, precision=args.precision)
     torch.cuda.synchronize()
     timers_all = []
     t0, t1 = _events()
@@ -159,7 +202,7 @@ def run_attention(args):
     t0.record()
     for _ in range(args.steps):
         timers = {"fwd": _events(), "bwd": _events()}
-        attention_step(c, timers)
+        attention_step(c, timers, args.precision)
         timers_all.append(timers)
     t1.record()
     torch.cuda.synchronize()
@@ -190,22 +233,25 @@ def run_attention(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 gate MFMA (bf16 dW_pe MFMA), fp32 state/softmax/accumulate",
+        "dtype": ("fp16 gate MFMA (bf16 dW_pe MFMA), fp32 state/softmax/accumulate"
+                  if args.precision == "bf16" else
+                  "fp32 mode: fp16 hi+lo gate MFMA (bf16 hi+lo dW_pe MFMA), fp32 state/softmax/accumulate"),
         "data": "synthetic Zipf(1.1) tokens, seeded; random N(0,0.02) weights",
         "config": {"workload": workload,
                    "B": c["B"], "T": L, "d_model": D, "heads": c["H"], "head_dim": c["hd"],
                    "N": N, "V": c["V"], "K_max": c["K"], "sum_K_b": int(c["counts"].sum()),
                    "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
                    "fwd_bwd_tflops": round((fwd_flop + bwd_flop) / ((fwd_ms + bwd_ms) * 1e-3) / 1e12, 2),
-                   "parallelism": "single GPU"},
+                   "precision": args.precision, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "flash_ema_bwd_kernel",
                      "achieved": round(bwd_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(bwd_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": TRAFFIC_BYTES.get(c["config"])},
+                     "traffic": TRAFFIC_BYTES.get(c["config"]) if args.precision == "bf16" else None},
     }
     if not args.no_cpu_baseline and c["config"] == "cfg2":
         # (at cfg4 one whole sequence alone takes the oracle minutes)
         line["cpu_baseline"] = cpu_baseline_attention(c)
+        line["cpu_baseline_dense_forward"] = cpu_baseline_dense_forward(c)
     return line
 
 
@@ -259,7 +305,7 @@ def run_scan(args):
         touched += int(torch.isin(d["unique"][b, :d["counts"][b]], d["x"][b]).sum())
     nbytes = B * T * 8 + B * T * N * 4 + 2 * touched * N * 4 + touched * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {
+    line = {
         "metric": "EMA query scan GB/s (cfg3: B56 T2048 N128 V50257)",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
@@ -269,8 +315,24 @@ def run_scan(args):
                    "bytes_per_call": nbytes, "python_entry_ms": round(wrapper_ms, 4)},
         "roofline": {"bound": "hbm", "kernel": "ema_query_scan_kernel", "achieved": round(gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None},
+                     "traffic": TRAFFIC_BYTES["scan"]},
     }
+    if not args.no_cpu_baseline:
+        # the reference's CPU scan (dense per-vocabulary tables, a loop over T vectorised over
+        # B: triton_ema_query.py:67-117) on the whole configuration, as the oracle restates it
+        from oracle import scan as oscan
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        c0 = time.perf_counter()
+        oscan.query_scan_dense_loop(d["x"], d["rhos"], V, d["c_base"], d["unique"])
+        sec = time.perf_counter() - c0
+        line["cpu_baseline"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": cores,
+                                "kind": "port", "cpu_model": _cpu_model(),
+                                "sample": (f"the whole configuration (B={B}, T={T}, N={N}, V={V}) "
+                                           f"through the reference's dense-table loop in torch fp32 "
+                                           f"on {cores} threads: {sec:.2f} s, {B * T / sec:.0f} tokens/s; "
+                                           f"value = the same algorithmic bytes over that time")}
+    return line
 
 
 def run_gating(args):
@@ -327,7 +389,7 @@ def run_gating(args):
                        "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4)},
             "roofline": {"bound": "hbm", "kernel": "gating_fwd_kernel + gating_bwd_kernel",
                          "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES["gating"]}}
 
 
 def run_model(args):
@@ -339,7 +401,7 @@ def run_model(args):
     torch.set_float32_matmul_precision("high")   # train.py:94-95
     d = make_doc_batch(B, T, V, N, min_hl=1.0, max_hl=2048.0, seed=0)
     torch.manual_seed(1)
-    model = SlotTransformerLM(V, D, n_layers, H, N=N, dropout=0.1).to(dev)
+    model = SlotTransformerLM(V, D, n_layers, H, N=N, dropout=0.1, attn_precision=args.precision).to(dev)
     opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
     x, uniq, cb, tgt = (d[k].to(dev) for k in ("x", "unique", "c_base", "targets"))
     pm = uniq >= 0
@@ -369,7 +431,9 @@ def run_model(args):
     return {"metric": "SlotTransformerLM training step tokens/s (cfg5)", "value": round(B * T / (ms * 1e-3), 1),
             "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "bf16 autocast (attention fp32 state, fp16 gate MFMA)",
+            "vs_baseline": None,
+            "dtype": ("bf16 autocast (attention fp32 state, fp16 gate MFMA)" if args.precision == "bf16"
+                      else "bf16 autocast (attention fp32 mode: fp16 hi+lo gate MFMA)"),
             "data": "synthetic lognormal(median 1500) Zipf(1.1) documents, chunked, random init",
             "config": {"workload": "cfg5 full training step", "layers": n_layers, "d_model": D,
                        "heads": H, "N": N, "V": V, "B": B, "T": T, "params": n_params,
@@ -464,7 +528,7 @@ def run_corpus(args):
         od.corpus_states(tokens[:n], doc_ids[:n], rh.cpu().numpy())
         sec = time.perf_counter() - c0
         line["cpu_baseline"] = {"value": round(n / sec, 1), "unit": "tokens/s", "cores": 1,
-                                "kind": "port",
+                                "kind": "port", "cpu_model": _cpu_model(),
                                 "sample": "the first 2^22 tokens of the same corpus, data.py:276-303 "
                                           f"per-token loop in numpy ({sec:.1f} s)"}
     return line
@@ -577,7 +641,7 @@ def run_batch(args):
             nb += 1
         sec = time.perf_counter() - c0
         line["cpu_baseline"] = {"value": round(ntok / sec, 1), "unit": "tokens/s", "cores": 1,
-                                "kind": "port",
+                                "kind": "port", "cpu_model": _cpu_model(),
                                 "sample": f"{nb} of the timed batches, data.py:93-148 per-sample loop "
                                           f"+ collate in numpy ({sec:.1f} s)"}
     return line
@@ -652,7 +716,7 @@ def run_factored(args):
         o.backward(dO.cpu()[:1, :Tc])
         sec = time.perf_counter() - c0
         line["cpu_baseline"] = {"value": round(Tc / sec, 1), "unit": "tokens/s",
-                                "cores": torch.get_num_threads(), "kind": "port",
+                                "cores": torch.get_num_threads(), "kind": "port", "cpu_model": _cpu_model(),
                                 "sample": f"one sequence, its first {Tc} steps, factored_ema.py:22-96 "
                                           f"loop in torch fp32 + autograd backward ({sec:.1f} s)"}
     return line
@@ -667,6 +731,9 @@ def main():
                                            "corpus", "batch", "factored"),
                     default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--precision", choices=("bf16", "fp32"), default="bf16",
+                    help="attention gate operands: fp16 (bf16 mode, the default) or fp16 hi + lo "
+                         "pairs (fp32 mode); attention, cfg4 and model workloads")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "

@@ -3,7 +3,10 @@
 ``query_scan`` and ``boundary_states`` call the plain-C restatement in
 ``oracle/ema_oracle.c`` (built by ``oracle/Makefile``); the ``*_closed_form``
 functions evaluate the closed forms directly in float64 pure Python for tiny
-inputs and are what pins the C restatement.
+inputs and are what pins the C restatement.  ``query_scan_dense_loop`` is the
+reference's CPU algorithm itself (dense per-vocabulary state, one step at a time,
+vectorised over the batch) in torch: the CPU baseline the benchmark times at full size,
+pinned to the C restatement and the known answers in tests/test_oracle_scan.py.
 """
 import ctypes
 import os
@@ -137,3 +140,44 @@ def boundary_states_closed_form(x, unique, rhos, Br, c_init=None):
                         acc = acc + rhos ** (T - 1 - s)
                 out[b, j, k] = acc
     return out
+
+
+def query_scan_dense_loop(x, rhos, vocab_size, c_init=None, c_init_keys=None, doc_ids=None):
+    """C_seq [B, L, N] float32 by the algorithm of compute_query_ema_history_pt
+    (mathbrain/triton_ema_query.py:67-117): per-vocabulary tables of the last position
+    (-1e6 when unseen), the last counter row and the last document, a padding key -1 sent to
+    the spare row V (:84-88); at each step the row of x_t is decayed by rho^(t - T_last),
+    zeroed if its last occurrence was in another document, stored, and written back + 1
+    (:94-115).  torch, float32, on the CPU."""
+    import torch
+    x = torch.as_tensor(x).long()
+    rh = torch.as_tensor(rhos, dtype=torch.float32)
+    B, L = x.shape
+    N = rh.shape[0]
+    C_seq = torch.zeros(B, L, N, dtype=torch.float32)
+    T_last = torch.full((B, vocab_size + 1), -1000000.0, dtype=torch.float32)
+    C_last = torch.zeros(B, vocab_size + 1, N, dtype=torch.float32)
+    D_last = torch.full((B, vocab_size + 1), -1, dtype=torch.int32)
+    if c_init is not None and c_init_keys is not None:
+        keys = torch.as_tensor(c_init_keys).long()
+        keys = torch.where(keys == -1, torch.full_like(keys, vocab_size), keys)
+        T_last.scatter_(1, keys, 0.0)
+        C_last.scatter_(1, keys.unsqueeze(-1).expand(-1, -1, N),
+                        torch.as_tensor(c_init, dtype=torch.float32))
+        if doc_ids is not None:
+            first = torch.as_tensor(doc_ids)[:, :1].to(torch.int32).expand_as(keys)
+            D_last.scatter_(1, keys, first)
+    docs = None if doc_ids is None else torch.as_tensor(doc_ids).to(torch.int32)
+    bi = torch.arange(B)
+    for t in range(L):
+        xt = x[:, t]
+        tl = T_last[bi, xt]
+        c = C_last[bi, xt] * rh.unsqueeze(0) ** (t - tl).unsqueeze(1)
+        if docs is not None:
+            same = (D_last[bi, xt] == docs[:, t]) | (tl < 0)
+            c = c * same.unsqueeze(1).float()
+            D_last[bi, xt] = docs[:, t]
+        C_seq[:, t] = c
+        T_last[bi, xt] = float(t)
+        C_last[bi, xt] = c + 1.0
+    return C_seq.numpy()

@@ -183,3 +183,41 @@ def test_chunked_equals_single_pass(block):
     # here the chunk states come from numpy's pow and the scan from glibc powf,
     # each within 1 ulp, so the mean of |diff| is allowed a second ulp's worth.
     assert np.abs(truth - rebuilt).mean() < 2e-7
+
+
+# ---- the reference's dense-table CPU loop (the benchmark's CPU baseline) ------------
+
+def test_dense_loop_known_answers():
+    # tests/test_doc_boundary.py:71-105 and :108-134 through the dense-table loop
+    rhos = np.array([0.9, 0.5], np.float32)
+    x = np.array([[0, 1, 0, 2, 0, 1]])
+    C = scan.query_scan_dense_loop(x, rhos, 3, doc_ids=np.zeros_like(x))
+    assert np.allclose(C[0, 2], rhos ** 2, atol=1e-6)
+    assert np.allclose(C[0, 4], (rhos ** 2 + 1.0) * rhos ** 2, atol=1e-6)
+    x = np.array([[0, 1, 0, 2]])
+    c_init = np.array([[[2.0, 1.5], [0.0, 0.0], [0.0, 0.0]]], np.float32)
+    C = scan.query_scan_dense_loop(x, rhos, 3, c_init, np.array([[0, 1, 2]]), doc_ids=np.zeros_like(x))
+    assert np.allclose(C[0, 0], [2.0, 1.5])
+    x = np.array([[0, 1, 2, 0, 1, 0, 1, 3, 0, 1]])
+    doc = np.array([[0, 0, 0, 0, 0, 1, 1, 1, 1, 1]])
+    r4 = np.array([0.9, 0.8, 0.7, 0.6], np.float32)
+    C = scan.query_scan_dense_loop(x, r4, 5, doc_ids=doc)
+    assert np.allclose(C[0, 5], 0.0) and np.allclose(C[0, 8], r4 ** 3, atol=1e-6)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_dense_loop_equals_c_restatement(seed):
+    """Two independent restatements of the same reference function: the dense per-vocabulary
+    loop and the lazy C scan, with c_init, padding keys and document resets."""
+    rng = np.random.default_rng(seed)
+    B, L, V, N, K = 3, 200, 40, 8, 12
+    x = rng.integers(0, V, (B, L))
+    keys = np.stack([rng.permutation(V)[:K] for _ in range(B)])
+    keys[:, -2:] = -1
+    c_init = rng.random((B, K, N)).astype(np.float32) * 3
+    docs = np.cumsum(rng.random((B, L)) < 0.02, axis=1)
+    rhos = rhos_logspace(N, 1.0, 256.0)
+    for d in (None, docs):
+        a = scan.query_scan_dense_loop(x, rhos, V, c_init, keys, d)
+        b = scan.query_scan(x, rhos, V, c_init, keys, d)
+        assert np.allclose(a, b, rtol=1e-5, atol=1e-6), float(np.abs(a - b).max())
