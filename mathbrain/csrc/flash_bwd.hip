@@ -102,7 +102,11 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     const int g = lane >> 4;
     const int hl = wave & 3;
     const int th = wave >> 2;
-    const int h = hg * kBwdHeads + hl;
+    // a group holds hpg <= 4 heads (hpg divides H); waves of the missing heads only help
+    // stage and synchronise, and read head 0 for their (unused) setup
+    const int hpg = a.H / a.head_groups;
+    const bool active = hl < hpg;
+    const int h = active ? hg * hpg + hl : 0;
 
     // Gate weights as the B operand: W[n = 32 ns + 8 g + e][d = 16 dt + c16] * log2 e,
     // one fragment per (head, dt, ns, lane) in LDS.
@@ -116,7 +120,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int n = min(32 * ns + 8 * (ln >> 4) + e, a.N - 1);
-            w[e] = a.W[(int64_t)n * D + (hg * kBwdHeads + hh) * HD + 16 * dt + (ln & 15)];
+            w[e] = a.W[(int64_t)n * D + (hh < hpg ? hg * hpg + hh : 0) * HD + 16 * dt + (ln & 15)];
         }
         f16x8 v, vl;
 #pragma unroll
@@ -166,7 +170,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         for (int nt = 0; nt < NTW; ++nt) dWacc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     Producer<NPAD, SB, MAXI, MAXE> prod;
-    const int col0 = hg * WID;
+    const int col0 = hg * hpg * HD;  // WID columns from here are staged (zeros past D)
     // Forward scores of a batch, one float per thread (SCN <= blockDim.x): one register held
     // across the slot loop, not four.
     float s2pre = 0.f;
@@ -176,8 +180,8 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         const int hh = (threadIdx.x / kTB) % kBwdHeads;
         const int t = t0 + threadIdx.x % kTB;
         const int k = batch * SB + j;
-        s2pre = (k < kend && t < a.L)
-                    ? a.S2in[(((int64_t)b * a.H + hg * kBwdHeads + hh) * a.K + k) * a.L + t]
+        s2pre = (k < kend && t < a.L && hh < hpg)
+                    ? a.S2in[(((int64_t)b * a.H + hg * hpg + hh) * a.K + k) * a.L + t]
                     : 0.f;
     };
     auto store_scores = [&](float* dst) {
@@ -206,6 +210,10 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         const BatchMeta* meta = meta_of(bi);
         for (int j = 0; j < SB; ++j) {
             if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
+            if (!active) {                // a wave without a head: only the exchange barrier
+                if (XH) __syncthreads();
+                continue;
+            }
             // Forward scores of this lane's 4 steps, staged in LDS with the batch.
             f32x4 s2v = {0.f, 0.f, 0.f, 0.f};
             if (HAS_S)
@@ -382,7 +390,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int t = t0 + 16 * th + 4 * g + i;
-        if (t >= a.L) continue;
+        if (t >= a.L || !active) continue;
         float* dst = a.dQ + (((int64_t)b * a.H + h) * a.L + t) * HD;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) dst[16 * dt + c16] = dq[dt][i] * qf;
@@ -392,7 +400,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
             const int n = 16 * ((XH ? NTW * th : 0) + nt) + c16;
-            if (n >= a.N) continue;
+            if (n >= a.N || !active) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 atomicAdd(&a.dW[(int64_t)n * D + h * HD + 16 * dt + 4 * g + i], dWacc[dt][nt][i]);
@@ -415,7 +423,10 @@ static size_t bwd_lds_bytes() {
 template <int HD, int NS, int SB, bool PREC = false>
 static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     FlashArgsV a = a0;
-    a.head_groups = a.H / kBwdHeads;
+    int hpg = 1;  // heads per group: the largest divisor of H that is at most four
+    for (int d = kBwdHeads; d > 1; --d)
+        if (a.H % d == 0) { hpg = d; break; }
+    a.head_groups = a.H / hpg;
     constexpr int NPAD = 32 * NS;
     constexpr int WID = kBwdHeads * HD;
     const int nthr = 64 * 2 * kBwdHeads;
@@ -484,8 +495,6 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     int rc = flash_validate("mb_flash_ema_bwd", a, hd);
     if (rc) return rc;
     MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_bwd: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
-    if (H % kBwdHeads)
-        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: H=%d must be a multiple of %d", H, kBwdHeads);
     // dE_k, dE_v and dW_pe are accumulated with atomics, so they are cleared first -- also
     // when there is no step to accumulate (B or L zero), which leaves them zero; every dQ
     // element is written once.

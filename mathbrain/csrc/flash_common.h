@@ -297,7 +297,8 @@ struct Producer {
                 const int which = r / w4;
                 const int c4 = r % w4;
                 const int k = bi * SB + j;
-                if (k < kend) {
+                // columns past D (heads a partial head group does not have) stay zero
+                if (k < kend && col0 + c4 * 4 < D) {
                     const float* src =
                         (which ? a.Ev : a.Ek) + e_row<VR>(a, b, k, VR ? meta[j].u : 0) * D + col0 + c4 * 4;
                     v = *reinterpret_cast<const float4*>(src);

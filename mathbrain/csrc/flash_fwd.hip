@@ -40,14 +40,20 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
     const int D = a.H * HD;
     const int ntb = (a.L + kTB - 1) / kTB;
     const int logical = xcd_major(blockIdx.x, gridDim.x);
-    const int b = logical / ntb;
-    const int t0 = (logical % ntb) * kTB;
+    // one workgroup per (b, 32-step block, head group); a group holds hpg heads (hpg
+    // divides H), one wave each, and waves past hpg only help stage and synchronise
+    const int hg = logical % a.head_groups;
+    const int b = logical / (a.head_groups * ntb);
+    const int t0 = ((logical / a.head_groups) % ntb) * kTB;
     const int cbi = t0 / a.Br;
     const int cb = cbi * a.Br;
+    const int hpg = a.H / a.head_groups;
+    const int WIDF = hpg * HD;     // embedding columns staged: this group's heads
+    const int col0 = hg * WIDF;
 
     // LDS: two staging buffers, a 3-deep ring of batch slot info (batch i+2's info is
     // written while batch i is still being read), the window, the power table.
-    const int stage_bytes = (int)S::bytes(D);
+    const int stage_bytes = (int)S::bytes(WIDF);
     BatchMeta* metas = reinterpret_cast<BatchMeta*>(smem + 2 * stage_bytes);
     int64_t* win = reinterpret_cast<int64_t*>(metas + 3 * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
@@ -66,7 +72,8 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
     const int lane = threadIdx.x & 63;
     const int c16 = lane & 15;
     const int g = lane >> 4;
-    const int h = wave;
+    const bool active = wave < hpg;
+    const int h = active ? hg * hpg + wave : 0;  // idle waves read head 0 and write nothing
     const int x32 = (lane ^ 32) << 2;  // ds_bpermute byte address of lane l ^ 32
 
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
@@ -97,7 +104,7 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
                     lo[e] = (_Float16)(ws - (float)wf[dt][ns][e]);
                 }
                 // this wave's head's W_lo fragments, read back in the slot loop
-                if (PREC) wlo[((h * DT + dt) * NS + ns) * 64 + lane] = lo;
+                if (PREC) wlo[((wave * DT + dt) * NS + ns) * 64 + lane] = lo;
             }
     }
 
@@ -127,21 +134,22 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
     if (nb > 0) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
         if (VR) __syncthreads();  // the load reads the batch's token ids
-        prod.template load<VR>(a, b, cbi, 0, kend, D, 0, D, meta_of(0));
+        prod.template load<VR>(a, b, cbi, 0, kend, D, col0, WIDF, meta_of(0));
         __syncthreads();
-        prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), D);
+        prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), WIDF);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
 
     for (int bi = 0; bi < nb; ++bi) {
         const int cur = bi & 1;
-        if (bi + 1 < nb) prod.template load<VR>(a, b, cbi, bi + 1, kend, D, 0, D, meta_of(bi + 1));
+        if (bi + 1 < nb) prod.template load<VR>(a, b, cbi, bi + 1, kend, D, col0, WIDF, meta_of(bi + 1));
         const _Float16* cdec = cdec_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
         for (int j = 0; j < SB; ++j) {
-            if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
+            // padding slot (uniform across the workgroup), or a wave without a head
+            if (meta[j].u < 0 || !active) continue;
             f16x8 cf[2][NS];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
@@ -152,8 +160,8 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
             f32x4 ek[DT], ev[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                ek[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 0) * D + h * HD + 16 * dt + 4 * g);
-                ev[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 1) * D + h * HD + 16 * dt + 4 * g);
+                ek[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 0) * WIDF + wave * HD + 16 * dt + 4 * g);
+                ev[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 1) * WIDF + wave * HD + 16 * dt + 4 * g);
             }
             f32x4 gt[2][DT];
 #pragma unroll
@@ -171,7 +179,7 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
                     if (PREC) {  // small terms first
 #pragma unroll
                         for (int ns = 0; ns < NS; ++ns)
-                            acc = mfma16x16x32(wlo[((h * DT + dt) * NS + ns) * 64 + lane], cf[tt][ns], acc);
+                            acc = mfma16x16x32(wlo[((wave * DT + dt) * NS + ns) * 64 + lane], cf[tt][ns], acc);
 #pragma unroll
                         for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cl[ns], acc);
                     }
@@ -239,7 +247,7 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
         }
         if (bi + 1 < nb) {
             prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
-                                              E_of(cur ^ 1), D);
+                                              E_of(cur ^ 1), WIDF);
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();
@@ -249,7 +257,7 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         const int t = t0 + 16 * tt + c16;
-        if (t >= a.L) continue;
+        if (t >= a.L || !active) continue;
         const bool any = l[tt] > 0.f;
         const float inv = any ? kLn2 / l[tt] : 0.f;
         float* orow = a.O + (((int64_t)b * a.H + h) * a.L + t) * HD;
@@ -267,23 +275,36 @@ flash_ema_fwd_kernel(typename FlashArgsOf<VR>::type a) {
 }
 
 template <int HD, int NS, int SB, bool PREC>
-static size_t fwd_lds_bytes(int D, int H) {
-    return 2 * Stage<32 * NS, SB, false, PREC>::bytes(D) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
-           65 * 32 * NS * 4 + 16 + (PREC ? (size_t)H * (HD / 16) * NS * 64 * 16 : 0);
+static size_t fwd_lds_bytes(int width, int nwaves) {
+    return 2 * Stage<32 * NS, SB, false, PREC>::bytes(width) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
+           65 * 32 * NS * 4 + 16 + (PREC ? (size_t)nwaves * (HD / 16) * NS * 64 * 16 : 0);
+}
+
+// Heads per workgroup: all of them up to 8 (one wave each), else the largest divisor of
+// H that is at most 8, so that every group is whole.
+static int fwd_heads_per_group(int H) {
+    if (H <= 8) return H;
+    for (int d = 8; d > 1; --d)
+        if (H % d == 0) return d;
+    return 1;
 }
 
 template <int HD, int NS, int SB, bool PREC = false>
-static int launch_fwd(const FlashArgsV& a, bool vr, hipStream_t st) {
-    const int D = a.H * HD;
-    const int nthr = 64 * a.H;
+static int launch_fwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
+    FlashArgsV a = a0;
+    const int hpg = fwd_heads_per_group(a.H);
+    a.head_groups = a.H / hpg;
+    const int width = hpg * HD;
+    // at least four waves, so that the producer's share per thread stays bounded
+    const int nthr = 64 * (hpg < 4 ? 4 : hpg);
     constexpr int NPAD = 32 * NS;
     const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
-    const int nvec = SB * 2 * (D / 4);
-    const size_t lds = fwd_lds_bytes<HD, NS, SB, PREC>(D, a.H);
+    const int nvec = SB * 2 * (width / 4);
+    const size_t lds = fwd_lds_bytes<HD, NS, SB, PREC>(width, nthr / 64);
     if (lds > 160 * 1024)
-        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: D=%d, N=%d needs %zu B of LDS", D, a.N, lds);
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: %d heads of %d, N=%d need %zu B of LDS", hpg, HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
-    dim3 grid(a.B * ntb);
+    dim3 grid(a.B * ntb * a.head_groups);
     const FlashArgs& base = a;
 #define MB_FWD(MI, ME)                                                                           \
     do {                                                                                         \
@@ -297,7 +318,7 @@ static int launch_fwd(const FlashArgsV& a, bool vr, hipStream_t st) {
     } while (0)
     const int me = (nvec + nthr - 1) / nthr;
     if (mi > 4 || me > 4)
-        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: D=%d, N=%d too wide for %d threads", D, a.N, nthr);
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: width %d, N=%d too wide for %d threads", width, a.N, nthr);
     if (mi <= 1 && me <= 1) MB_FWD(1, 1);
     else if (mi <= 1 && me <= 2) MB_FWD(1, 2);
     else if (mi <= 2 && me <= 2) MB_FWD(2, 2);
@@ -313,8 +334,7 @@ int flash_validate(const char* who, const FlashArgs& a, int hd) {
     MB_REQUIRE(a.N >= 1 && a.Np >= a.N, "%s: need 1 <= N=%d <= Np=%d", who, a.N, a.Np);
     if (hd != 32 && hd != 64)
         return fail(MB_ERR_UNSUPPORTED, "%s: head_dim %d (supported: 32, 64)", who, hd);
-    if (a.H < 4 || a.H > 8)
-        return fail(MB_ERR_UNSUPPORTED, "%s: %d heads (supported: 4..8, one wave per head)", who, a.H);
+    if (a.H > 64) return fail(MB_ERR_UNSUPPORTED, "%s: %d heads (supported: 1..64)", who, a.H);
     if (a.N > 128) return fail(MB_ERR_UNSUPPORTED, "%s: N=%d > 128", who, a.N);
     MB_REQUIRE(a.Br >= 1, "%s: Br=%d must be >= 1", who, a.Br);
     if (!(a.Br <= 32 || a.Br == 64))
