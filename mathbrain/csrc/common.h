@@ -62,29 +62,32 @@ __device__ inline void log2_split(float rho, float& hi, float& lo) {
     lo = __builtin_isfinite(l) ? (float)(l - (double)hi) : 0.0f;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave on DPP: shifts by 1, 2, 4 and 8 lanes
+// inside each row of 16 (lanes shifted in from outside the row add 0), then lane 15's sum
+// broadcast into rows 1 and 3 and lane 31's into rows 2 and 3.  No LDS traffic.
+__device__ inline int wave_inclusive_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+
 // Exclusive scan of one int per thread over a whole block (blockDim.x a multiple of 64,
-// at most 1024).  `scratch` holds >= 16 ints of LDS.  Returns the exclusive prefix and
+// at most 1024).  `scratch` holds >= 33 ints of LDS.  Returns the exclusive prefix and
 // writes the block total to `total`.
 __device__ inline int block_exclusive_scan(int v, int* scratch, int& total) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nwaves = blockDim.x >> 6;
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        int o = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += o;
-    }
+    const int incl = wave_inclusive_scan(v);
     if (lane == 63) scratch[wave] = incl;
     __syncthreads();
     if (wave == 0) {
-        int w = lane < nwaves ? scratch[lane] : 0;
-        int wi = w;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-            int o = __shfl_up(wi, d, 64);
-            if (lane >= d) wi += o;
-        }
+        const int w = lane < nwaves ? scratch[lane] : 0;
+        const int wi = wave_inclusive_scan(w);
         if (lane < nwaves) scratch[16 + lane] = wi - w;  // exclusive wave offsets
         if (lane == nwaves - 1) scratch[32] = wi;
     }

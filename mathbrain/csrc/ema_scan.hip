@@ -20,19 +20,21 @@ constexpr size_t kMaxLds = 160 * 1024;
 
 // ---- query scan ---------------------------------------------------------------------------
 //
-// After the sort, chain c is the sorted range [chain_start[c], chain_start[c+1]) and the
-// recurrence along it, in pre-increment values C_j = C_seq at the chain's j-th position,
+// After the sort, chain c is the sorted range [chain_start[c], chain_start[c+1]) of one
+// token, and the recurrence along it, in pre-increment values C_j = C_seq at the chain's
+// j-th position,
 //   C_1 = c0 rho^t_1,   C_j = (C_{j-1} + 1) rho^(t_j - t_{j-1})
-// is linear.  Chains are cut into segments of at most S elements, so that no lane group
-// walks more than S steps however frequent a token is (the top Zipf token of a 2048-token
-// sequence occurs ~190 times).  Pass A walks every segment that is not its chain's last
-// one from zero and keeps its local sum at the segment's last element,
-//   agg_k = sum_{j in segment k, j < last} rho^(t_last - t_j),
-// in LDS.  Pass B walks every segment again and writes C_seq; segment i of a chain first
-// rebuilds its carry-in from the chain's earlier aggregates,
-//   C_last(k) = (C_last(k-1) + 1) rho^(t_last(k) - t_last(k-1)) + agg_k,
-// (C_last(-1) + 1 := c0 at t = 0), which costs i <= L/S steps.  With doc_ids, a segment
-// that contains a document change drops its carry (flag kept beside the aggregate).
+// is linear.  The sorted order is cut every S elements (S a power of two): lane group g
+// walks the range [g S, (g + 1) S) in lockstep with the other groups of its wave, S steps
+// for every group however the chains fall.  A range that starts inside a chain needs the
+// chain's state at its start: pass A walks, for every cut m that falls inside a chain, the
+// chain's piece that the cut closes, from zero, and keeps its local sum at the piece's last
+// element j_m = m S - 1,
+//   agg_m = sum_{j in piece, j < j_m} rho^(t_{j_m} - t_j),
+// in LDS.  Pass B rebuilds a range's carry-in from the chain's earlier cuts,
+//   P(m) = P(m') rho^(t_{j_m} - t_{j_m'}) + agg_m + 1     (post-increment state at t_{j_m}),
+// (P := c0 at t = 0 before the first cut), which costs at most L/S steps.  With doc_ids, a
+// piece that contains a document change drops its carry (flag kept beside the aggregate).
 
 template <int VEC>
 struct Vec {
@@ -67,6 +69,15 @@ __device__ inline void store_vec(float* dst, const float* v, int n0, int N) {
     }
 }
 
+// Makes every register of `a` ready here.  Vector-memory waits count loads and stores in
+// one in-order counter, so a load's first use after some stores also waits for those
+// stores; settling a chunk's loads before its stores leaves the walk with no such waits.
+template <typename T, int n>
+__device__ inline void settle(T (&a)[n]) {
+#pragma unroll
+    for (int i = 0; i < n; ++i) asm volatile("" : "+v"(a[i]));
+}
+
 // x^e for an integer e >= 0 by binary exponentiation in double precision.
 __device__ inline double powi(double x, int e) {
     double r = 1.0;
@@ -78,187 +89,210 @@ __device__ inline double powi(double x, int e) {
     return r;
 }
 
-// Radix sort rounds per wave (64 keys each): 2 cover L <= 2048 with 16 waves, and that
-// variant is register-light enough for two workgroups per CU; 8 cover L <= 8192.
+// Radix sort rounds per wave (64 keys each): 2 cover L <= 2048 with 16 waves, 8 cover
+// L <= 8192.  A thread holds at most MAXR tokens of its sequence.
 constexpr int kScanRoundsSmall = 2;
 constexpr int kScanRoundsLarge = 8;
+// Loads issued before the sort so that its LDS phases hide their latency: c_init key ids
+// (K <= 4 * 1024 in registers, more are fetched during the lookup) and power-table entries.
+constexpr int kKeyPrefetch = 4;
+constexpr int kTablePrefetch = 4;
 
-// Byte offsets of the per-sequence index inside dynamic LDS.  The radix sort's scratch,
-// the slot lookup's element->chain map and the power tables are live at different times
-// and share space.
+// Byte offsets of the per-sequence index inside dynamic LDS.  The sorted keys take Lp =
+// 2^ceil(log2 L) entries (the tail holds all-ones sentinels for the lookup); the radix
+// sort's scratch overlaps everything after them.
 struct ScanLds {
-    size_t keys, chain_start, chain_seg, seg_chain, nf_seg, chain_key, r1;
-    size_t sort_b, sort_cnt;             // during the sort (from the end of keys)
-    size_t elem_chain, scan_scratch;     // during the chain build and slot lookup (r1)
-    size_t agg, aggr, lowT, highT;       // during the walks (r1)
+    size_t keys, chain_start, elem_chain, chain_key, agg, aggr, lowT, highT, scan_scratch;
+    size_t sort_b, sort_cnt;
     size_t total;
-    __host__ __device__ ScanLds(int L, int key_bytes, int nthr, int nf_max, int slice_w, int nH) {
+    // rows of the power tables and of the cut aggregates hold 1 << lgRow floats (the slice
+    // width rounded up to a power of two, so that row addressing is a shift)
+    __host__ __device__ ScanLds(int L, int Lp, int key_bytes, int nthr, int ncut, int nH, int lgRow) {
         auto al = [](size_t o) { return (o + 15) & ~(size_t)15; };
         keys = 0;
-        size_t o = al((size_t)L * key_bytes);
+        size_t o = al((size_t)Lp * key_bytes);
         const size_t after_keys = o;
-        chain_start = o; o += (size_t)(L + 1) * 2;
-        chain_seg = o;   o += (size_t)(L + 1) * 2;
-        seg_chain = o;   o += (size_t)L * 2;
-        nf_seg = o;      o += (size_t)nf_max * 2;
-        o = al(o);
-        chain_key = o;   o += (size_t)L * 4;
-        r1 = o = al(o);
-        elem_chain = r1;
-        agg = r1;
-        aggr = agg + (size_t)nf_max * slice_w * 4;
-        lowT = al(aggr + (size_t)nf_max * 4);
-        highT = lowT + (size_t)64 * slice_w * 4;
-        const size_t walk_end = highT + (size_t)nH * slice_w * 4;
-        scan_scratch = al(elem_chain + (size_t)L * 2);
-        const size_t lookup_end = scan_scratch + 64 * 4;
+        chain_start = o;  o += (size_t)(L + 1) * 2;
+        elem_chain = o;   o += (size_t)L * 2;
+        chain_key = o = al(o);
+        o += (size_t)L * 4;
+        agg = o;          o += (size_t)(ncut + 1) * 4 << lgRow;
+        aggr = o;         o += (size_t)(ncut + 1) * 4;
+        lowT = o = al(o);
+        highT = lowT + ((size_t)64 * 4 << lgRow);
+        o = highT + ((size_t)nH * 4 << lgRow);
+        scan_scratch = o = al(o);
+        o += 64 * 4;
+        total = al(o);
         sort_b = after_keys;
         sort_cnt = al(sort_b + (size_t)L * key_bytes);
-        const size_t sort_end = sort_cnt + (size_t)(4 * nthr + 64) * 4;
-        total = al(walk_end > lookup_end ? walk_end : lookup_end);
-        if (sort_end > total) total = al(sort_end);
+        const size_t sort_end = al(sort_cnt + (size_t)(4 * nthr + 64) * 4);
+        if (sort_end > total) total = sort_end;
     }
 };
 
 // Query scan: one workgroup per (sequence b, slice of slice_w decay rates).
-//   1. keys = (token << pb | position) in position order, stably radix-sorted by token:
-//      chain c = the sorted range [chain_start[c], chain_start[c+1]) of one token.
-//   2. chains are cut into segments of at most S elements; c_init keys are matched to
-//      their chains.
-//   3. pass A: local aggregates of the non-final segments; pass B: every segment rebuilds
-//      its carry-in from its chain's earlier aggregates and writes its C_seq rows.
+//   0. this thread's tokens, c_init key ids and power-table entries go to registers;
+//   1. keys = (token << pb | position) in position order, stably radix-sorted by token;
+//   2. one block scan numbers the chains (element -> chain map, chain starts); the power
+//      tables go to LDS;
+//   3. c_init keys are matched to their chains (the last duplicate wins);
+//   4. each lane group gathers its range's first chunk and issues its c_init row loads;
+//      pass A computes the cut aggregates meanwhile;
+//   5. pass B: every group walks its range and writes the C_seq rows (and the final state
+//      and stamp at each chain's last element).
 // rho^d comes from two LDS tables per rate, rho^(d mod 64) * rho^(64 floor(d / 64)),
 // each entry a correctly rounded float of a double-precision power.
 template <typename KeyT, int VEC, bool DOCS, int MAXR>
-__global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(MAXR <= 2 ? 8 : 1)))
+__global__ void __launch_bounds__(kScanThreads)
 ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L,
                       const float* __restrict__ rhos, int N, const float* __restrict__ c_init,
                       const int64_t* __restrict__ c_init_keys, int K,
                       const int64_t* __restrict__ doc_ids, float* __restrict__ C_seq,
                       float* state_out, int32_t* __restrict__ stamp_out, int pb, int tok_bits,
-                      int slice_w, int S, int nf_max) {
+                      int slice_w, int lgS, int ncut) {
+    // elements per unrolled chunk of a pass-B walk; their c_init rows (and with doc_ids
+    // their documents) sit in registers
+    constexpr int CH = DOCS ? 4 : 8;
     extern __shared__ __align__(16) unsigned char smem[];
     const int b = blockIdx.x;
     const int slice = blockIdx.y;
+    const int nthr = blockDim.x;
     const int nH = (L - 1) / 64 + 1;
-    const ScanLds lay(L, (int)sizeof(KeyT), blockDim.x, nf_max, slice_w, nH);
+    const int Lp = 1 << pb;
+    const int lgRow = ceil_log2(slice_w);
+    const ScanLds lay(L, Lp, (int)sizeof(KeyT), nthr, ncut, nH, lgRow);
     KeyT* keys = reinterpret_cast<KeyT*>(smem + lay.keys);
     uint16_t* chain_start = reinterpret_cast<uint16_t*>(smem + lay.chain_start);
-    uint16_t* chain_seg = reinterpret_cast<uint16_t*>(smem + lay.chain_seg);
-    uint16_t* seg_chain = reinterpret_cast<uint16_t*>(smem + lay.seg_chain);
-    uint16_t* nf_seg = reinterpret_cast<uint16_t*>(smem + lay.nf_seg);
-    int* chain_key = reinterpret_cast<int*>(smem + lay.chain_key);
     uint16_t* elem_chain = reinterpret_cast<uint16_t*>(smem + lay.elem_chain);
+    int* chain_key = reinterpret_cast<int*>(smem + lay.chain_key);
     float* agg = reinterpret_cast<float*>(smem + lay.agg);
     int* aggr = reinterpret_cast<int*>(smem + lay.aggr);
     float* lowT = reinterpret_cast<float*>(smem + lay.lowT);
     float* highT = reinterpret_cast<float*>(smem + lay.highT);
-    int* scratch;
+    int* scratch = reinterpret_cast<int*>(smem + lay.scan_scratch);
+    const int S = 1 << lgS;
 
-    // 1. sorted (token, position) keys
+    // 0. early loads: tokens, c_init key ids, rates; then the power-table entries
+    // (double-precision work that overlaps the loads' latency)
+    uint64_t tokv[MAXR];
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) {
+        const int i = threadIdx.x + r * nthr;
+        tokv[r] = i < L ? (uint64_t)x[(int64_t)b * sb + (int64_t)i * sl] : 0;
+    }
+    int64_t pre_key[kKeyPrefetch];
+#pragma unroll
+    for (int r = 0; r < kKeyPrefetch; ++r) {
+        const int k = threadIdx.x + r * nthr;
+        pre_key[r] = k < K ? c_init_keys[(int64_t)b * K + k] : (int64_t)-1;
+    }
+    const int n_tab = (64 + nH) * slice_w;
+    auto table_value = [](int j, double rho) -> float {
+        return (float)(j < 64 ? powi(rho, j) : powi(powi(rho, 64), j - 64));
+    };
+    auto table_rate = [&](int i) { return slice * slice_w + i % slice_w; };
+    float pre_tab[kTablePrefetch];
+#pragma unroll
+    for (int r = 0; r < kTablePrefetch; ++r) {
+        const int i = threadIdx.x + r * nthr;
+        pre_tab[r] = i < n_tab && table_rate(i) < N ? rhos[table_rate(i)] : 0.f;
+    }
+    const int64_t doc0 = DOCS ? doc_ids[(int64_t)b * L] : 0;
+#pragma unroll
+    for (int r = 0; r < kTablePrefetch; ++r) {
+        const int i = threadIdx.x + r * nthr;
+        pre_tab[r] = i < n_tab ? table_value(i / slice_w, (double)pre_tab[r]) : 0.f;
+    }
+
+    // 1. sorted (token, position) keys, then all-ones sentinels up to Lp
     {
         const KeyT tokmask = (pb == 0) ? ~KeyT(0) : ((~KeyT(0)) >> pb);
-        for (int i = threadIdx.x; i < L; i += blockDim.x) {
-            const uint64_t tok = (uint64_t)x[(int64_t)b * sb + (int64_t)i * sl];
-            keys[i] = ((KeyT)tok & tokmask) << pb | (KeyT)i;
+#pragma unroll
+        for (int r = 0; r < MAXR; ++r) {
+            const int i = threadIdx.x + r * nthr;
+            if (i < L) keys[i] = ((KeyT)tokv[r] & tokmask) << pb | (KeyT)i;
         }
         __syncthreads();
         KeyT* sorted = block_radix_sort<MAXR>(keys, reinterpret_cast<KeyT*>(smem + lay.sort_b),
-                                                        reinterpret_cast<int*>(smem + lay.sort_cnt), L,
-                                                        pb, tok_bits);
+                                              reinterpret_cast<int*>(smem + lay.sort_cnt), L, pb,
+                                              tok_bits);
         if (sorted != keys) {
-            for (int i = threadIdx.x; i < L; i += blockDim.x) keys[i] = sorted[i];
+            for (int i = threadIdx.x; i < L; i += nthr) keys[i] = sorted[i];
             __syncthreads();
         }
+        for (int i = L + threadIdx.x; i < Lp; i += nthr) keys[i] = ~KeyT(0);
     }
-    scratch = reinterpret_cast<int*>(smem + lay.scan_scratch);
 
-    // chain heads (first element of each token run), element -> chain map
-    const int per = (L + blockDim.x - 1) / blockDim.x;
-    const int i0 = threadIdx.x * per;
-    const int i1 = min(i0 + per, L);
-    int cnt = 0;
-    for (int i = i0; i < i1; ++i) cnt += (i == 0 || (keys[i] >> pb) != (keys[i - 1] >> pb));
-    int n_chains;
-    int c = block_exclusive_scan(cnt, scratch, n_chains);
-    for (int i = i0; i < i1; ++i) {
-        if (i == 0 || (keys[i] >> pb) != (keys[i - 1] >> pb)) chain_start[c++] = (uint16_t)i;
-        elem_chain[i] = (uint16_t)(c - 1);
-    }
-    if (threadIdx.x == 0) chain_start[n_chains] = (uint16_t)L;
-    if (stamp_out && slice == 0)
-        for (int k = threadIdx.x; k < K; k += blockDim.x) stamp_out[(int64_t)b * K + k] = -1;
-    __syncthreads();
-
-    // 2. segments: chain c owns segments [chain_seg[c], chain_seg[c+1])
-    const int cper = (n_chains + blockDim.x - 1) / blockDim.x;
-    const int c0i = threadIdx.x * cper;
-    const int c1i = min(c0i + cper, n_chains);
-    int nseg = 0;
-    for (int cc = c0i; cc < c1i; ++cc) nseg += (chain_start[cc + 1] - chain_start[cc] + S - 1) / S;
-    int n_segs;
-    int so = block_exclusive_scan(nseg, scratch, n_segs);
-    for (int cc = c0i; cc < c1i; ++cc) {
-        chain_seg[cc] = (uint16_t)so;
-        chain_key[cc] = -1;
-        const int ns = (chain_start[cc + 1] - chain_start[cc] + S - 1) / S;
-        for (int q = 0; q < ns; ++q) seg_chain[so + q] = (uint16_t)cc;
-        for (int q = 0; q + 1 < ns; ++q) nf_seg[so - cc + q] = (uint16_t)(so + q);
-        so += ns;
-    }
-    if (threadIdx.x == 0) chain_seg[n_chains] = (uint16_t)n_segs;
-    __syncthreads();
-
-    // each key row seeds the chain of its token; the last duplicate key wins, as a
-    // sequential scatter_ leaves it (triton_ema_query.py:146-149).  Four lookups per
-    // thread run in lockstep so their dependent LDS reads overlap.
-    for (int kb = threadIdx.x; kb < K; kb += 4 * blockDim.x) {
-        uint64_t tok[4];
-        int lo[4], hi[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int k = kb + r * blockDim.x;
-            const int64_t u = k < K ? c_init_keys[(int64_t)b * K + k] : (int64_t)-1;
-            tok[r] = (uint64_t)u;
-            lo[r] = 0;
-            hi[r] = u < 0 ? 0 : L;
-        }
-        for (int it = 0; it < 32; ++it) {
-            bool any = false;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (lo[r] < hi[r]) {
-                    const int mid = (lo[r] + hi[r]) >> 1;
-                    if ((uint64_t)(keys[mid] >> pb) < tok[r]) lo[r] = mid + 1; else hi[r] = mid;
-                    any = true;
-                }
+    // 2. chain ids from one scan of head counts, element -> chain map, chain starts; the
+    // power tables (highT follows lowT: entry j >= 64 is rho^(64 (j - 64)))
+    {
+        const int per = (L + nthr - 1) / nthr;
+        const int i0 = threadIdx.x * per;
+        const int i1 = min(i0 + per, L);
+        auto chain_head = [&](int i) { return i == 0 || (keys[i] >> pb) != (keys[i - 1] >> pb); };
+        int cnt = 0;
+        for (int i = i0; i < i1; ++i) cnt += chain_head(i);
+        int n_chains;
+        int c = block_exclusive_scan(cnt, scratch, n_chains);
+        for (int i = i0; i < i1; ++i) {
+            if (chain_head(i)) {
+                chain_start[c] = (uint16_t)i;
+                chain_key[c] = -1;
+                ++c;
             }
-            if (!any) break;
+            elem_chain[i] = (uint16_t)(c - 1);
+        }
+        if (threadIdx.x == 0) chain_start[n_chains] = (uint16_t)L;
+        auto table_slot = [&](int i) { return ((i / slice_w) << lgRow) + i % slice_w; };
+#pragma unroll
+        for (int r = 0; r < kTablePrefetch; ++r) {
+            const int i = threadIdx.x + r * nthr;
+            if (i < n_tab) lowT[table_slot(i)] = pre_tab[r];
+        }
+        for (int i = threadIdx.x + kTablePrefetch * nthr; i < n_tab; i += nthr)
+            lowT[table_slot(i)] = table_rate(i) < N ? table_value(i / slice_w, (double)rhos[table_rate(i)]) : 0.f;
+        if (stamp_out && slice == 0)
+            for (int k = threadIdx.x; k < K; k += nthr) stamp_out[(int64_t)b * K + k] = -1;
+        __syncthreads();
+    }
+
+    // 3. each key row seeds the chain of its token; the last duplicate key wins, as a
+    // sequential scatter_ leaves it (triton_ema_query.py:146-149).  Lower bounds by halving
+    // steps over the Lp sentinel-padded keys: no bounds test, so a thread's lookups keep
+    // their LDS reads in flight together.
+    // Token ids compare in KeyT.  A key id that no sorted token can equal (negative, or
+    // wider than the key layout's token field) searches for all-ones and is never matched.
+    const uint64_t tok_lim = (uint64_t)(KeyT)~KeyT(0) >> pb;  // largest token the keys hold
+    for (int kb = threadIdx.x; kb < K; kb += kKeyPrefetch * nthr) {
+        KeyT tok[kKeyPrefetch];
+        int lo[kKeyPrefetch];
+        bool valid[kKeyPrefetch];
+#pragma unroll
+        for (int r = 0; r < kKeyPrefetch; ++r) {
+            const int k = kb + r * nthr;
+            const int64_t u = kb == (int)threadIdx.x ? pre_key[r]
+                                                     : (k < K ? c_init_keys[(int64_t)b * K + k] : (int64_t)-1);
+            valid[r] = k < K && u >= 0 && (uint64_t)u <= tok_lim;
+            tok[r] = valid[r] ? (KeyT)u : ~KeyT(0);
+            lo[r] = 0;  // every key before lo is below tok
+        }
+        for (int step = Lp >> 1; step > 0; step >>= 1) {
+#pragma unroll
+            for (int r = 0; r < kKeyPrefetch; ++r)
+                lo[r] += (KeyT)(keys[lo[r] + step - 1] >> pb) < tok[r] ? step : 0;
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int k = kb + r * blockDim.x;
-            if (k < K && (int64_t)tok[r] >= 0 && lo[r] < L && (uint64_t)(keys[lo[r]] >> pb) == tok[r])
-                atomicMax(&chain_key[elem_chain[lo[r]]], k);
+        for (int r = 0; r < kKeyPrefetch; ++r) {
+            lo[r] += (KeyT)(keys[lo[r]] >> pb) < tok[r] ? 1 : 0;
+            if (valid[r] && lo[r] < L && (KeyT)(keys[lo[r]] >> pb) == tok[r])
+                atomicMax(&chain_key[elem_chain[lo[r]]], kb + r * nthr);
         }
     }
-    __syncthreads();  // elem_chain is dead from here; r1 now holds the tables and aggregates
-
-    // power tables of this slice's rates
-    for (int i = threadIdx.x; i < (64 + nH) * slice_w; i += blockDim.x) {
-        const int j = i / slice_w;
-        const int r = i % slice_w;
-        const int nn = slice * slice_w + r;
-        float v = 0.f;
-        if (nn < N) {
-            const double rho = (double)rhos[nn];
-            v = (float)(j < 64 ? powi(rho, j) : powi(powi(rho, 64), j - 64));
-        }
-        lowT[i] = v;  // highT follows lowT: entry j >= 64 is rho^(64 (j - 64))
-    }
+    __syncthreads();
 
     const int lanes = slice_w / VEC;
-    const int groups = blockDim.x / lanes;
+    const int groups = nthr / lanes;
     const int g = threadIdx.x / lanes;
     const int lane_r = (threadIdx.x % lanes) * VEC;  // rate offset inside the slice
     const int n0 = slice * slice_w + lane_r;
@@ -268,8 +302,8 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     auto doc_of = [&](int pos) { return doc_ids[(int64_t)b * L + pos]; };
     // rho^d for this lane's VEC rates
     auto powv = [&](int d, float* pw) {
-        const float* lo = lowT + (d & 63) * slice_w + lane_r;
-        const float* hi = highT + (d >> 6) * slice_w + lane_r;
+        const float* lo = lowT + ((d & 63) << lgRow) + lane_r;
+        const float* hi = highT + ((d >> 6) << lgRow) + lane_r;
         if (VEC == 4) {
             const float4 a = *reinterpret_cast<const float4*>(lo);
             const float4 h = *reinterpret_cast<const float4*>(hi);
@@ -279,127 +313,157 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
             for (int v = 0; v < VEC; ++v) pw[v] = lo[v] * hi[v];
         }
     };
-    float* const Cb = C_seq + (int64_t)b * L * N + n0;
-    __syncthreads();
+    // row offsets as 24-bit products from per-sequence bases (the host checks L * N and
+    // K * N against 2^31 and K against 2^24)
+    float* const Cb = C_seq + (int64_t)b * L * N;
+    const float* const c0b = c_init + (int64_t)b * K * N;
+    float* const stb = state_out ? state_out + (int64_t)b * K * N : nullptr;
+    auto row = [&](int r) { return (int)__umul24((unsigned)r, (unsigned)N) + n0; };
 
-    // 3a. pass A: local aggregates of the non-final segments
-    const int n_nf = n_segs - n_chains;
-    if (g < groups) {
-        for (int f = g; f < n_nf; f += groups) {
-            const int s = nf_seg[f];
-            const int cc = seg_chain[s];
-            const int qi = s - chain_seg[cc];
-            const int beg = chain_start[cc] + qi * S;
-            float h[VEC];
+    // 4. this group's sorted range [ra, re) (the host picks S so that no group has two),
+    // its first chunk's walk starts and their c_init rows.  A walk starts at the range's
+    // first element and at every chain head; `key` -1 marks a start without a key row.
+    const int ra = g * S;
+    const int re = g < groups && ra < L ? min(ra + S, L) : ra;
+    Vec<VEC> c0v[CH];
+    int keyv[CH];
+    int64_t docv[CH];
+    uint32_t startm = 0, lastm = 0;  // bit e: element c + e starts a walk / ends its chain
+    auto gather = [&](int c) {
+        startm = lastm = 0;
+        int prev = c > 0 ? elem_chain[c - 1] : -1;
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) h[v] = 0.f;
-            int reset = 0;
-            int tp = pos_of(beg);
-            int64_t dprev = 0;
+        for (int e = 0; e < CH; ++e) {
+            const int j = c + e;
+            const bool in = j < re;
+            const int cid = in ? elem_chain[j] : prev;
+            const int nxt = in && j + 1 < L ? elem_chain[j + 1] : -1;
+            const bool start = in && (j == ra || cid != prev);
+            startm |= (start ? 1u : 0u) << e;
+            lastm |= (in && nxt != cid ? 1u : 0u) << e;
+            keyv[e] = start ? chain_key[cid] : -1;
+            c0v[e] = load_vec<VEC>(c0b + row(keyv[e] >= 0 ? keyv[e] : 0), start && keyv[e] >= 0 && active,
+                                   n0, N);
+            if (DOCS) docv[e] = in ? doc_of(pos_of(j)) : 0;
+            prev = cid;
+        }
+    };
+    if (ra < re) gather(ra);
+
+    // pass A: the aggregate of the chain piece that each interior cut closes (cut g + 1
+    // closes this group's range)
+    for (int m = 1 + g; g < groups && m <= ncut; m += groups) {
+        const int last = m << lgS;
+        const int cc = elem_chain[last - 1];
+        if (cc != elem_chain[last]) continue;  // a chain starts at the cut
+        const int cs = chain_start[cc];
+        const int beg = max(cs, last - S);
+        float h[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) h[v] = 0.f;
+        int reset = 0;
+        int tp = pos_of(beg);
+        int64_t dprev = 0;
+        if (DOCS) {
+            const bool first = beg == cs;
+            const bool has_prev = !first || chain_key[cc] >= 0;
+            const int64_t dcur = doc_of(tp);
+            const int64_t dref = first ? doc0 : doc_of(pos_of(beg - 1));
+            reset = has_prev && dref != dcur;
+            dprev = dcur;
+        }
+        int tn = pos_of(min(beg + 1, last - 1));
+        for (int j = beg + 1; j < last; ++j) {
+            const int t = tn;
+            tn = pos_of(min(j + 1, last - 1));  // next position, read one step ahead
+            float pw[VEC];
+            powv(t - tp, pw);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) h[v] = (h[v] + 1.0f) * pw[v];
             if (DOCS) {
-                const bool has_prev = qi > 0 || chain_key[cc] >= 0;
-                const int64_t dcur = doc_of(tp);
-                const int64_t dref = qi > 0 ? doc_of(pos_of(beg - 1)) : doc_of(0);
-                reset = has_prev && dref != dcur;
+                const int64_t dcur = doc_of(t);
+                if (dcur != dprev) {
+                    reset = 1;
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) h[v] = 0.f;
+                }
                 dprev = dcur;
             }
-            for (int j = beg + 1; j < beg + S; ++j) {
-                const int t = pos_of(j);
-                float pw[VEC];
-                powv(t - tp, pw);
-#pragma unroll
-                for (int v = 0; v < VEC; ++v) h[v] = (h[v] + 1.0f) * pw[v];
-                if (DOCS) {
-                    const int64_t dcur = doc_of(t);
-                    if (dcur != dprev) {
-                        reset = 1;
-#pragma unroll
-                        for (int v = 0; v < VEC; ++v) h[v] = 0.f;
-                    }
-                    dprev = dcur;
-                }
-                tp = t;
-            }
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) agg[f * slice_w + lane_r + v] = h[v];
-            if (DOCS && lane_r == 0) aggr[f] = reset;
+            tp = t;
         }
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) agg[(m << lgRow) + lane_r + v] = h[v];
+        if (DOCS && lane_r == 0) aggr[m] = reset;
     }
     __syncthreads();
 
-    // 3b. pass B: every segment, from its carry-in, writes C_seq rows (and the final
-    // state).  A group takes its segments kBatch at a time and issues their c_init row
-    // loads first.
-    constexpr int kBatch = MAXR <= 2 ? 2 : 4;
-    if (g < groups) {
-        for (int s0 = g; s0 < n_segs; s0 += kBatch * groups) {
-            Vec<VEC> c0v[kBatch];
-            int keyv[kBatch];
+    // 5. pass B: the walk, CH elements per chunk; P is the post-increment state at time tp.
+    // The range's first element starts from its chain's c0 and, when the range starts inside
+    // the chain, the carries through the chain's cuts in (cs, ra].
+    float P[VEC];
 #pragma unroll
-            for (int r = 0; r < kBatch; ++r) {
-                const int s = s0 + r * groups;
-                keyv[r] = s < n_segs ? chain_key[seg_chain[s]] : -1;
-                c0v[r] = load_vec<VEC>(c_init + ((int64_t)b * K + (keyv[r] >= 0 ? keyv[r] : 0)) * N + n0,
-                                       keyv[r] >= 0 && active, n0, N);
-            }
+    for (int v = 0; v < VEC; ++v) P[v] = c0v[0].v[v];
+    int tp = 0;
+    int key = keyv[0];
+    bool has_prev = key >= 0;
+    int64_t dprev = doc0;
+    if (ra < re) {
+        const int cs = chain_start[elem_chain[ra]];
+        for (int m = (cs >> lgS) + 1; m <= g; ++m) {
+            const int tl = pos_of((m << lgS) - 1);
+            const bool drop = DOCS && aggr[m];
+            float pw[VEC];
+            powv(tl - tp, pw);
 #pragma unroll
-            for (int r = 0; r < kBatch; ++r) {
-                const int s = s0 + r * groups;
-                if (s >= n_segs) break;
-                const int cc = seg_chain[s];
-                const int key = keyv[r];
-                const int cs = chain_start[cc];
-                const int ce = chain_start[cc + 1];
-                const int f0 = chain_seg[cc] - cc;  // non-final index of the chain's first segment
-                const int qi = s - chain_seg[cc];
-                const int beg = cs + qi * S;
-                const int end = min(beg + S, ce);
-                // post-increment state P at time tp entering the chain: c0 at t = 0
-                float P[VEC];
+            for (int v = 0; v < VEC; ++v)
+                P[v] = (drop ? 0.f : P[v] * pw[v]) + agg[(m << lgRow) + lane_r + v] + 1.0f;
+            tp = tl;
+        }
+        if (DOCS && ra > cs) {
+            dprev = doc_of(tp);
+            has_prev = true;
+        }
+        startm &= ~1u;
+    }
+    for (int c = ra; c < re; c += CH) {
+        if (c != ra) gather(c);
 #pragma unroll
-                for (int v = 0; v < VEC; ++v) P[v] = c0v[r].v[v];
-                int tp = 0;
-                bool has_prev = key >= 0;
-                int64_t dprev = 0;
-                if (DOCS && has_prev) dprev = doc_of(0);
-                for (int k = 0; k < qi; ++k) {  // carry through the chain's earlier segments
-                    const int tl = pos_of(cs + (k + 1) * S - 1);
-                    const bool drop = DOCS && aggr[f0 + k];
-                    float pw[VEC];
-                    powv(tl - tp, pw);
+        for (int e = 0; e < CH; ++e) settle(c0v[e].v);
+        if (DOCS) settle(docv);
+        int tn = pos_of(c);
 #pragma unroll
-                    for (int v = 0; v < VEC; ++v)
-                        P[v] = (drop ? 0.f : P[v] * pw[v]) + agg[(f0 + k) * slice_w + lane_r + v] + 1.0f;
-                    tp = tl;
+        for (int e = 0; e < CH; ++e) {
+            const int j = c + e;
+            if (j < re) {
+                const int t = tn;
+                tn = pos_of(min(j + 1, re - 1));  // next position, read one step ahead
+                if ((startm >> e) & 1) {
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) P[v] = c0v[e].v[v];
+                    tp = 0;
+                    key = keyv[e];
+                    has_prev = key >= 0;
+                    dprev = doc0;
                 }
-                if (DOCS && qi > 0) {
-                    dprev = doc_of(tp);
+                float cv[VEC];
+                powv(t - tp, cv);
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) cv[v] *= P[v];
+                if (DOCS) {
+                    const int64_t dcur = docv[e];
+                    if (has_prev && dcur != dprev) {
+#pragma unroll
+                        for (int v = 0; v < VEC; ++v) cv[v] = 0.f;
+                    }
+                    dprev = dcur;
                     has_prev = true;
                 }
-                int t = tp;
-                for (int j = beg; j < end; ++j) {
-                    t = pos_of(j);
-                    float cv[VEC];
-                    powv(t - tp, cv);
+                if (active && t < L) store_vec<VEC>(Cb + row(t), cv, n0, N);
 #pragma unroll
-                    for (int v = 0; v < VEC; ++v) cv[v] *= P[v];
-                    if (DOCS) {
-                        const int64_t dcur = doc_of(t);
-                        if (has_prev && dcur != dprev) {
-#pragma unroll
-                            for (int v = 0; v < VEC; ++v) cv[v] = 0.f;
-                        }
-                        dprev = dcur;
-                        has_prev = true;
-                    }
-                    if (active && t < L) store_vec<VEC>(Cb + t * N, cv, n0, N);
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) P[v] = cv[v] + 1.0f;
-                    tp = t;
-                }
-                if (end == ce && key >= 0) {
-                    if (state_out && active)
-                        store_vec<VEC>(state_out + ((int64_t)b * K + key) * N + n0, P, n0, N);
+                for (int v = 0; v < VEC; ++v) P[v] = cv[v] + 1.0f;
+                tp = t;
+                if (((lastm >> e) & 1) && key >= 0) {
+                    if (stb && active) store_vec<VEC>(stb + row(key), P, n0, N);
                     if (stamp_out && slice == 0 && lane_r == 0) stamp_out[(int64_t)b * K + key] = t;
                 }
             }
@@ -549,6 +613,9 @@ extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x
     if (L > kMaxScanL)
         return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d exceeds the on-chip limit %d", L,
                     kMaxScanL);
+    if ((int64_t)L * N >= (1ll << 31) || (int64_t)K * N >= (1ll << 31) || K >= (1 << 24))
+        return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d, K=%d, N=%d: rows of one sequence must "
+                    "stay below 2^31 elements (and K below 2^24)", L, K, N);
     const int pb = ceil_log2(L);
     const bool wide = vocab_size > 0 && (pb >= 32 || (uint64_t)vocab_size > (1ull << (32 - pb)));
     // token bits the radix sort orders by: those of vocab_size - 1 (ids are < vocab_size)
@@ -562,12 +629,14 @@ extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x
     int slice_w = N >= 32 ? 32 : N;
     if (vec4) slice_w = (slice_w + 3) & ~3;
     const int ns = (N + slice_w - 1) / slice_w;
-    // segment length: at most kMaxNonFinal non-final segments per sequence
-    constexpr int kMaxNonFinal = 128;
-    const int S = std::max(16, (L + kMaxNonFinal - 1) / kMaxNonFinal);
-    const int nf_max = L / S;
+    // segment length S: a power of two >= 16 that gives each lane group of pass B at most
+    // one sorted range of S elements
+    const int groups = kScanThreads / (slice_w / (vec4 ? 4 : 1));
+    int lgS = 4;
+    while (((L - 1) >> lgS) + 1 > groups) ++lgS;
+    const int ncut = (L - 1) >> lgS;
     const int nH = (L - 1) / 64 + 1;
-    const ScanLds lay(L, wide ? 8 : 4, kScanThreads, nf_max, slice_w, nH);
+    const ScanLds lay(L, 1 << pb, wide ? 8 : 4, kScanThreads, ncut, nH, ceil_log2(slice_w));
     if (lay.total > kMaxLds)
         return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d with vocab %lld needs %zu B of LDS",
                     L, (long long)vocab_size, lay.total);
@@ -582,7 +651,7 @@ extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x
         if (rc) return rc;                                                                     \
         hipLaunchKernelGGL(kfn, grid, dim3(kScanThreads), lay.total, st, x, x_stride_b,        \
                            x_stride_l, L, rhos, N, c_init, c_init_keys, K, doc_ids, C_seq,     \
-                           state_out, stamp_out, pb, tok_bits, slice_w, S, nf_max);            \
+                           state_out, stamp_out, pb, tok_bits, slice_w, lgS, ncut);           \
     } while (0)
 #define MB_LAUNCH_SCAN_D(KT, V)                                     \
     do {                                                            \
