@@ -57,7 +57,7 @@ TRAFFIC_BYTES = {
     "cfg2": 13261.7e6,
     "cfg4": 45724.7e6,
     "corpus": 19654.0e6,   # the three mb_corpus_states launches (profiles/corpus_states_64M_tokens.md)
-    "scan": 109.2e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
+    "scan": 110.3e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
     "gating": 387.3e6,     # gating_fwd_kernel + gating_bwd_kernel (profiles/gating_cfg2_rows.md)
 }
 
