@@ -402,6 +402,9 @@ def run_model(args):
     d = make_doc_batch(B, T, V, N, min_hl=1.0, max_hl=2048.0, seed=0)
     torch.manual_seed(1)
     model = SlotTransformerLM(V, D, n_layers, H, N=N, dropout=0.1, attn_precision=args.precision).to(dev)
+    if args.fold_query_gating:  # queries inside the attention kernel (off by default)
+        for layer in model.layers:
+            layer.attn.fold_query_gating = True
     opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
     x, uniq, cb, tgt = (d[k].to(dev) for k in ("x", "unique", "c_base", "targets"))
     pm = uniq >= 0
@@ -440,6 +443,8 @@ def run_model(args):
                        "K_max": int(uniq.shape[1]), "unpadded_tokens": real,
                        "steps_per_s": round(1e3 / ms, 3),
                        "unpadded_tokens_per_s": round(real / (ms * 1e-3), 1),
+                       "query_gating": "inside the attention kernel" if args.fold_query_gating
+                                       else "separate kernel + q_proj GEMM",
                        "loss": round(float(loss), 4)}}
 
 
@@ -734,6 +739,9 @@ def main():
     ap.add_argument("--precision", choices=("bf16", "fp32"), default="bf16",
                     help="attention gate operands: fp16 (bf16 mode, the default) or fp16 hi + lo "
                          "pairs (fp32 mode); attention, cfg4 and model workloads")
+    ap.add_argument("--fold-query-gating", action="store_true",
+                    help="model workload: compute the queries inside the attention kernel "
+                         "(SlotAttentionLayer.fold_query_gating; off by default)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "

@@ -154,7 +154,8 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
  * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to
  * ~45,000 steps) and W_pe * log2(e), with fp32 accumulation.
  *
- * Supported: hd in {32, 64}, 4 <= H <= 8, N <= 128, Br <= 32 or Br == 64.
+ * Supported: hd in {32, 64}, 1 <= H <= 64, N <= 128 (N <= 64 with MB_FLASH_FP32), Br <= 32
+ * or Br == 64.
  */
 int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,
                      const int64_t *x, int64_t x_sb, int64_t x_sl, const float *E_k,
@@ -181,7 +182,7 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
  * order is not fixed, as in the reference's tl.atomic_add.  The gate is recomputed as
  * in the forward; the dW_pe product takes bf16 c_dec and bf16 dpre (as the reference's
  * triton_flash_ema.py:463-465 does) with fp32 accumulation.  Supported: as
- * mb_flash_ema_fwd with H a multiple of 4.
+ * mb_flash_ema_fwd.
  */
 int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,
                      const float *dO, const int64_t *x, int64_t x_sb, int64_t x_sl,
@@ -190,6 +191,38 @@ int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
                      const float *LSE, int B, int H, int L, int hd, int K, int N, int Np, int nc,
                      int Br, int64_t V_total, int flags, const float *scores, float *dQ,
                      float *dE_k, float *dE_v, float *dW_pe, void *stream);
+
+/*
+ * Flash-EMA attention forward with the query gating folded into its prologue.  Replaces
+ * fused_apply_symmetric_query_gating followed by q_proj and flash_ema_forward
+ * (mathbrain/triton_fused_gating.py:179-197, model.py:75-87): each workgroup computes its
+ * own queries
+ *
+ *   Q[b,t,:] = q_proj(LayerNorm_eps(x_q[b,t] * SiLU((C_seq[b,t] + 1) . W_pe)) * ln_w + ln_b)
+ *
+ * (the LayerNorm output bit for bit as mb_gating_fwd computes it; q_proj on the matrix
+ * cores from fp16 hi + lo operand pairs, ~2^-22 relative per product), viewed as
+ * [B, H, L, hd] (column h*hd + d of Q is head h, dim d), and then runs the attention of
+ * mb_flash_ema_fwd on it.  Q is never written.  Arguments as mb_flash_ema_fwd without
+ * Q and scores, plus
+ *
+ *   x_q       [B, L, D] fp32 (D = H*hd), element strides xq_sb, xq_sl, columns contiguous
+ *   C_seq     [B, L, N] fp32, element strides c_sb, c_sl, columns contiguous
+ *   ln_w, ln_b [D] fp32 (ln_q), eps > 0
+ *   W_q       [D, D] fp32 contiguous (q_proj.weight: row = output column of Q)
+ *
+ * W_pe serves both the query gate and the key gate, as in the reference.  The backward is
+ * mb_flash_ema_bwd on Q recomputed from x_ln (the q_proj and gating gradients need x_ln, so
+ * the caller recomputes it with mb_gating_fwd).  Supported: as mb_flash_ema_fwd with D a
+ * multiple of 32 and at most 1024.
+ */
+int mb_flash_ema_fwd_gq(const float *x_q, int64_t xq_sb, int64_t xq_sl, const float *C_seq,
+                        int64_t c_sb, int64_t c_sl, const float *ln_w, const float *ln_b, float eps,
+                        const float *W_q, const int64_t *x, int64_t x_sb, int64_t x_sl,
+                        const float *E_k, const float *E_v, const float *W_pe, const float *rhos,
+                        const int64_t *unique, const float *C_bounds, int B, int H, int L, int hd,
+                        int K, int N, int Np, int nc, int Br, int64_t V_total, int flags, float *O,
+                        float *LSE, void *stream);
 
 /*
  * Fused symmetric query gating, forward.  Replaces _fused_gating_fwd and the forward of

@@ -1,0 +1,352 @@
+// Flash-EMA gated cross-attention forward kernel on gfx950 (template, its LDS size and its
+// launcher), shared by the entry points of flash_fwd.hip and flash_gq_fwd.hip.
+//
+// Replaces _flash_ema_fwd and flash_ema_forward (mathbrain/triton_flash_ema.py:121-241,
+// :529-568).  Semantics, per sequence b, head h, step t and valid slot k:
+//   g[t,k,:] = SiLU(c_dec[t,k,:] . W_pe[:, h])         (fp16 operands, fp32 accumulate)
+//   s[t,k]   = q_t . (e_k[k] * g[t,k]) / sqrt(hd)
+//   O_t      = sum_k softmax_k(s) e_v[k] * g[t,k],   LSE_t = log sum_k exp(s)
+// where, when v_total >= 0, the softmax also holds the V - K_b absent slots of the
+// dense reference (mathbrain/flash_ema_attention.py:76-77): their counters are zero,
+// so their gate SiLU(0) = 0 gives score 0 and value 0, i.e. they add (V - K_b) e^0 to
+// the denominator and nothing to the numerator.
+//
+// Layout: one workgroup per (b, 32-step block) with one wave per head.  The gate GEMM
+// is computed transposed, pre^T[d, t] = W^T[d, :] c_dec^T[:, t], with
+// v_mfma_f32_16x16x32_f16, so each lane owns one step t (lane % 16 of a 16-step tile)
+// and 16 of the head's 64 dims (rows 16*dt + 4*(lane/16) + i): the score's sum over d
+// stays in registers (plus two cross-lane adds), and O_t's sum over slots accumulates
+// in registers across the slot loop.  The online softmax runs in the log2 domain
+// (W is pre-scaled by log2 e) and rescales only when a score beats the running max by
+// more than 2^8, which keeps every exponential <= 256.
+#pragma once
+#include "flash_gq.h"
+
+#include <algorithm>
+
+namespace mb {
+
+constexpr float kTau = 8.0f;
+
+// VR: E_k / E_v are vocabulary tables indexed by the slot's token id (MB_FLASH_VOCAB_ROWS).
+// PREC (MB_FLASH_FP32): the gate GEMM carries both operands as fp16 hi + lo pairs,
+//   pre = W_lo c_hi + W_hi c_lo + W_hi c_hi  (three MFMAs, fp32 accumulation),
+// which leaves ~2^-22 relative error per product instead of fp16's 2^-11; W_lo waits in
+// LDS (W_hi stays in registers) and the producer writes a c_lo tile beside c_hi.
+// GQ: the workgroup computes its queries from the gating inputs (flash_gq.h) instead of
+// reading Q.
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR, bool PREC = false, bool GQ = false>
+__global__ void __launch_bounds__(512, 1)
+flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
+    constexpr int NPAD = 32 * NS;
+    constexpr int DT = HD / 16;
+    using S = Stage<NPAD, SB, false, PREC>;
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int D = a.H * HD;
+    const int ntb = (a.L + kTB - 1) / kTB;
+    const int logical = xcd_major(blockIdx.x, gridDim.x);
+    // one workgroup per (b, 32-step block, head group); a group holds hpg heads (hpg
+    // divides H), one wave each, and waves past hpg only help stage and synchronise
+    const int hg = logical % a.head_groups;
+    const int b = logical / (a.head_groups * ntb);
+    const int t0 = ((logical / a.head_groups) % ntb) * kTB;
+    const int cbi = t0 / a.Br;
+    const int cb = cbi * a.Br;
+    const int hpg = a.H / a.head_groups;
+    const int WIDF = hpg * HD;     // embedding columns staged: this group's heads
+    const int col0 = hg * WIDF;
+
+    // LDS: two staging buffers, a 3-deep ring of batch slot info (batch i+2's info is
+    // written while batch i is still being read), the window, the power table.
+    const int stage_bytes = (int)S::bytes(WIDF);
+    BatchMeta* metas = reinterpret_cast<BatchMeta*>(smem + 2 * stage_bytes);
+    int64_t* win = reinterpret_cast<int64_t*>(metas + 3 * SB);
+    float* powt = reinterpret_cast<float*>(win + kMaxWin);
+    int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
+    f16x8* wlo = reinterpret_cast<f16x8*>(kinfo + 4);  // PREC: [head][dt][ns][lane]
+#define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
+#define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
+#define meta_of(batch) (metas + ((batch) % 3) * SB)
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int c16 = lane & 15;
+    const int g = lane >> 4;
+    const bool active = wave < hpg;
+    const int h = active ? hg * hpg + wave : 0;  // idle waves read head 0 and write nothing
+
+    // Queries of this lane's steps (lane c16 of step tile tt, dims 16 dt + 4 g + i).
+    f32x4 qs[2][DT];
+    if constexpr (GQ) {
+        // the prologue uses the start of LDS before anything else is staged there
+        float* xl = reinterpret_cast<float*>(smem);
+        gq_layer_norm<SILU>(a, b, t0, D, xl);
+        if (active) gq_project_fwd<HD>(a, h, D, xl, lane, qs);
+        __syncthreads();
+    }
+
+    flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
+    const int kvalid = kinfo[0];
+    const int kend = kinfo[1];
+    const int nb = (kend + SB - 1) / SB;
+    const int x32 = (lane ^ 32) << 2;  // ds_bpermute byte address of lane l ^ 32
+
+    // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
+    // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
+    f16x8 wf[DT][NS];
+    {
+        float wraw[DT][NS][8];
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ns = 0; ns < NS; ++ns)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int n = min(32 * ns + 8 * g + e, a.N - 1);
+                    wraw[dt][ns][e] = a.W[(int64_t)n * D + h * HD + 16 * dt + c16];
+                }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ns = 0; ns < NS; ++ns) {
+                f16x8 lo;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int n = 32 * ns + 8 * g + e;
+                    float ws = n < a.N ? wraw[dt][ns][e] * kLog2e : 0.f;
+                    if (PREC) asm volatile("" : "+v"(ws));  // hi and lo of one float32 product
+                    wf[dt][ns][e] = (_Float16)ws;
+                    lo[e] = (_Float16)(ws - (float)wf[dt][ns][e]);
+                }
+                // this wave's head's W_lo fragments, read back in the slot loop
+                if (PREC) wlo[((wave * DT + dt) * NS + ns) * 64 + lane] = lo;
+            }
+    }
+
+    // Queries pre-scaled by 1/sqrt(hd).
+    const float qscale = 1.0f / sqrtf((float)HD);
+    f32x4 o[2][DT];
+    float m[2], l[2];
+    const float absent = a.v_total >= 0.f ? fmaxf(a.v_total - (float)kvalid, 0.f) : 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int t = t0 + 16 * tt + c16;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 16 * dt + 4 * g + i;
+                if constexpr (GQ) {
+                    qs[tt][dt][i] = t < a.L ? qs[tt][dt][i] * qscale : 0.f;
+                } else {
+                    const float* qrow = a.Q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)t * a.q_sl;
+                    qs[tt][dt][i] = t < a.L ? qrow[(int64_t)d * a.q_sd] * qscale : 0.f;
+                }
+                o[tt][dt][i] = 0.f;
+            }
+        }
+        m[tt] = a.v_total >= 0.f ? 0.f : -INFINITY;
+        l[tt] = absent;
+    }
+
+    Producer<NPAD, SB, MAXI, MAXE> prod;
+    if (nb > 0) {
+        flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
+        if (VR) __syncthreads();  // the load reads the batch's token ids
+        prod.template load<VR>(a, b, cbi, 0, kend, D, col0, WIDF, meta_of(0));
+        __syncthreads();
+        prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), WIDF);
+        if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
+        __syncthreads();
+    }
+
+    for (int bi = 0; bi < nb; ++bi) {
+        const int cur = bi & 1;
+        if (bi + 1 < nb) prod.template load<VR>(a, b, cbi, bi + 1, kend, D, col0, WIDF, meta_of(bi + 1));
+        const _Float16* cdec = cdec_of(cur);
+        const float* E = E_of(cur);
+        const BatchMeta* meta = meta_of(bi);
+        for (int j = 0; j < SB; ++j) {
+            // padding slot (uniform across the workgroup), or a wave without a head
+            if (meta[j].u < 0 || !active) continue;
+            f16x8 cf[2][NS];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns)
+                    cf[tt][ns] = *reinterpret_cast<const f16x8*>(
+                        cdec + (j * kTB + 16 * tt + c16) * S::CROW + 32 * ns + 8 * g);
+            f32x4 ek[DT], ev[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                ek[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 0) * WIDF + wave * HD + 16 * dt + 4 * g);
+                ev[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 1) * WIDF + wave * HD + 16 * dt + 4 * g);
+            }
+            f32x4 gt[2][DT];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                f16x8 cl[NS];
+                if (PREC) {
+#pragma unroll
+                    for (int ns = 0; ns < NS; ++ns)
+                        cl[ns] = *reinterpret_cast<const f16x8*>(
+                            cdec + S::CDEC + (j * kTB + 16 * tt + c16) * S::CROW + 32 * ns + 8 * g);
+                }
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    if (PREC) {  // small terms first
+#pragma unroll
+                        for (int ns = 0; ns < NS; ++ns)
+                            acc = mfma16x16x32(wlo[((wave * DT + dt) * NS + ns) * 64 + lane], cf[tt][ns], acc);
+#pragma unroll
+                        for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cl[ns], acc);
+                    }
+#pragma unroll
+                    for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cf[tt][ns], acc);
+                    gt[tt][dt] = acc;
+                }
+            }
+            float s[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                float sacc = 0.f;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float x = gt[tt][dt][i];
+                        float gv = x;
+                        if (SILU) {
+                            const float ex = __builtin_amdgcn_exp2f(-x);
+                            gv = x * __builtin_amdgcn_rcpf(1.0f + ex);
+                        }
+                        gt[tt][dt][i] = gv;
+                        sacc = __builtin_fmaf(qs[tt][dt][i], ek[dt][i] * gv, sacc);
+                    }
+                // lanes l ^ 16 (ds_swizzle, bitmask mode: and 0x1f, xor 0x10) and l ^ 32
+                // (ds_bpermute with a byte address computed once)
+                sacc += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(sacc), 0x401F));
+                sacc += __int_as_float(__builtin_amdgcn_ds_bpermute(x32, __float_as_int(sacc)));
+                s[tt] = sacc;
+            }
+            // One (rare) rescale branch for both step tiles, so that the softmax and P.V of
+            // the two tiles form one block the scheduler can interleave.
+            const bool need0 = s[0] > m[0] + kTau;
+            const bool need1 = s[1] > m[1] + kTau;
+            if (__any(need0 || need1)) {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const float mn = (tt ? need1 : need0) ? s[tt] : m[tt];
+                    const float alpha = __builtin_amdgcn_exp2f(m[tt] - mn);
+                    l[tt] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[tt][dt] *= alpha;
+                    m[tt] = mn;
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const float p = __builtin_amdgcn_exp2f(s[tt] - m[tt]);
+                l[tt] += p;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[tt][dt][i] = __builtin_fmaf(p, ev[dt][i] * gt[tt][dt][i], o[tt][dt][i]);
+            }
+            if (a.S2out && g == 0) {
+                float* srow = a.S2out + (((int64_t)b * a.H + h) * a.K + bi * SB + j) * a.L;
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int t = t0 + 16 * tt + c16;
+                    if (t < a.L) srow[t] = s[tt];
+                }
+            }
+        }
+        if (bi + 1 < nb) {
+            prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+                                              E_of(cur ^ 1), WIDF);
+            if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
+        }
+        __syncthreads();
+    }
+
+    // O = ln2 * o / l  (the gate carried a factor log2 e), LSE = ln2 * (m + log2 l).
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int t = t0 + 16 * tt + c16;
+        if (t >= a.L || !active) continue;
+        const bool any = l[tt] > 0.f;
+        const float inv = any ? kLn2 / l[tt] : 0.f;
+        float* orow = a.O + (((int64_t)b * a.H + h) * a.L + t) * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const f32x4 v = o[tt][dt] * inv;
+            *reinterpret_cast<f32x4*>(orow + 16 * dt + 4 * g) = v;
+        }
+        if (g == 0)
+            a.LSE[((int64_t)b * a.H + h) * a.L + t] = any ? (m[tt] + __log2f(l[tt])) * kLn2 : -INFINITY;
+    }
+#undef cdec_of
+#undef E_of
+#undef meta_of
+}
+
+template <int HD, int NS, int SB, bool PREC>
+static size_t fwd_lds_bytes(int width, int nwaves) {
+    return 2 * Stage<32 * NS, SB, false, PREC>::bytes(width) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
+           65 * 32 * NS * 4 + 16 + (PREC ? (size_t)nwaves * (HD / 16) * NS * 64 * 16 : 0);
+}
+
+// Heads per workgroup: all of them up to 8 (one wave each), else the largest divisor of
+// H that is at most 8, so that every group is whole.
+static int fwd_heads_per_group(int H) {
+    if (H <= 8) return H;
+    for (int d = 8; d > 1; --d)
+        if (H % d == 0) return d;
+    return 1;
+}
+
+template <int HD, int NS, int SB, bool PREC = false, bool GQ = false, class A = FlashArgsV>
+static int launch_fwd(const A& a0, bool vr, hipStream_t st) {
+    A a = a0;
+    const int hpg = fwd_heads_per_group(a.H);
+    a.head_groups = a.H / hpg;
+    const int width = hpg * HD;
+    // at least four waves, so that the producer's share per thread stays bounded
+    const int nthr = 64 * (hpg < 4 ? 4 : hpg);
+    constexpr int NPAD = 32 * NS;
+    const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
+    const int nvec = SB * 2 * (width / 4);
+    size_t lds = fwd_lds_bytes<HD, NS, SB, PREC>(width, nthr / 64);
+    if (GQ) lds = std::max(lds, gq_fwd_lds_bytes(a.H * HD, a.N));
+    if (lds > 160 * 1024)
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: %d heads of %d, N=%d need %zu B of LDS", hpg, HD, a.N, lds);
+    const int ntb = (a.L + kTB - 1) / kTB;
+    dim3 grid(a.B * ntb * a.head_groups);
+    // the kernels without VR take the base argument block, the GQ ones always FlashArgsG
+    const typename FlashArgsK<false, GQ>::type& base = a;
+#define MB_FWD(MI, ME)                                                                           \
+    do {                                                                                         \
+        const int rc_ = vr ? launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true, PREC, GQ>    \
+                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true, PREC, GQ>,  \
+                                             grid, nthr, lds, st, a, "mb_flash_ema_fwd")                      \
+                           : launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false, PREC, GQ>   \
+                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false, PREC, GQ>, \
+                                             grid, nthr, lds, st, base, "mb_flash_ema_fwd");                  \
+        if (rc_) return rc_;                                                                     \
+    } while (0)
+    const int me = (nvec + nthr - 1) / nthr;
+    if (mi > 4 || me > 4)
+        return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: width %d, N=%d too wide for %d threads", width, a.N, nthr);
+    if (mi <= 1 && me <= 1) MB_FWD(1, 1);
+    else if (mi <= 1 && me <= 2) MB_FWD(1, 2);
+    else if (mi <= 2 && me <= 2) MB_FWD(2, 2);
+    else MB_FWD(4, 4);
+#undef MB_FWD
+    return check_launch("mb_flash_ema_fwd");
+}
+
+}  // namespace mb

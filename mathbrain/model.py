@@ -17,7 +17,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .triton_ema_query import compute_query_ema_history
-from .triton_flash_ema import FlashEMAFunction, _build_unique_index, precompute_boundaries
+from .triton_flash_ema import (FlashEMAFunction, GatedQueryFlashEMAFunction, _build_unique_index,
+                               precompute_boundaries)
 from .triton_fused_gating import fused_apply_symmetric_query_gating
 from .layernorm import layer_norm
 from .rmsnorm import rms_norm
@@ -77,6 +78,18 @@ class SlotAttentionLayer(nn.Module):
         self.absent_mass = absent_mass
         # the attention's gate operands: fp16 ("bf16" mode) or fp16 hi + lo pairs ("fp32")
         self.precision = precision
+        # True: compute the queries (gating, ln_q, q_proj) inside the attention kernel
+        # (GatedQueryFlashEMAFunction) when the shapes allow it.  Off by default: measured at
+        # configuration 5 it costs more than it saves -- every 32-step workgroup streams all of
+        # q_proj.weight, a training step's backward needs Q and the LayerNorm output anyway, and
+        # even a forward without autograd took 35.7 ms against 35.3 ms with the separate gating
+        # kernel and q_proj GEMM
+        self.fold_query_gating = False
+
+    def _folds_query_gating(self, D):
+        return (bool(self.fold_query_gating) and self.pe_proj.bias is None and self.q_proj.bias is None
+                and self.ln_q.weight is not None and self.ln_q.bias is not None and D % 32 == 0
+                and D <= 1024)
 
     def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None,
                 E_active=None):
@@ -98,17 +111,24 @@ class SlotAttentionLayer(nn.Module):
         memory_base = layer_norm(E_active, self.ln_kv.weight, self.ln_kv.bias, self.ln_kv.eps)
         E_k_active = self.k_proj(memory_base)
         E_v_active = self.v_proj(memory_base)
-        # 2. query gating (model.py:75)
-        Q_t = fused_apply_symmetric_query_gating(x_q, C_seq, self.pe_proj, self.ln_q, self.q_proj,
-                                                 self.use_silu)
-        # 3. gated cross-attention (model.py:79-87)
         H = self.n_heads
         hd = D // H
-        Q_mha = Q_t.view(B, L, H, hd).transpose(1, 2)
         W_pe_t = self.pe_proj.weight.t()
-        out_mha = FlashEMAFunction.apply(Q_mha, x, E_k_active, E_v_active, W_pe_t, rhos,
-                                         E_slots.shape[0], unique_tensor, K_max, C_bounds, self.use_silu,
-                                         64, self.absent_mass, self.precision)
+        if self._folds_query_gating(D):
+            # 2 + 3. query gating, ln_q and q_proj inside the attention kernels
+            out_mha = GatedQueryFlashEMAFunction.apply(
+                x_q, C_seq, W_pe_t, self.ln_q.weight, self.ln_q.bias, self.q_proj.weight, x, E_k_active,
+                E_v_active, rhos, E_slots.shape[0], unique_tensor, K_max, C_bounds, H, self.use_silu, 64,
+                self.absent_mass, self.precision, self.ln_q.eps)
+        else:
+            # 2. query gating (model.py:75)
+            Q_t = fused_apply_symmetric_query_gating(x_q, C_seq, self.pe_proj, self.ln_q, self.q_proj,
+                                                     self.use_silu)
+            # 3. gated cross-attention (model.py:79-87)
+            Q_mha = Q_t.view(B, L, H, hd).transpose(1, 2)
+            out_mha = FlashEMAFunction.apply(Q_mha, x, E_k_active, E_v_active, W_pe_t, rhos,
+                                             E_slots.shape[0], unique_tensor, K_max, C_bounds, self.use_silu,
+                                             64, self.absent_mass, self.precision)
         out = out_mha.transpose(1, 2).reshape(B, L, D)
         out = self.o_proj(out)
         return self.resid_dropout(out)

@@ -361,3 +361,144 @@ class FlashEMAFunction(torch.autograd.Function):
         if ctx.W_rows > dW.shape[0]:  # W_pe passed with padded rows: their gradient is 0
             dW = torch.cat([dW, dW.new_zeros(ctx.W_rows - dW.shape[0], dW.shape[1])])
         return dQ, None, dEk, dEv, dW, None, None, None, None, None, None, None, None, None
+
+
+# ---- the query gating folded into the attention ------------------------------------------
+
+def _gq_prepare(x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, B, K, N, D, what):
+    Ek, table = _slot_rows(E_k, B, K, D, int(V_total), what)
+    Ev, table_v = _slot_rows(E_v, B, K, D, int(V_total), what)
+    if table != table_v:
+        raise ValueError(f"{what}: E_k and E_v must both be tables or both gathered rows")
+    W = W_pe.to(torch.float32)
+    if W.shape[0] < N or W.shape[1] != D:
+        raise ValueError(f"{what}: W_pe must be [N, H*hd] = {(N, D)}, got {tuple(W.shape)}")
+    W = W[:N].contiguous()
+    rh = rhos.detach().to(torch.float32).contiguous()
+    uniq = unique_tensor.to(torch.int64).contiguous()
+    xl = x if x.dtype == torch.int64 else x.long()
+    Cb = C_bounds.to(torch.float32).contiguous()
+    if Cb.dim() != 4 or Cb.shape[0] != B or Cb.shape[2] != K or Cb.shape[3] < N:
+        raise ValueError(f"{what}: C_bounds must be [B, nc, K_max, >=N], got {tuple(Cb.shape)}")
+    return Ek, Ev, table, W, rh, uniq, xl, Cb
+
+
+def _rows_f32(t, width):
+    """fp32 view with contiguous columns and whole-row strides (copied if needed)."""
+    t = t.to(torch.float32)
+    if t.stride(-1) != 1 or t.stride(-2) < width:
+        t = t.contiguous()
+    return t
+
+
+def _fwd_gq_fake(x_q, C_seq, W_pe, ln_w, ln_b, W_q, eps, x, E_k, E_v, rhos, unique_tensor, C_bounds,
+                 V_total, n_heads, use_silu, Br, absent_mass, fp32):
+    B, L, D = x_q.shape
+    hd = D // n_heads
+    return (x_q.new_empty((B, n_heads, L, hd), dtype=torch.float32),
+            x_q.new_empty((B, n_heads, L), dtype=torch.float32))
+
+
+@_lib.traced_op("flash_ema_fwd_gq", _fwd_gq_fake)
+def flash_ema_fwd_gq(x_q: torch.Tensor, C_seq: torch.Tensor, W_pe: torch.Tensor, ln_w: torch.Tensor,
+                     ln_b: torch.Tensor, W_q: torch.Tensor, eps: float, x: torch.Tensor, E_k: torch.Tensor,
+                     E_v: torch.Tensor, rhos: torch.Tensor, unique_tensor: torch.Tensor,
+                     C_bounds: torch.Tensor, V_total: int, n_heads: int, use_silu: bool, Br: int,
+                     absent_mass: bool, fp32: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """(O, LSE) of the attention on Q = q_proj(LayerNorm(x_q * gate((C_seq + 1) @ W_pe))), the
+    queries computed inside the attention kernel (one mb_flash_ema_fwd_gq launch)."""
+    dev = _lib.require_gpu(x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k, E_v, rhos, unique_tensor,
+                           C_bounds, what="flash_ema_forward (gated queries)")
+    B, L, D = x_q.shape
+    H = int(n_heads)
+    if D % H:
+        raise ValueError(f"d_model {D} is not a multiple of n_heads {H}")
+    hd = D // H
+    K = unique_tensor.shape[1]
+    N = rhos.shape[0]
+    if C_seq.shape[:2] != (B, L) or C_seq.shape[2] != N:
+        raise ValueError(f"C_seq must be [B, L, N] = {(B, L, N)}, got {tuple(C_seq.shape)}")
+    if tuple(W_q.shape) != (D, D):
+        raise ValueError(f"W_q (q_proj.weight) must be [D, D] = {(D, D)}, got {tuple(W_q.shape)}")
+    Ek, Ev, table, W, rh, uniq, xl, Cb = _gq_prepare(x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds,
+                                                      V_total, B, K, N, D, "flash_ema_forward")
+    xq = _rows_f32(x_q, D)
+    C = _rows_f32(C_seq, N)
+    lw = ln_w.to(torch.float32).contiguous()
+    lb = ln_b.to(torch.float32).contiguous()
+    Wq = W_q.to(torch.float32).contiguous()
+    O = torch.empty(B, H, L, hd, dtype=torch.float32, device=dev)
+    LSE = torch.empty(B, H, L, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("mb_flash_ema_fwd_gq", _lib.ptr(xq), xq.stride(0), xq.stride(1), _lib.ptr(C), C.stride(0),
+                  C.stride(1), _lib.ptr(lw), _lib.ptr(lb), float(eps), _lib.ptr(Wq), _lib.ptr(xl),
+                  xl.stride(0), xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W), _lib.ptr(rh),
+                  _lib.ptr(uniq), _lib.ptr(Cb), B, H, L, hd, K, N, Cb.shape[3], Cb.shape[1], int(Br),
+                  int(V_total), _flash_flags(use_silu, absent_mass, table, fp32), _lib.ptr(O), _lib.ptr(LSE),
+                  _lib.stream(dev))
+    return O, LSE
+
+
+class GatedQueryFlashEMAFunction(torch.autograd.Function):
+    """The query side and the attention of SlotAttentionLayer (model.py:75-87) in one launch:
+    apply(x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k_active, E_v_active, rhos, V_total,
+    unique_tensor, K_max, C_bounds, n_heads, use_silu=True, Br=64, absent_mass=True,
+    precision="bf16", eps=1e-5) -> O [B, H, L, hd], equal to
+
+        Q = q_proj(LayerNorm_eps(x_q * SiLU((C_seq + 1) @ W_pe)))      (fused_apply_symmetric_query_gating)
+        FlashEMAFunction.apply(Q.view(B, L, H, hd).transpose(1, 2), x, E_k_active, E_v_active, W_pe, ...)
+
+    with W_pe = pe_proj.weight.t() [N, D] (shared by the query gate and the key gate, as in
+    the reference), ln_w / ln_b = ln_q's parameters, W_q = q_proj.weight [D, D].  The forward
+    kernel computes Q itself: the gating kernel, the q_proj GEMM and Q's trip through HBM are
+    gone.  The backward recomputes the LayerNorm output x_ln (which the q_proj and gating
+    gradients need) and Q from it, runs the attention backward, and dQ then gives
+    dW_q = dQ^T x_ln, dx_ln = dQ W_q and the gating gradients.  Gradients flow to x_q, W_pe,
+    ln_w, ln_b, W_q, E_k_active and E_v_active (and C_seq if it requires one).  Supported:
+    d_model a multiple of 32, at most 1024."""
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float32)
+    def forward(ctx, x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k_active, E_v_active, rhos, V_total,
+                unique_tensor, K_max, C_bounds, n_heads, use_silu=True, Br=64, absent_mass=True,
+                precision="bf16", eps=1e-5):
+        fp32 = _fp32(precision)
+        if unique_tensor.shape[1] != K_max:
+            raise ValueError(f"unique_tensor has {unique_tensor.shape[1]} slots but K_max={K_max}")
+        O, LSE = flash_ema_fwd_gq(x_q, C_seq, W_pe, ln_w, ln_b, W_q, float(eps), x, E_k_active, E_v_active,
+                                  rhos, unique_tensor, C_bounds, int(V_total), int(n_heads), bool(use_silu),
+                                  int(Br), bool(absent_mass), fp32)
+        ctx.save_for_backward(x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k_active, E_v_active, rhos,
+                              unique_tensor, C_bounds, O, LSE)
+        ctx.cfg = (int(V_total), bool(use_silu), int(Br), bool(absent_mass), fp32, float(eps), int(n_heads))
+        return O
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, dO):
+        from .triton_fused_gating import gating_bwd, gating_fwd
+        (x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k, E_v, rhos, unique_tensor, C_bounds, O,
+         LSE) = ctx.saved_tensors
+        V_total, use_silu, Br, absent_mass, fp32, eps, H = ctx.cfg
+        B, L, D = x_q.shape
+        hd = D // H
+        N = rhos.shape[0]
+        Wpe = W_pe[:N]
+        x_ln, mu, rstd = gating_fwd(x_q, None, None, C_seq, Wpe, ln_w, ln_b, use_silu, eps)
+        xr = x_ln.reshape(B * L, D)
+        Q = (xr @ W_q.t()).view(B, L, H, hd).transpose(1, 2)
+        dQ, dEk, dEv, dWa = flash_ema_bwd(Q, x, E_k, E_v, Wpe, rhos, unique_tensor, C_bounds, O, LSE,
+                                          dO.contiguous(), V_total, use_silu, Br, absent_mass, fp32)
+        dQr = dQ.transpose(1, 2).reshape(B * L, D)  # row (b, t), column h hd + d
+        dW_q = dQr.t() @ xr
+        dx_ln = dQr @ W_q
+        dxq, dpre, dbias, dlnw, dlnb = gating_bwd(dx_ln.view(B, L, D), x_q, None, None, C_seq, Wpe, ln_w,
+                                                  mu, rstd, use_silu)
+        # the gate's weight gradient: sum_r (C_seq[r] + 1)^T dpre[r] (the bias term's column sum
+        # came reduced from the kernel), plus the attention's
+        dW = torch.addmm(dbias.unsqueeze(0).expand(N, D), C_seq.reshape(-1, N).t(), dpre) + dWa
+        if W_pe.shape[0] > N:  # W_pe passed with padded rows: their gradient is 0
+            dW = torch.cat([dW, dW.new_zeros(W_pe.shape[0] - N, D)])
+        dC = (dpre @ Wpe.t()).reshape(C_seq.shape) if ctx.needs_input_grad[1] else None
+        return (dxq, dC, dW, dlnw, dlnb, dW_q, None, dEk, dEv, None, None, None, None, None, None, None,
+                None, None, None, None)
