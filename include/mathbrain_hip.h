@@ -149,6 +149,12 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
  *   scores    NULL, or [B, H, K, L] fp32 output: s[t,k] * log2(e) for every valid slot
  *             (rows of padding slots are not written).  Passed to mb_flash_ema_bwd, it
  *             spares the backward the score recomputation.
+ *   workspace NULL, or workspace_bytes >= mb_flash_ema_fwd_workspace(...) bytes of device
+ *             memory (16-byte aligned, contents irrelevant): room for the partial softmax
+ *             states when the launch splits each workgroup's slots into parts so that the
+ *             workgroups fill the device's last round (e.g. 896 workgroups of one per CU
+ *             on 256 CUs).  Without it (or when smaller) the launch runs unsplit; O and LSE
+ *             agree either way up to the order of the softmax sums.
  *
  * The gate operands are fp16: c_dec (chunk-start states above 65440 saturate there;
  * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to
@@ -162,7 +168,15 @@ int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
                      const float *E_v, const float *W_pe, const float *rhos,
                      const int64_t *unique, const float *C_bounds, int B, int H, int L, int hd,
                      int K, int N, int Np, int nc, int Br, int64_t V_total, int flags, float *O,
-                     float *LSE, float *scores, void *stream);
+                     float *LSE, float *scores, void *workspace, int64_t workspace_bytes,
+                     void *stream);
+
+/*
+ * Workspace bytes mb_flash_ema_fwd wants on the current device for these shapes and flags
+ * (0: it would not split), or -1 for arguments mb_flash_ema_fwd rejects (mb_last_error).
+ * No counterpart in the reference, whose Triton grid needs no workspace.
+ */
+int64_t mb_flash_ema_fwd_workspace(int B, int H, int L, int hd, int K, int N, int flags);
 
 /*
  * Flash-EMA gated cross-attention backward.  Replaces FlashEMAFunction.backward and its

@@ -32,7 +32,8 @@ SIGNATURES = {
     "mb_ema_boundary_states": ([_p, _i64, _i64, _i, _i, _p, _i, _p, _i, _i, _p, _i64, _p, _p, _i, _p], _i),
     "mb_unique_rows": ([_p, _i64, _i64, _i, _i, _p, _i, _p, _p], _i),
     "mb_flash_ema_fwd": ([_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p,
-                          _i, _i, _i, _i, _i, _i, _i, _i, _i, _i64, _i, _p, _p, _p, _p], _i),
+                          _i, _i, _i, _i, _i, _i, _i, _i, _i, _i64, _i, _p, _p, _p, _p, _i64, _p], _i),
+    "mb_flash_ema_fwd_workspace": ([_i, _i, _i, _i, _i, _i, _i], _i64),
     "mb_flash_ema_bwd": ([_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p,
                           _p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i64, _i, _p, _p, _p, _p,
                           _p, _p], _i),

@@ -451,10 +451,10 @@ static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     const FlashArgs& base = a;
 #define MB_BWD(MI, ME)                                                                            \
     do {                                                                                          \
-        const int rc_ = vr ? launch_with_lds(MB_BWD_PICK(MI, ME, true), grid, nthr, lds, st, a,      \
-                                             "mb_flash_ema_bwd")                                  \
-                           : launch_with_lds(MB_BWD_PICK(MI, ME, false), grid, nthr, lds, st, base, \
-                                             "mb_flash_ema_bwd");                                 \
+        const int rc_ = vr ? launch_with_lds(MB_BWD_PICK(MI, ME, true), grid, nthr, lds, st,        \
+                                             "mb_flash_ema_bwd", a)                               \
+                           : launch_with_lds(MB_BWD_PICK(MI, ME, false), grid, nthr, lds, st,       \
+                                             "mb_flash_ema_bwd", base);                           \
         if (rc_) return rc_;                                                                      \
     } while (0)
     if (mi <= 1 && me <= 1) MB_BWD(1, 1);

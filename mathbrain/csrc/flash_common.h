@@ -80,17 +80,17 @@ template <> struct FlashArgsOf<true> { using type = FlashArgsV; };
 __device__ inline int64_t e_rows_of(const FlashArgs& a) { return (int64_t)a.B * a.K; }
 __device__ inline int64_t e_rows_of(const FlashArgsV& a) { return a.e_rows; }
 
-// Sets a kernel's dynamic LDS limit and launches it with its argument block.
-template <class Kern, class Args>
-static int launch_with_lds(Kern k, dim3 grid, int nthr, size_t lds, hipStream_t st,
-                           const Args& args, const char* who) {
+// Sets a kernel's dynamic LDS limit and launches it with its arguments.
+template <class Kern, class... Args>
+static int launch_with_lds(Kern k, dim3 grid, int nthr, size_t lds, hipStream_t st, const char* who,
+                           const Args&... args) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return fail((int)e, "%s: LDS attribute: %s", who, hipGetErrorString(e));
     }
-    hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, args);
+    hipLaunchKernelGGL(k, grid, dim3(nthr), lds, st, args...);
     return MB_OK;
 }
 

@@ -26,13 +26,49 @@ int flash_validate(const char* who, const FlashArgs& a, int hd) {
 
 using namespace mb;
 
+// Picks the kernel instantiation for (hd, N, flags) and launches it, or with ws_need only
+// plans the slot split (see launch_fwd).
+static int fwd_dispatch(const FlashArgsV& a, int hd, int N, int flags, bool vr, hipStream_t st, float* part,
+                        int64_t ws_bytes, int64_t* ws_need) {
+    const int NS = (N + 31) / 32;
+    if (flags & MB_FLASH_FP32) {
+        // hi + lo operand tiles and the W_lo fragments in LDS: two slots per batch
+        if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
+        if (hd == 64)
+            return NS == 1 ? launch_fwd<64, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
+                           : launch_fwd<64, 2, 2, true>(a, vr, st, part, ws_bytes, ws_need);
+        return NS == 1 ? launch_fwd<32, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
+                       : launch_fwd<32, 2, 2, true>(a, vr, st, part, ws_bytes, ws_need);
+    }
+    if (hd == 64) {
+        if (NS == 1) return launch_fwd<64, 1, 4>(a, vr, st, part, ws_bytes, ws_need);
+        if (NS == 2) return launch_fwd<64, 2, 4>(a, vr, st, part, ws_bytes, ws_need);
+        return launch_fwd<64, 4, 2>(a, vr, st, part, ws_bytes, ws_need);
+    }
+    if (NS == 1) return launch_fwd<32, 1, 4>(a, vr, st, part, ws_bytes, ws_need);
+    if (NS == 2) return launch_fwd<32, 2, 4>(a, vr, st, part, ws_bytes, ws_need);
+    return launch_fwd<32, 4, 2>(a, vr, st, part, ws_bytes, ws_need);
+}
+
+extern "C" int64_t mb_flash_ema_fwd_workspace(int B, int H, int L, int hd, int K, int N, int flags) {
+    FlashArgsV a{};
+    a.B = B; a.H = H; a.L = L; a.hd = hd; a.K = K; a.N = N; a.Np = N; a.Br = 64;
+    a.nc = L > 0 ? (L + 63) / 64 : 1;
+    a.silu = (flags & MB_FLASH_SILU) ? 1 : 0;
+    if (flash_validate("mb_flash_ema_fwd_workspace", a, hd)) return -1;
+    if (B <= 0 || L <= 0) return 0;
+    int64_t need = 0;
+    if (fwd_dispatch(a, hd, N, flags, (flags & MB_FLASH_VOCAB_ROWS) != 0, nullptr, nullptr, 0, &need)) return -1;
+    return need;
+}
+
 extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int64_t q_sl,
                                 int64_t q_sd, const int64_t* x, int64_t x_sb, int64_t x_sl,
                                 const float* E_k, const float* E_v, const float* W_pe,
                                 const float* rhos, const int64_t* unique, const float* C_bounds,
                                 int B, int H, int L, int hd, int K, int N, int Np, int nc, int Br,
                                 int64_t V_total, int flags, float* O, float* LSE, float* scores,
-                                void* stream) {
+                                void* workspace, int64_t workspace_bytes, void* stream) {
     FlashArgsV a{};
     a.Q = Q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_sl = q_sl; a.q_sd = q_sd;
     a.x = x; a.x_sb = x_sb; a.x_sl = x_sl;
@@ -47,23 +83,11 @@ extern "C" int mb_flash_ema_fwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     int rc = flash_validate("mb_flash_ema_fwd", a, hd);
     if (rc) return rc;
     MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_fwd: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
+    MB_REQUIRE(workspace_bytes >= 0, "mb_flash_ema_fwd: negative workspace size %lld", (long long)workspace_bytes);
+    MB_REQUIRE(((uintptr_t)workspace & 15) == 0, "mb_flash_ema_fwd: workspace must be 16-byte aligned");
     if (B == 0 || L == 0) return MB_OK;
     MB_REQUIRE(Q && x && rhos && unique && O && LSE && W_pe, "mb_flash_ema_fwd: null pointer");
     MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_fwd: null slot pointer");
-    hipStream_t st = (hipStream_t)stream;
-    const int NS = (N + 31) / 32;
-    if (flags & MB_FLASH_FP32) {
-        // hi + lo operand tiles and the W_lo fragments in LDS: two slots per batch
-        if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
-        if (hd == 64) return NS == 1 ? launch_fwd<64, 1, 4, true>(a, vr, st) : launch_fwd<64, 2, 2, true>(a, vr, st);
-        return NS == 1 ? launch_fwd<32, 1, 4, true>(a, vr, st) : launch_fwd<32, 2, 2, true>(a, vr, st);
-    }
-    if (hd == 64) {
-        if (NS == 1) return launch_fwd<64, 1, 4>(a, vr, st);
-        if (NS == 2) return launch_fwd<64, 2, 4>(a, vr, st);
-        return launch_fwd<64, 4, 2>(a, vr, st);
-    }
-    if (NS == 1) return launch_fwd<32, 1, 4>(a, vr, st);
-    if (NS == 2) return launch_fwd<32, 2, 4>(a, vr, st);
-    return launch_fwd<32, 4, 2>(a, vr, st);
+    return fwd_dispatch(a, hd, N, flags, vr, (hipStream_t)stream, static_cast<float*>(workspace),
+                        workspace ? workspace_bytes : 0, nullptr);
 }

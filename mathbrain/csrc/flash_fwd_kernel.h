@@ -35,9 +35,19 @@ constexpr float kTau = 8.0f;
 // LDS (W_hi stays in registers) and the producer writes a c_lo tile beside c_hi.
 // GQ: the workgroup computes its queries from the gating inputs (flash_gq.h) instead of
 // reading Q.
+// Slot parts of the forward: each (b, block, head group) runs as ksplit workgroups over
+// consecutive ranges of its slot batches.  With ksplit > 1 each part writes its unnormalised
+// softmax state to `part` (ksplit x [B*H*L][hd] sums o, then ksplit x [B*H*L] (m, l) pairs)
+// and flash_fwd_merge_kernel forms O and LSE.  A second kernel argument, so that the
+// argument block the backward shares keeps its layout.
+struct FwdSplit {
+    float* part;
+    int ksplit;
+};
+
 template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR, bool PREC = false, bool GQ = false>
 __global__ void __launch_bounds__(512, 1)
-flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
+flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
     using S = Stage<NPAD, SB, false, PREC>;
@@ -46,11 +56,13 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
     const int D = a.H * HD;
     const int ntb = (a.L + kTB - 1) / kTB;
     const int logical = xcd_major(blockIdx.x, gridDim.x);
-    // one workgroup per (b, 32-step block, head group); a group holds hpg heads (hpg
-    // divides H), one wave each, and waves past hpg only help stage and synchronise
+    // one workgroup per (b, slot part, 32-step block, head group); a group holds hpg heads
+    // (hpg divides H), one wave each, and waves past hpg only help stage and synchronise.
+    // The blocks of one (b, part) are neighbours, so they share an XCD's L2 for their rows.
     const int hg = logical % a.head_groups;
-    const int b = logical / (a.head_groups * ntb);
     const int t0 = ((logical / a.head_groups) % ntb) * kTB;
+    const int part = (logical / (a.head_groups * ntb)) % sp.ksplit;
+    const int b = logical / (a.head_groups * ntb * sp.ksplit);
     const int cbi = t0 / a.Br;
     const int cb = cbi * a.Br;
     const int hpg = a.H / a.head_groups;
@@ -89,7 +101,10 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
     flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
     const int kvalid = kinfo[0];
     const int kend = kinfo[1];
-    const int nb = (kend + SB - 1) / SB;
+    // this part's batches [bi0, bi1)
+    const int nball = (kend + SB - 1) / SB;
+    const int bi0 = part * nball / sp.ksplit;
+    const int bi1 = (part + 1) * nball / sp.ksplit;
     const int x32 = (lane ^ 32) << 2;  // ds_bpermute byte address of lane l ^ 32
 
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
@@ -128,7 +143,8 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
     const float qscale = 1.0f / sqrtf((float)HD);
     f32x4 o[2][DT];
     float m[2], l[2];
-    const float absent = a.v_total >= 0.f ? fmaxf(a.v_total - (float)kvalid, 0.f) : 0.f;
+    // the absent slots' mass (score 0, no value) joins part 0's softmax sum
+    const float absent = a.v_total >= 0.f && part == 0 ? fmaxf(a.v_total - (float)kvalid, 0.f) : 0.f;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         const int t = t0 + 16 * tt + c16;
@@ -151,19 +167,19 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
     }
 
     Producer<NPAD, SB, MAXI, MAXE> prod;
-    if (nb > 0) {
-        flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
+    if (bi1 > bi0) {
+        flash_batch_meta<SB>(a, b, bi0, kend, win, meta_of(bi0));
         if (VR) __syncthreads();  // the load reads the batch's token ids
-        prod.template load<VR>(a, b, cbi, 0, kend, D, col0, WIDF, meta_of(0));
+        prod.template load<VR>(a, b, cbi, bi0, kend, D, col0, WIDF, meta_of(bi0));
         __syncthreads();
-        prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(0), cdec_of(0), nullptr, E_of(0), WIDF);
-        if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
+        prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(bi0), cdec_of(0), nullptr, E_of(0), WIDF);
+        if (bi0 + 1 < bi1) flash_batch_meta<SB>(a, b, bi0 + 1, kend, win, meta_of(bi0 + 1));
         __syncthreads();
     }
 
-    for (int bi = 0; bi < nb; ++bi) {
-        const int cur = bi & 1;
-        if (bi + 1 < nb) prod.template load<VR>(a, b, cbi, bi + 1, kend, D, col0, WIDF, meta_of(bi + 1));
+    for (int bi = bi0; bi < bi1; ++bi) {
+        const int cur = (bi - bi0) & 1;
+        if (bi + 1 < bi1) prod.template load<VR>(a, b, cbi, bi + 1, kend, D, col0, WIDF, meta_of(bi + 1));
         const _Float16* cdec = cdec_of(cur);
         const float* E = E_of(cur);
         const BatchMeta* meta = meta_of(bi);
@@ -265,14 +281,30 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
                 }
             }
         }
-        if (bi + 1 < nb) {
+        if (bi + 1 < bi1) {
             prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
                                               E_of(cur ^ 1), WIDF);
-            if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
+            if (bi + 2 < bi1) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         __syncthreads();
     }
 
+    if (sp.ksplit > 1) {  // this part's (o, m, l); flash_fwd_merge_kernel combines the parts
+        const int64_t rows = (int64_t)a.B * a.H * a.L;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = t0 + 16 * tt + c16;
+            if (t >= a.L || !active) continue;
+            const int64_t r = ((int64_t)b * a.H + h) * a.L + t;
+            float* prow = sp.part + ((int64_t)part * rows + r) * HD;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(prow + 16 * dt + 4 * g) = o[tt][dt];
+            if (g == 0)
+                reinterpret_cast<float2*>(sp.part + (int64_t)sp.ksplit * rows * HD)[(int64_t)part * rows + r] =
+                    make_float2(m[tt], l[tt]);
+        }
+        return;
+    }
     // O = ln2 * o / l  (the gate carried a factor log2 e), LSE = ln2 * (m + log2 l).
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -294,6 +326,83 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a) {
 #undef meta_of
 }
 
+// Combines the ksplit partial softmax states of each row (b, h, t): with M = max_p m_p and
+// w_p = 2^(m_p - M), l = sum_p w_p l_p, O = ln2 sum_p w_p o_p / l and LSE = ln2 (M + log2 l),
+// what one pass over all the slots gives up to the order of the sums.  HD / 4 lanes per
+// row, one f32x4 of O each.
+template <int HD>
+__global__ void __launch_bounds__(256)
+flash_fwd_merge_kernel(const float* __restrict__ part, int ks, int64_t rows, float* __restrict__ O,
+                       float* __restrict__ LSE) {
+    constexpr int LPR = HD / 4;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t r = i / LPR;
+    const int c = (int)(i % LPR) * 4;
+    if (r >= rows) return;
+    const float2* ml = reinterpret_cast<const float2*>(part + (int64_t)ks * rows * HD);
+    float M = -INFINITY;
+    for (int p = 0; p < ks; ++p) M = fmaxf(M, ml[p * rows + r].x);
+    float l = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {  // else no part saw a slot or an absent mass: l stays 0
+        for (int p = 0; p < ks; ++p) {
+            const float2 v = ml[p * rows + r];
+            const float w = __builtin_amdgcn_exp2f(v.x - M);  // 0 for an empty part (m = -inf)
+            l += w * v.y;
+            o += w * *reinterpret_cast<const f32x4*>(part + (p * rows + r) * HD + c);
+        }
+    }
+    const bool any = l > 0.f;
+    const float inv = any ? kLn2 / l : 0.f;
+    *reinterpret_cast<f32x4*>(O + r * HD + c) = o * inv;
+    if (c == 0) LSE[r] = any ? (M + __log2f(l)) * kLn2 : -INFINITY;
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Slot parts per workgroup of the forward.  The workgroups of one launch run in rounds of
+// `conc` (all that the device holds at once) and take about equally long, so G of them
+// take ceil(G / conc) rounds: 896 at configuration 2 take 4 rounds of 256 where 3.5 would
+// do.  Splitting each workgroup's slot batches into ks parts gives G ks workgroups of
+// 1 / ks the length; a split must save at least 3 % (each part repeats the prologue and
+// its state goes through the merge) and keep at least four batches per part.
+static int fwd_parts(int64_t G, int64_t conc, int nbatch) {
+    if (G <= 0 || conc <= 0) return 1;
+    int best = 1;
+    double best_cost = (double)((G + conc - 1) / conc);
+    for (int ks = 2; ks <= 4; ++ks) {
+        if (nbatch < 4 * ks) break;
+        const double cost = (double)((G * ks + conc - 1) / conc) / ks * (1.0 + 0.02 * (ks - 1));
+        if (cost < 0.97 * best_cost) {
+            best = ks;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+// Bytes of the forward's split workspace for ks parts.
+static int64_t fwd_part_bytes(int ks, int B, int H, int L, int hd) {
+    return ks > 1 ? (int64_t)ks * B * H * L * (hd + 2) * 4 : 0;
+}
+
 template <int HD, int NS, int SB, bool PREC>
 static size_t fwd_lds_bytes(int width, int nwaves) {
     return 2 * Stage<32 * NS, SB, false, PREC>::bytes(width) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
@@ -309,8 +418,12 @@ static int fwd_heads_per_group(int H) {
     return 1;
 }
 
+// Launches the forward (and, when the slot batches are split, the merge).  With ws_need set
+// it only plans: *ws_need = the workspace bytes the split wants (0: no split).  A launch
+// splits only when `part` holds that many bytes (ws_bytes); otherwise it runs unsplit.
 template <int HD, int NS, int SB, bool PREC = false, bool GQ = false, class A = FlashArgsV>
-static int launch_fwd(const A& a0, bool vr, hipStream_t st) {
+static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullptr, int64_t ws_bytes = 0,
+                      int64_t* ws_need = nullptr) {
     A a = a0;
     const int hpg = fwd_heads_per_group(a.H);
     a.head_groups = a.H / hpg;
@@ -325,18 +438,37 @@ static int launch_fwd(const A& a0, bool vr, hipStream_t st) {
     if (lds > 160 * 1024)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: %d heads of %d, N=%d need %zu B of LDS", hpg, HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
-    dim3 grid(a.B * ntb * a.head_groups);
+    const int64_t G = (int64_t)a.B * ntb * a.head_groups;
+    const int64_t rows = (int64_t)a.B * a.H * a.L;
     // the kernels without VR take the base argument block, the GQ ones always FlashArgsG
+    auto run = [&](auto kern, const auto& args) -> int {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nthr, lds) != hipSuccess || per_cu < 1) {
+            (void)hipGetLastError();
+            per_cu = 1;
+        }
+        const int ks = GQ ? 1 : fwd_parts(G, (int64_t)device_cus() * per_cu, (a.K + SB - 1) / SB);
+        const int64_t need = fwd_part_bytes(ks, a.B, a.H, a.L, HD);
+        if (ws_need) {
+            *ws_need = need;
+            return MB_OK;
+        }
+        const FwdSplit sp{part, (ks > 1 && part && ws_bytes >= need) ? ks : 1};
+        const int rc = launch_with_lds(kern, dim3(G * sp.ksplit), nthr, lds, st, "mb_flash_ema_fwd", args, sp);
+        if (rc || sp.ksplit == 1) return rc;
+        const int64_t threads = rows * (HD / 4);
+        hipLaunchKernelGGL(flash_fwd_merge_kernel<HD>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                           (const float*)part, sp.ksplit, rows, a.O, a.LSE);
+        return MB_OK;
+    };
     const typename FlashArgsK<false, GQ>::type& base = a;
-#define MB_FWD(MI, ME)                                                                           \
-    do {                                                                                         \
-        const int rc_ = vr ? launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true, PREC, GQ>    \
-                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true, PREC, GQ>,  \
-                                             grid, nthr, lds, st, a, "mb_flash_ema_fwd")                      \
-                           : launch_with_lds(a.silu ? flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false, PREC, GQ>   \
-                                                    : flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false, PREC, GQ>, \
-                                             grid, nthr, lds, st, base, "mb_flash_ema_fwd");                  \
-        if (rc_) return rc_;                                                                     \
+#define MB_FWD(MI, ME)                                                                                       \
+    do {                                                                                                     \
+        const int rc_ = vr ? (a.silu ? run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true, PREC, GQ>, a)         \
+                                     : run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true, PREC, GQ>, a))       \
+                           : (a.silu ? run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false, PREC, GQ>, base)     \
+                                     : run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false, PREC, GQ>, base));  \
+        if (rc_ || ws_need) return rc_;                                                                      \
     } while (0)
     const int me = (nvec + nthr - 1) / nthr;
     if (mi > 4 || me > 4)

@@ -8,6 +8,7 @@ registered as a torch op (mathbrain::boundary_states, unique_rows, flash_ema_fwd
 flash_ema_bwd) so that torch.compile traces through the attention instead of breaking
 the graph at the ctypes call.
 """
+import functools
 from typing import Optional
 
 import torch
@@ -163,13 +164,26 @@ def _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_
     O = torch.empty(B, H, L, hd, dtype=torch.float32, device=dev)
     LSE = torch.empty(B, H, L, dtype=torch.float32, device=dev)
     S2 = torch.empty(B, H, K, L, dtype=torch.float32, device=dev) if return_scores else None
+    flags = _flash_flags(use_silu, absent_mass, table, fp32)
     with torch.cuda.device(dev):
+        nws = _fwd_workspace_bytes(B, H, L, hd, K, N, flags, dev.index)
+        ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws > 0 else None
         _lib.call("mb_flash_ema_fwd", _lib.ptr(Qf), *Qf.stride(), _lib.ptr(xl), xl.stride(0),
                   xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W), _lib.ptr(rh),
                   _lib.ptr(uniq), _lib.ptr(Cb), B, H, L, hd, K, N, Cb.shape[3], Cb.shape[1],
-                  int(Br), int(V_total), _flash_flags(use_silu, absent_mass, table, fp32), _lib.ptr(O),
-                  _lib.ptr(LSE), _lib.ptr(S2), _lib.stream(dev))
+                  int(Br), int(V_total), flags, _lib.ptr(O), _lib.ptr(LSE), _lib.ptr(S2), _lib.ptr(ws), nws,
+                  _lib.stream(dev))
     return O, LSE, S2, Ek, Ev, table
+
+
+@functools.lru_cache(maxsize=256)
+def _fwd_workspace_bytes(B, H, L, hd, K, N, flags, device_index):
+    """Bytes of the forward's slot-split workspace (mb_flash_ema_fwd_workspace) on the
+    current device, which is `device_index`."""
+    n = _lib.lib().mb_flash_ema_fwd_workspace(B, H, L, hd, K, N, flags)
+    if n < 0:
+        raise _lib.HipKernelError("mb_flash_ema_fwd_workspace: " + _lib.lib().mb_last_error().decode(errors="replace"))
+    return int(n)
 
 
 def _fwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br, absent_mass,
@@ -183,7 +197,8 @@ def flash_ema_fwd(Q: torch.Tensor, x: torch.Tensor, E_k: torch.Tensor, E_v: torc
                   W_pe: torch.Tensor, rhos: torch.Tensor, unique_tensor: torch.Tensor,
                   C_bounds: torch.Tensor, V_total: int, use_silu: bool, Br: int,
                   absent_mass: bool, fp32: bool) -> tuple[torch.Tensor, torch.Tensor]:
-    """(O, LSE) of flash_ema_forward (one mb_flash_ema_fwd launch)."""
+    """(O, LSE) of flash_ema_forward (mb_flash_ema_fwd: one launch, and a merge launch when it
+    splits the slots into parts)."""
     O, LSE = _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br,
                        absent_mass, False, fp32)[:2]
     return O, LSE
