@@ -494,6 +494,7 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     a.e_rows = vr ? V_total : 0;
     int rc = flash_validate("mb_flash_ema_bwd", a, hd);
     if (rc) return rc;
+    if (hd > 64) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: head_dim %d (supported: 32, 64)", hd);
     MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_bwd: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
     // dE_k, dE_v and dW_pe are accumulated with atomics, so they are cleared first -- also
     // when there is no step to accumulate (B or L zero), which leaves them zero; every dQ

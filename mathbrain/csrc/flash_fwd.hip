@@ -9,8 +9,8 @@ int flash_validate(const char* who, const FlashArgs& a, int hd) {
     MB_REQUIRE(a.B >= 0 && a.L >= 0 && a.K >= 0, "%s: negative B=%d, L=%d or K=%d", who, a.B, a.L, a.K);
     MB_REQUIRE(a.H >= 1, "%s: H=%d must be >= 1", who, a.H);
     MB_REQUIRE(a.N >= 1 && a.Np >= a.N, "%s: need 1 <= N=%d <= Np=%d", who, a.N, a.Np);
-    if (hd != 32 && hd != 64)
-        return fail(MB_ERR_UNSUPPORTED, "%s: head_dim %d (supported: 32, 64)", who, hd);
+    if (hd != 32 && hd != 64 && hd != 128)
+        return fail(MB_ERR_UNSUPPORTED, "%s: head_dim %d (supported: 32, 64, 128)", who, hd);
     if (a.H > 64) return fail(MB_ERR_UNSUPPORTED, "%s: %d heads (supported: 1..64)", who, a.H);
     if (a.N > 128) return fail(MB_ERR_UNSUPPORTED, "%s: N=%d > 128", who, a.N);
     MB_REQUIRE(a.Br >= 1, "%s: Br=%d must be >= 1", who, a.Br);
@@ -34,11 +34,17 @@ static int fwd_dispatch(const FlashArgsV& a, int hd, int N, int flags, bool vr, 
     if (flags & MB_FLASH_FP32) {
         // hi + lo operand tiles and the W_lo fragments in LDS: two slots per batch
         if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
+        if (hd == 128) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: MB_FLASH_FP32 needs head_dim <= 64");
         if (hd == 64)
             return NS == 1 ? launch_fwd<64, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
                            : launch_fwd<64, 2, 2, true>(a, vr, st, part, ws_bytes, ws_need);
         return NS == 1 ? launch_fwd<32, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
                        : launch_fwd<32, 2, 2, true>(a, vr, st, part, ws_bytes, ws_need);
+    }
+    if (hd == 128) {  // two waves per head, one 16-step tile each
+        if (NS == 1) return launch_fwd<128, 1, 4>(a, vr, st, part, ws_bytes, ws_need);
+        if (NS == 2) return launch_fwd<128, 2, 4>(a, vr, st, part, ws_bytes, ws_need);
+        return launch_fwd<128, 4, 2>(a, vr, st, part, ws_bytes, ws_need);
     }
     if (hd == 64) {
         if (NS == 1) return launch_fwd<64, 1, 4>(a, vr, st, part, ws_bytes, ws_need);

@@ -45,11 +45,16 @@ struct FwdSplit {
     int ksplit;
 };
 
+// TW: 16-step tiles per wave.  2 (head_dim <= 64): wave w < hpg takes head w and both tiles
+// of the block; 1 (head_dim 128): wave w < 2 hpg takes head w % hpg and tile w / hpg, so that
+// a lane's queries, outputs and gate tiles stay within the register budget.
 template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR, bool PREC = false, bool GQ = false>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     constexpr int NPAD = 32 * NS;
     constexpr int DT = HD / 16;
+    constexpr int TW = HD > 64 ? 1 : 2;
+    static_assert(TW == 2 || (!GQ && !PREC), "head_dim 128: default mode only");
     using S = Stage<NPAD, SB, false, PREC>;
     extern __shared__ __align__(16) unsigned char smem[];
 
@@ -76,7 +81,9 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     int64_t* win = reinterpret_cast<int64_t*>(metas + 3 * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
-    f16x8* wlo = reinterpret_cast<f16x8*>(kinfo + 4);  // PREC: [head][dt][ns][lane]
+    // PREC: each wave's W_lo fragments [wave][dt][ns][lane]; TW = 1: the group's W fragments
+    // [head][dt][ns][lane], one copy that the two waves of a head read
+    f16x8* wlo = reinterpret_cast<f16x8*>(kinfo + 4);
 #define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
 #define meta_of(batch) (metas + ((batch) % 3) * SB)
@@ -85,11 +92,13 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     const int lane = threadIdx.x & 63;
     const int c16 = lane & 15;
     const int g = lane >> 4;
-    const bool active = wave < hpg;
-    const int h = active ? hg * hpg + wave : 0;  // idle waves read head 0 and write nothing
+    const bool active = wave < (TW == 2 ? hpg : 2 * hpg);
+    const int tile0 = TW == 2 ? 0 : wave / hpg;  // the wave's first 16-step tile
+    const int hw = TW == 2 ? wave : wave % hpg;  // the wave's head within the group
+    const int h = active ? hg * hpg + hw : 0;    // idle waves read head 0 and write nothing
 
-    // Queries of this lane's steps (lane c16 of step tile tt, dims 16 dt + 4 g + i).
-    f32x4 qs[2][DT];
+    // Queries of this lane's steps (lane c16 of step tile tile0 + tt, dims 16 dt + 4 g + i).
+    f32x4 qs[TW][DT];
     if constexpr (GQ) {
         // the prologue uses the start of LDS before anything else is staged there
         float* xl = reinterpret_cast<float*>(smem);
@@ -109,8 +118,23 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
 
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
     // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
-    f16x8 wf[DT][NS];
-    {
+    f16x8 wf[TW == 2 ? DT : 1][TW == 2 ? NS : 1];
+    if constexpr (TW == 1) {
+        if (active && tile0 == 0) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns) {
+                    f16x8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int n = 32 * ns + 8 * g + e;
+                        v[e] = (_Float16)(n < a.N ? a.W[(int64_t)n * D + h * HD + 16 * dt + c16] * kLog2e : 0.f);
+                    }
+                    wlo[((hw * DT + dt) * NS + ns) * 64 + lane] = v;
+                }
+        }
+    } else {
         float wraw[DT][NS][8];
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
@@ -141,13 +165,13 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
 
     // Queries pre-scaled by 1/sqrt(hd).
     const float qscale = 1.0f / sqrtf((float)HD);
-    f32x4 o[2][DT];
-    float m[2], l[2];
+    f32x4 o[TW][DT];
+    float m[TW], l[TW];
     // the absent slots' mass (score 0, no value) joins part 0's softmax sum
     const float absent = a.v_total >= 0.f && part == 0 ? fmaxf(a.v_total - (float)kvalid, 0.f) : 0.f;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int t = t0 + 16 * tt + c16;
+    for (int tt = 0; tt < TW; ++tt) {
+        const int t = t0 + 16 * (tile0 + tt) + c16;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -186,28 +210,34 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
         for (int j = 0; j < SB; ++j) {
             // padding slot (uniform across the workgroup), or a wave without a head
             if (meta[j].u < 0 || !active) continue;
-            f16x8 cf[2][NS];
+            f16x8 cf[TW][NS];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
+            for (int tt = 0; tt < TW; ++tt)
 #pragma unroll
                 for (int ns = 0; ns < NS; ++ns)
                     cf[tt][ns] = *reinterpret_cast<const f16x8*>(
-                        cdec + (j * kTB + 16 * tt + c16) * S::CROW + 32 * ns + 8 * g);
+                        cdec + (j * kTB + 16 * (tile0 + tt) + c16) * S::CROW + 32 * ns + 8 * g);
+            // the slot's e_k / e_v rows, this lane's dims; with one tile per wave read where used
+            auto e_row4 = [&](int which, int dt) {
+                return *reinterpret_cast<const f32x4*>(E + (j * 2 + which) * WIDF + hw * HD + 16 * dt + 4 * g);
+            };
             f32x4 ek[DT], ev[DT];
+            if constexpr (TW == 2) {
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                ek[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 0) * WIDF + wave * HD + 16 * dt + 4 * g);
-                ev[dt] = *reinterpret_cast<const f32x4*>(E + (j * 2 + 1) * WIDF + wave * HD + 16 * dt + 4 * g);
+                for (int dt = 0; dt < DT; ++dt) {
+                    ek[dt] = e_row4(0, dt);
+                    ev[dt] = e_row4(1, dt);
+                }
             }
-            f32x4 gt[2][DT];
+            f32x4 gt[TW][DT];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
+            for (int tt = 0; tt < TW; ++tt) {
                 f16x8 cl[NS];
                 if (PREC) {
 #pragma unroll
                     for (int ns = 0; ns < NS; ++ns)
                         cl[ns] = *reinterpret_cast<const f16x8*>(
-                            cdec + S::CDEC + (j * kTB + 16 * tt + c16) * S::CROW + 32 * ns + 8 * g);
+                            cdec + S::CDEC + (j * kTB + 16 * (tile0 + tt) + c16) * S::CROW + 32 * ns + 8 * g);
                 }
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
@@ -220,16 +250,20 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
                         for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cl[ns], acc);
                     }
 #pragma unroll
-                    for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cf[tt][ns], acc);
+                    for (int ns = 0; ns < NS; ++ns) {
+                        if constexpr (TW == 2) acc = mfma16x16x32(wf[dt][ns], cf[tt][ns], acc);
+                        else acc = mfma16x16x32(wlo[((hw * DT + dt) * NS + ns) * 64 + lane], cf[tt][ns], acc);
+                    }
                     gt[tt][dt] = acc;
                 }
             }
-            float s[2];
+            float s[TW];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
+            for (int tt = 0; tt < TW; ++tt) {
                 float sacc = 0.f;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
+                for (int dt = 0; dt < DT; ++dt) {
+                    const f32x4 ekd = TW == 2 ? ek[dt] : e_row4(0, dt);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const float x = gt[tt][dt][i];
@@ -239,8 +273,9 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
                             gv = x * __builtin_amdgcn_rcpf(1.0f + ex);
                         }
                         gt[tt][dt][i] = gv;
-                        sacc = __builtin_fmaf(qs[tt][dt][i], ek[dt][i] * gv, sacc);
+                        sacc = __builtin_fmaf(qs[tt][dt][i], ekd[i] * gv, sacc);
                     }
+                }
                 // lanes l ^ 16 (ds_swizzle, bitmask mode: and 0x1f, xor 0x10) and l ^ 32
                 // (ds_bpermute with a byte address computed once)
                 sacc += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(sacc), 0x401F));
@@ -250,10 +285,10 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
             // One (rare) rescale branch for both step tiles, so that the softmax and P.V of
             // the two tiles form one block the scheduler can interleave.
             const bool need0 = s[0] > m[0] + kTau;
-            const bool need1 = s[1] > m[1] + kTau;
+            const bool need1 = TW == 2 && s[TW - 1] > m[TW - 1] + kTau;
             if (__any(need0 || need1)) {
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
+                for (int tt = 0; tt < TW; ++tt) {
                     const float mn = (tt ? need1 : need0) ? s[tt] : m[tt];
                     const float alpha = __builtin_amdgcn_exp2f(m[tt] - mn);
                     l[tt] *= alpha;
@@ -263,20 +298,22 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
                 }
             }
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
+            for (int tt = 0; tt < TW; ++tt) {
                 const float p = __builtin_amdgcn_exp2f(s[tt] - m[tt]);
                 l[tt] += p;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
+                for (int dt = 0; dt < DT; ++dt) {
+                    const f32x4 evd = TW == 2 ? ev[dt] : e_row4(1, dt);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        o[tt][dt][i] = __builtin_fmaf(p, ev[dt][i] * gt[tt][dt][i], o[tt][dt][i]);
+                        o[tt][dt][i] = __builtin_fmaf(p, evd[i] * gt[tt][dt][i], o[tt][dt][i]);
+                }
             }
             if (a.S2out && g == 0) {
                 float* srow = a.S2out + (((int64_t)b * a.H + h) * a.K + bi * SB + j) * a.L;
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    const int t = t0 + 16 * tt + c16;
+                for (int tt = 0; tt < TW; ++tt) {
+                    const int t = t0 + 16 * (tile0 + tt) + c16;
                     if (t < a.L) srow[t] = s[tt];
                 }
             }
@@ -292,8 +329,8 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     if (sp.ksplit > 1) {  // this part's (o, m, l); flash_fwd_merge_kernel combines the parts
         const int64_t rows = (int64_t)a.B * a.H * a.L;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int t = t0 + 16 * tt + c16;
+        for (int tt = 0; tt < TW; ++tt) {
+            const int t = t0 + 16 * (tile0 + tt) + c16;
             if (t >= a.L || !active) continue;
             const int64_t r = ((int64_t)b * a.H + h) * a.L + t;
             float* prow = sp.part + ((int64_t)part * rows + r) * HD;
@@ -307,8 +344,8 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     }
     // O = ln2 * o / l  (the gate carried a factor log2 e), LSE = ln2 * (m + log2 l).
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int t = t0 + 16 * tt + c16;
+    for (int tt = 0; tt < TW; ++tt) {
+        const int t = t0 + 16 * (tile0 + tt) + c16;
         if (t >= a.L || !active) continue;
         const bool any = l[tt] > 0.f;
         const float inv = any ? kLn2 / l[tt] : 0.f;
@@ -403,17 +440,18 @@ static int64_t fwd_part_bytes(int ks, int B, int H, int L, int hd) {
     return ks > 1 ? (int64_t)ks * B * H * L * (hd + 2) * 4 : 0;
 }
 
+// nfrag: W fragment sets in LDS (PREC: one W_lo set per wave; head_dim 128: one W set per head)
 template <int HD, int NS, int SB, bool PREC>
-static size_t fwd_lds_bytes(int width, int nwaves) {
+static size_t fwd_lds_bytes(int width, int nfrag) {
     return 2 * Stage<32 * NS, SB, false, PREC>::bytes(width) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
-           65 * 32 * NS * 4 + 16 + (PREC ? (size_t)nwaves * (HD / 16) * NS * 64 * 16 : 0);
+           65 * 32 * NS * 4 + 16 + (size_t)nfrag * (HD / 16) * NS * 64 * 16;
 }
 
-// Heads per workgroup: all of them up to 8 (one wave each), else the largest divisor of
-// H that is at most 8, so that every group is whole.
-static int fwd_heads_per_group(int H) {
-    if (H <= 8) return H;
-    for (int d = 8; d > 1; --d)
+// Heads per workgroup: all of them up to hmax (8 with one wave per head, 4 with two), else
+// the largest divisor of H that is at most hmax, so that every group is whole.
+static int fwd_heads_per_group(int H, int hmax) {
+    if (H <= hmax) return H;
+    for (int d = hmax; d > 1; --d)
         if (H % d == 0) return d;
     return 1;
 }
@@ -425,15 +463,21 @@ template <int HD, int NS, int SB, bool PREC = false, bool GQ = false, class A = 
 static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullptr, int64_t ws_bytes = 0,
                       int64_t* ws_need = nullptr) {
     A a = a0;
-    const int hpg = fwd_heads_per_group(a.H);
+    constexpr int TW = HD > 64 ? 1 : 2;  // 16-step tiles per wave, as the kernel takes them
+    // head_dim 128: up to four heads (eight waves), fewer where their W fragments and
+    // staging would not fit in LDS
+    int hpg = fwd_heads_per_group(a.H, TW == 2 ? 8 : 4);
+    while (TW == 1 && hpg > 1 && fwd_lds_bytes<HD, NS, SB, PREC>(hpg * HD, hpg) > 160 * 1024)
+        hpg = fwd_heads_per_group(a.H, hpg - 1);
     a.head_groups = a.H / hpg;
     const int width = hpg * HD;
     // at least four waves, so that the producer's share per thread stays bounded
-    const int nthr = 64 * (hpg < 4 ? 4 : hpg);
+    const int nwv = TW == 2 ? hpg : 2 * hpg;
+    const int nthr = 64 * (nwv < 4 ? 4 : nwv);
     constexpr int NPAD = 32 * NS;
     const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
     const int nvec = SB * 2 * (width / 4);
-    size_t lds = fwd_lds_bytes<HD, NS, SB, PREC>(width, nthr / 64);
+    size_t lds = fwd_lds_bytes<HD, NS, SB, PREC>(width, PREC ? nthr / 64 : (TW == 1 ? hpg : 0));
     if (GQ) lds = std::max(lds, gq_fwd_lds_bytes(a.H * HD, a.N));
     if (lds > 160 * 1024)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: %d heads of %d, N=%d need %zu B of LDS", hpg, HD, a.N, lds);

@@ -54,6 +54,7 @@ extern "C" int mb_flash_ema_fwd_gq(const float* x_q, int64_t xq_sb, int64_t xq_s
     a.e_rows = vr ? V_total : 0;
     int rc = flash_validate("mb_flash_ema_fwd_gq", a, hd);
     if (rc) return rc;
+    if (hd > 64) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd_gq: head_dim %d (supported: 32, 64)", hd);
     if ((rc = gq_validate("mb_flash_ema_fwd_gq", a))) return rc;
     MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_fwd_gq: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
     if (B == 0 || L == 0) return MB_OK;
