@@ -160,8 +160,9 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
  * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to
  * ~45,000 steps) and W_pe * log2(e), with fp32 accumulation.
  *
- * Supported: hd in {32, 64}, 1 <= H <= 64, N <= 128 (N <= 64 with MB_FLASH_FP32), Br <= 32
- * or Br == 64.
+ * Supported: hd in {32, 64, 128} (32 or 64 with MB_FLASH_FP32), 1 <= H <= 64, N <= 128 (N <= 64
+ * with MB_FLASH_FP32), Br <= 32 or Br == 64.  At hd 128 each head takes two waves, one per
+ * 16-step tile of the workgroup's 32 steps.
  */
 int mb_flash_ema_fwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,
                      const int64_t *x, int64_t x_sb, int64_t x_sl, const float *E_k,
@@ -196,7 +197,8 @@ int64_t mb_flash_ema_fwd_workspace(int B, int H, int L, int hd, int K, int N, in
  * order is not fixed, as in the reference's tl.atomic_add.  The gate is recomputed as
  * in the forward; the dW_pe product takes bf16 c_dec and bf16 dpre (as the reference's
  * triton_flash_ema.py:463-465 does) with fp32 accumulation.  Supported: as
- * mb_flash_ema_fwd.
+ * mb_flash_ema_fwd.  At hd 128 each head runs as two 64-dim halves on two waves that add
+ * their score and dO . v partial sums through LDS.
  */
 int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t q_sd,
                      const float *dO, const int64_t *x, int64_t x_sb, int64_t x_sl,
@@ -227,8 +229,8 @@ int mb_flash_ema_bwd(const float *Q, int64_t q_sb, int64_t q_sh, int64_t q_sl, i
  *
  * W_pe serves both the query gate and the key gate, as in the reference.  The backward is
  * mb_flash_ema_bwd on Q recomputed from x_ln (the q_proj and gating gradients need x_ln, so
- * the caller recomputes it with mb_gating_fwd).  Supported: as mb_flash_ema_fwd with D a
- * multiple of 32 and at most 1024.
+ * the caller recomputes it with mb_gating_fwd).  Supported: as mb_flash_ema_fwd with hd 32
+ * or 64 and D a multiple of 32 and at most 1024.
  */
 int mb_flash_ema_fwd_gq(const float *x_q, int64_t xq_sb, int64_t xq_sl, const float *C_seq,
                         int64_t c_sb, int64_t c_sl, const float *ln_w, const float *ln_b, float eps,

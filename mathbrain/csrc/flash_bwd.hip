@@ -52,8 +52,11 @@ static int zero_fill(float* p, int64_t n, hipStream_t st) {
 // c_lo + W_hi c_hi) and the dW_pe product bf16 hi + lo pairs (dpre_lo c_hi + dpre_hi c_lo
 // + dpre_hi c_hi), both with fp32 accumulation; the producer writes the lo tiles beside
 // the hi ones and W_lo's fragments sit beside W_hi's in LDS.
+// SUB (head_dim 128 = 2 HD): a wave takes one 64-dim half ("sub-head") of a head, waves hl
+// and hl ^ 1 the two halves of one; everything is per dim except the score and dO . v sums
+// (and D = dO . O), which the pair adds through LDS: one barrier per slot.
 template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NTW, bool XH, bool VR,
-          bool PREC = false>
+          bool PREC = false, bool SUB = false>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     constexpr int NPAD = 32 * NS;
@@ -66,10 +69,12 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     constexpr bool TT = SB > 1 || XH || PREC;
     static_assert(!XH || SB == 1, "the dpre exchange buffer is reused slot after slot");
     static_assert(!(XH && PREC), "the fp32 mode takes N <= 64");
+    static_assert(!(SUB && PREC), "head_dim 128: default mode only");
+    constexpr int HDR = SUB ? 2 * HD : HD;  // the head's dims
     using S = Stage<NPAD, SB, TT, PREC>;
     extern __shared__ __align__(16) unsigned char smem[];
 
-    const int D = a.H * HD;
+    const int D = a.H * HDR;
     const int ntb = (a.L + kTB - 1) / kTB;
     const int logical = xcd_major(blockIdx.x, gridDim.x);
     const int hg = logical % a.head_groups;
@@ -90,6 +95,8 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
     bf16x4* xbuf = reinterpret_cast<bf16x4*>(kinfo + 4);  // XH: [head][half][DT][64 lanes]
+    // SUB: the sub-heads' partial sums, [exchange parity][sub-head][half][2 sums][16 steps]
+    float* pbuf = reinterpret_cast<float*>(xbuf + (XH ? kBwdHeads * 2 * DT * 64 : 0));
 #define cdec_of(i) reinterpret_cast<_Float16*>(smem + (i) * stage_bytes)
 #define cdecT_of(i) reinterpret_cast<__bf16*>(smem + (i) * stage_bytes + S::CTOFF)
 #define E_of(i) reinterpret_cast<float*>(smem + (i) * stage_bytes + S::EOFF)
@@ -102,11 +109,38 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     const int g = lane >> 4;
     const int hl = wave & 3;
     const int th = wave >> 2;
-    // a group holds hpg <= 4 heads (hpg divides H); waves of the missing heads only help
-    // stage and synchronise, and read head 0 for their (unused) setup
-    const int hpg = a.H / a.head_groups;
+    // a group holds hpg <= 4 heads (hpg divides H; with SUB, hpg sub-heads of hpg / 2 heads);
+    // waves of the missing heads only help stage and synchronise, and read head 0 for their
+    // (unused) setup
+    const int hpg = (SUB ? 2 : 1) * (a.H / a.head_groups);
     const bool active = hl < hpg;
-    const int h = active ? hg * hpg + hl : 0;
+    const int h = active ? (SUB ? hg * (hpg >> 1) + (hl >> 1) : hg * hpg + hl) : 0;
+    const int sub0 = SUB ? (hl & 1) * HD : 0;  // the wave's first dim within head h
+    // SUB: adds the partner sub-head's values of this wave's 16 steps (v[i], w[i]: step
+    // 4 g + i, equal over the lanes of a row) through pbuf.  Every wave of the group makes
+    // the same exchanges, so the areas alternate with them: an area is written again only
+    // after the next exchange's barrier, when both waves have read it.
+    int xpar = 0;
+    auto pair_sum = [&](float (&v)[4], float (&w)[4]) {
+        float* mine = pbuf + ((xpar * kBwdHeads + hl) * 2 + th) * 32;
+        const float* other = pbuf + ((xpar * kBwdHeads + (hl ^ 1)) * 2 + th) * 32;
+        xpar ^= 1;
+        if (active && c16 == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                mine[4 * g + i] = v[i];
+                mine[16 + 4 * g + i] = w[i];
+            }
+        }
+        __syncthreads();
+        if (active) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] += other[4 * g + i];
+                w[i] += other[16 + 4 * g + i];
+            }
+        }
+    };
 
     // Gate weights as the B operand: W[n = 32 ns + 8 g + e][d = 16 dt + c16] * log2 e,
     // one fragment per (head, dt, ns, lane) in LDS.
@@ -139,7 +173,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     const int nb = (kend + SB - 1) / SB;
 
     // Per-lane rows: steps t = t0 + 16 th + 4 g + i, dims d = 16 dt + c16 of head h.
-    const float qscale = 1.0f / sqrtf((float)HD);
+    const float qscale = 1.0f / sqrtf((float)HDR);
     float qs[DT][4], dov[DT][4], dq[DT][4];
     float lse2[4], Dv[4];
     {
@@ -149,10 +183,10 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             const int t = t0 + 16 * th + 4 * g + i;
             const bool ok = t < a.L;
             const int64_t qoff = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)t * a.q_sl;
-            const int64_t ooff = (((int64_t)b * a.H + h) * a.L + t) * HD;
+            const int64_t ooff = (((int64_t)b * a.H + h) * a.L + t) * HDR;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const int d = 16 * dt + c16;
+                const int d = sub0 + 16 * dt + c16;
                 qs[dt][i] = ok ? a.Q[qoff + (int64_t)d * a.q_sd] * qscale : 0.f;
                 dov[dt][i] = ok ? a.dO[qoff + (int64_t)d * a.q_sd] : 0.f;
                 dq[dt][i] = 0.f;
@@ -162,6 +196,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) Dv[i] = row_sum16(dsum[i]);
+        if (SUB) pair_sum(Dv, dsum);  // (dsum's partner values are not used)
     }
     f32x4 dWacc[DT][NTW];
 #pragma unroll
@@ -180,8 +215,9 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         const int hh = (threadIdx.x / kTB) % kBwdHeads;
         const int t = t0 + threadIdx.x % kTB;
         const int k = batch * SB + j;
+        const int hs = SUB ? hg * (hpg >> 1) + (hh >> 1) : hg * hpg + hh;  // the scores' head
         s2pre = (k < kend && t < a.L && hh < hpg)
-                    ? a.S2in[(((int64_t)b * a.H + hg * hpg + hh) * a.K + k) * a.L + t]
+                    ? a.S2in[(((int64_t)b * a.H + hs) * a.K + k) * a.L + t]
                     : 0.f;
     };
     auto store_scores = [&](float* dst) {
@@ -210,7 +246,11 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         const BatchMeta* meta = meta_of(bi);
         for (int j = 0; j < SB; ++j) {
             if (meta[j].u < 0) continue;  // padding slot (uniform across the workgroup)
-            if (!active) {                // a wave without a head: only the exchange barrier
+            if (!active) {                // a wave without a head: only the exchange barriers
+                if (SUB) {
+                    float unused[4] = {0.f, 0.f, 0.f, 0.f};
+                    pair_sum(unused, unused);
+                }
                 if (XH) __syncthreads();
                 continue;
             }
@@ -269,11 +309,19 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                     if (!HAS_S) s[i] = __builtin_fmaf(qs[dt][i] * ek[dt], gv, s[i]);
                     dp[i] = __builtin_fmaf(dov[dt][i] * ev[dt], gv, dp[i]);
                 }
+            if (SUB) {  // the head's sums over both sub-heads
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (!HAS_S) s[i] = row_sum16(s[i]);
+                    dp[i] = row_sum16(dp[i]);
+                }
+                pair_sum(s, dp);
+            }
             float p[4], ds[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s2 = HAS_S ? s2v[i] : row_sum16(s[i]);  // score * log2 e
-                const float dpt = row_sum16(dp[i]) * kLn2;          // dO . v
+                const float s2 = HAS_S ? s2v[i] : (SUB ? s[i] : row_sum16(s[i]));  // score * log2 e
+                const float dpt = (SUB ? dp[i] : row_sum16(dp[i])) * kLn2;          // dO . v
                 p[i] = __builtin_amdgcn_exp2f(s2 - lse2[i]);
                 ds[i] = p[i] * (dpt - Dv[i]);
             }
@@ -391,7 +439,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     for (int i = 0; i < 4; ++i) {
         const int t = t0 + 16 * th + 4 * g + i;
         if (t >= a.L || !active) continue;
-        float* dst = a.dQ + (((int64_t)b * a.H + h) * a.L + t) * HD;
+        float* dst = a.dQ + (((int64_t)b * a.H + h) * a.L + t) * HDR + sub0;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) dst[16 * dt + c16] = dq[dt][i] * qf;
     }
@@ -403,7 +451,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             if (n >= a.N || !active) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                atomicAdd(&a.dW[(int64_t)n * D + h * HD + 16 * dt + 4 * g + i], dWacc[dt][nt][i]);
+                atomicAdd(&a.dW[(int64_t)n * D + h * HDR + sub0 + 16 * dt + 4 * g + i], dWacc[dt][nt][i]);
         }
 #undef cdec_of
 #undef cdecT_of
@@ -412,19 +460,22 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #undef meta_of
 }
 
-template <int HD, int NS, int SB, bool XH, bool PREC>
+template <int HD, int NS, int SB, bool XH, bool PREC, bool SUB = false>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
     return 2 * (Stage<32 * NS, SB, (SB > 1 || XH || PREC), PREC>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
            (size_t)(PREC ? 2 : 1) * kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
-           kMaxWin * 8 + 65 * 32 * NS * 4 + 16 + (XH ? (size_t)kBwdHeads * 2 * (HD / 16) * 64 * 8 : 0);
+           kMaxWin * 8 + 65 * 32 * NS * 4 + 16 + (XH ? (size_t)kBwdHeads * 2 * (HD / 16) * 64 * 8 : 0) +
+           (SUB ? (size_t)2 * kBwdHeads * 2 * 32 * 4 : 0);
 }
 
-template <int HD, int NS, int SB, bool PREC = false>
+template <int HD, int NS, int SB, bool PREC = false, bool SUB = false>
 static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     FlashArgsV a = a0;
-    int hpg = 1;  // heads per group: the largest divisor of H that is at most four
-    for (int d = kBwdHeads; d > 1; --d)
+    // heads per group: the largest divisor of H that is at most four (with SUB two heads,
+    // whose four sub-heads take the four wave pairs)
+    int hpg = 1;
+    for (int d = SUB ? kBwdHeads / 2 : kBwdHeads; d > 1; --d)
         if (a.H % d == 0) { hpg = d; break; }
     a.head_groups = a.H / hpg;
     constexpr int NPAD = 32 * NS;
@@ -438,16 +489,16 @@ static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     constexpr int NTW = NT < 256 / HD ? NT : 256 / HD;
     constexpr bool XH = NT > NTW;
     static_assert(NT == NTW || NT == 2 * NTW, "at most two half-waves per head");
-    const size_t lds = bwd_lds_bytes<HD, NS, SB, XH, PREC>();
+    const size_t lds = bwd_lds_bytes<HD, NS, SB, XH, PREC, SUB>();
     if (lds > 160 * 1024)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: hd=%d, N=%d needs %zu B of LDS", HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
     dim3 grid(a.B * ntb * a.head_groups);
 #define MB_BWD_PICK(MI, ME, VR)                                                                  \
-    (a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH, VR, PREC>       \
-                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH, VR, PREC>)     \
-            : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH, VR, PREC>      \
-                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH, VR, PREC>))
+    (a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH, VR, PREC, SUB>       \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH, VR, PREC, SUB>)     \
+            : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH, VR, PREC, SUB>      \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH, VR, PREC, SUB>))
     const FlashArgs& base = a;
 #define MB_BWD(MI, ME)                                                                            \
     do {                                                                                          \
@@ -494,7 +545,6 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     a.e_rows = vr ? V_total : 0;
     int rc = flash_validate("mb_flash_ema_bwd", a, hd);
     if (rc) return rc;
-    if (hd > 64) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: head_dim %d (supported: 32, 64)", hd);
     MB_REQUIRE(!vr || V_total >= 1, "mb_flash_ema_bwd: MB_FLASH_VOCAB_ROWS needs V_total >= 1 rows");
     // dE_k, dE_v and dW_pe are accumulated with atomics, so they are cleared first -- also
     // when there is no step to accumulate (B or L zero), which leaves them zero; every dQ
@@ -517,8 +567,14 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
     if (flags & MB_FLASH_FP32) {
         // hi + lo operand tiles and both W fragment sets in LDS: one slot per batch
         if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
+        if (hd == 128) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: MB_FLASH_FP32 needs head_dim <= 64");
         if (hd == 64) return NS == 1 ? launch_bwd<64, 1, 1, true>(a, vr, st) : launch_bwd<64, 2, 1, true>(a, vr, st);
         return NS == 1 ? launch_bwd<32, 1, 1, true>(a, vr, st) : launch_bwd<32, 2, 1, true>(a, vr, st);
+    }
+    if (hd == 128) {  // two 64-dim sub-heads per head
+        if (NS == 1) return launch_bwd<64, 1, 4, false, true>(a, vr, st);
+        if (NS == 2) return launch_bwd<64, 2, 4, false, true>(a, vr, st);
+        return launch_bwd<64, 4, 1, false, true>(a, vr, st);
     }
     if (hd == 64) {
         if (NS == 1) return launch_bwd<64, 1, 4>(a, vr, st);

@@ -89,7 +89,7 @@ class SlotAttentionLayer(nn.Module):
     def _folds_query_gating(self, D):
         return (bool(self.fold_query_gating) and self.pe_proj.bias is None and self.q_proj.bias is None
                 and self.ln_q.weight is not None and self.ln_q.bias is not None and D % 32 == 0
-                and D <= 1024)
+                and D <= 1024 and self.head_dim <= 64)
 
     def forward(self, x_q, x, E_slots, rhos, C_seq, unique_tensor=None, K_max=None, C_bounds=None,
                 E_active=None):
