@@ -15,6 +15,10 @@ with HIP events on the launch stream, against the dense bf16/fp16 MFMA peak of 2
 `cpu_baseline` times the CPU restatement of the reference algorithm (the oracle, a port
 of the reference's PyTorch path) on a bounded slice of the same workload on this host.
 
+After the headline measurement the default run adds `secondary`: the cfg3 query scan, the
+query gating at cfg2's rows and the cfg5 training step, each measured the way its own
+`--workload` measures it (fewer steps, no CPU baseline); `--no-secondary` skips them.
+
 `--workload cfg4` runs the same step at configuration 4 (B=16, T=4096, N=128, a random
 0-10 % tail of padding per sequence with dO zero there); it is a second measurement, not the
 headline metric.
@@ -727,6 +731,28 @@ def run_factored(args):
     return line
 
 
+def secondary(args):
+    """The other configurations' numbers, measured in the same run after the headline one
+    (its timed region is over): the cfg3 query scan, the query gating at cfg2's rows and
+    the cfg5 training step, each its own workload's measurement at fewer steps and without a
+    CPU baseline.  Each entry keeps that workload's value, unit, ms and roofline."""
+    out = {}
+    for name, fn, steps in (("cfg3_scan", run_scan, 50), ("gating_cfg2_rows", run_gating, 20),
+                            ("cfg5_training_step", run_model, 10)):
+        sub = argparse.Namespace(**vars(args))
+        sub.steps, sub.warmup, sub.no_cpu_baseline = steps, 3, True
+        sub.workload = name
+        r = fn(sub)
+        entry = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "steps": steps,
+                 "ms_per_step": r["ms_per_step"]}
+        if "roofline" in r:
+            entry["roofline"] = {k: r["roofline"][k] for k in ("kernel", "achieved", "unit", "frac")}
+        out[name] = entry
+        del r
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -739,6 +765,9 @@ def main():
     ap.add_argument("--precision", choices=("bf16", "fp32"), default="bf16",
                     help="attention gate operands: fp16 (bf16 mode, the default) or fp16 hi + lo "
                          "pairs (fp32 mode); attention, cfg4 and model workloads")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="default workload: skip the secondary measurements (cfg3 scan, gating, "
+                         "cfg5 training step) that follow the headline one in the same run")
     ap.add_argument("--fold-query-gating", action="store_true",
                     help="model workload: compute the queries inside the attention kernel "
                          "(SlotAttentionLayer.fold_query_gating; off by default)")
@@ -754,6 +783,8 @@ def main():
            "gating": run_gating, "model": run_model, "copy": run_copy, "corpus": run_corpus,
            "batch": run_batch, "factored": run_factored}[args.workload]
     line = run(args)
+    if args.workload == "attention" and not args.no_secondary:
+        line["secondary"] = secondary(args)
     print(json.dumps(line), flush=True)
 
 

@@ -317,11 +317,32 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                 }
                 pair_sum(s, dp);
             }
+            // The 16 lanes' sums (dims), both quantities' chains interleaved (the fp32 mode
+            // keeps one chain after the other: interleaved, its larger live set spills).
+            if (!SUB && PREC) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (!HAS_S) s[i] = row_sum16(s[i]);
+                    dp[i] = row_sum16(dp[i]);
+                }
+            } else if (!SUB) {
+                if (HAS_S) {
+                    row_sum16_n(dp);
+                } else {
+                    float sd[8] = {s[0], s[1], s[2], s[3], dp[0], dp[1], dp[2], dp[3]};
+                    row_sum16_n(sd);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        s[i] = sd[i];
+                        dp[i] = sd[4 + i];
+                    }
+                }
+            }
             float p[4], ds[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s2 = HAS_S ? s2v[i] : (SUB ? s[i] : row_sum16(s[i]));  // score * log2 e
-                const float dpt = (SUB ? dp[i] : row_sum16(dp[i])) * kLn2;          // dO . v
+                const float s2 = HAS_S ? s2v[i] : s[i];  // score * log2 e
+                const float dpt = dp[i] * kLn2;         // dO . v
                 p[i] = __builtin_amdgcn_exp2f(s2 - lse2[i]);
                 ds[i] = p[i] * (dpt - Dv[i]);
             }
@@ -334,6 +355,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             for (int dt = 0; dt < DT; ++dt) {
                 dEk[dt] = 0.f;
                 dEv[dt] = 0.f;
+                float dvv[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float gv = g2[dt][i];
@@ -348,9 +370,18 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                         const float sig = sg[dt][i];
                         dsil = __builtin_fmaf(gv, __builtin_fmaf(-kLn2, sig, kLn2), sig);
                     }
-                    const float dv = av * dsil;
-                    dpre[dt][i] = (__bf16)dv;
-                    if (PREC) dprel[dt][i] = (__bf16)(dv - (float)dpre[dt][i]);
+                    dvv[i] = av * dsil;
+                }
+                if (PREC) {  // bf16 hi + lo of each value
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        dpre[dt][i] = (__bf16)dvv[i];
+                        dprel[dt][i] = (__bf16)(dvv[i] - (float)dpre[dt][i]);
+                    }
+                } else {  // two values per conversion
+                    const bf16x2 d01 = cvt_pk_bf16(dvv[0], dvv[1]);
+                    const bf16x2 d23 = cvt_pk_bf16(dvv[2], dvv[3]);
+                    dpre[dt] = bf16x4{d01[0], d01[1], d23[0], d23[1]};
                 }
             }
             // dE: this lane's 4 steps summed in registers; the 4 row groups (other steps)

@@ -29,6 +29,7 @@ namespace mb {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -138,6 +139,28 @@ __device__ inline float rows4_reduce_scatter2(float v0, float v1) {
     const float x = a.x + a.y;             // rows 0,1: v0 over halves; rows 2,3: v1
     const float2 c = swap_odd_rows(x, 0.0f);
     return c.x + c.y;
+}
+
+// Sums over the 16 lanes of a DPP row of n values, stage by stage: the n independent
+// chains interleave, so no DPP read waits on the VALU write just before it.
+template <int n>
+__device__ inline void row_sum16_n(float (&v)[n]) {
+#pragma unroll
+    for (int i = 0; i < n; ++i) v[i] += __builtin_amdgcn_update_dpp(0.0f, v[i], 0xB1, 0xF, 0xF, false);
+#pragma unroll
+    for (int i = 0; i < n; ++i) v[i] += __builtin_amdgcn_update_dpp(0.0f, v[i], 0x4E, 0xF, 0xF, false);
+#pragma unroll
+    for (int i = 0; i < n; ++i) v[i] += __builtin_amdgcn_update_dpp(0.0f, v[i], 0x141, 0xF, 0xF, false);
+#pragma unroll
+    for (int i = 0; i < n; ++i) v[i] += __builtin_amdgcn_update_dpp(0.0f, v[i], 0x140, 0xF, 0xF, false);
+}
+
+// Two floats to a packed bf16 pair (round to nearest even) in one v_cvt_pk_bf16_f32; a
+// vector cast compiles to one conversion per value plus a v_perm here.
+__device__ inline bf16x2 cvt_pk_bf16(float lo, float hi) {
+    uint32_t r;
+    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return __builtin_bit_cast(bf16x2, r);
 }
 
 // Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane gets the sum.
