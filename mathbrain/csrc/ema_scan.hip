@@ -101,13 +101,20 @@ constexpr int kTablePrefetch = 4;
 // Byte offsets of the per-sequence index inside dynamic LDS.  The sorted keys take Lp =
 // 2^ceil(log2 L) entries (the tail holds all-ones sentinels for the lookup); the radix
 // sort's scratch overlaps everything after them.
+// Hash grouping: a token with at least long_run(L) positions (at most kMaxLongRuns such
+// tokens) is ranked through a position bitmap instead of by counting.
+constexpr int kMaxLongRuns = 128;
+__host__ __device__ inline int long_run(int L) { return L / kMaxLongRuns > 16 ? (L + kMaxLongRuns - 1) / kMaxLongRuns : 16; }
+
 struct ScanLds {
     size_t keys, chain_start, elem_chain, chain_key, agg, aggr, lowT, highT, scan_scratch;
     size_t sort_b, sort_cnt;
+    size_t htab, hcnt, hpre, hpos, hbits, hlpre, hnl;  // grouping by hash (lgTS > 0)
     size_t total;
     // rows of the power tables and of the cut aggregates hold 1 << lgRow floats (the slice
     // width rounded up to a power of two, so that row addressing is a shift)
-    __host__ __device__ ScanLds(int L, int Lp, int key_bytes, int nthr, int ncut, int nH, int lgRow) {
+    __host__ __device__ ScanLds(int L, int Lp, int key_bytes, int nthr, int ncut, int nH, int lgRow,
+                                int lgTS = 0) {
         auto al = [](size_t o) { return (o + 15) & ~(size_t)15; };
         keys = 0;
         size_t o = al((size_t)Lp * key_bytes);
@@ -126,10 +133,29 @@ struct ScanLds {
         total = al(o);
         sort_b = after_keys;
         sort_cnt = al(sort_b + (size_t)L * key_bytes);
-        const size_t sort_end = al(sort_cnt + (size_t)(4 * nthr + 64) * 4);
-        if (sort_end > total) total = sort_end;
+        htab = hcnt = hpre = hpos = hbits = hlpre = hnl = 0;
+        if (lgTS > 0) {  // the hash tables live beside the index; no sort scratch
+            const size_t W = (size_t)(L + 63) / 64;  // bitmap words of a long run
+            htab = total;
+            hcnt = htab + ((size_t)4 << lgTS);
+            hpre = hcnt + ((size_t)4 << lgTS);
+            hpos = hpre + ((size_t)4 << lgTS);
+            hbits = al(hpos + (size_t)(L + 8) * 2);
+            hlpre = hbits + kMaxLongRuns * W * 8;
+            hnl = al(hlpre + kMaxLongRuns * W * 2);
+            total = al(hnl + 4);
+        } else {
+            const size_t sort_end = al(sort_cnt + (size_t)(4 * nthr + 64) * 4);
+            if (sort_end > total) total = sort_end;
+        }
     }
 };
+
+// Table slot of a 32-bit token key (multiplicative hash, top lgTS bits).
+__device__ inline int hash_slot(uint32_t key, int lgTS) {
+    return (int)((key * 0x9E3779B1u) >> (32 - lgTS));
+}
+constexpr uint32_t kHashEmpty = 0xFFFFFFFFu;
 
 // Query scan: one workgroup per (sequence b, slice of slice_w decay rates).
 //   0. this thread's tokens, c_init key ids and power-table entries go to registers;
@@ -143,14 +169,15 @@ struct ScanLds {
 //      and stamp at each chain's last element).
 // rho^d comes from two LDS tables per rate, rho^(d mod 64) * rho^(64 floor(d / 64)),
 // each entry a correctly rounded float of a double-precision power.
-template <typename KeyT, int VEC, bool DOCS, int MAXR>
+template <typename KeyT, int VEC, bool DOCS, int MAXR, bool HASH>
 __global__ void __launch_bounds__(kScanThreads)
 ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L,
                       const float* __restrict__ rhos, int N, const float* __restrict__ c_init,
                       const int64_t* __restrict__ c_init_keys, int K,
                       const int64_t* __restrict__ doc_ids, float* __restrict__ C_seq,
                       float* state_out, int32_t* __restrict__ stamp_out, int pb, int tok_bits,
-                      int slice_w, int lgS, int ncut) {
+                      int slice_w, int lgS, int ncut, int lgTS) {
+    static_assert(!HASH || sizeof(KeyT) == 4, "hash grouping keys are 32-bit tokens");
     // elements per unrolled chunk of a pass-B walk; their c_init rows (and with doc_ids
     // their documents) sit in registers
     constexpr int CH = DOCS ? 4 : 8;
@@ -161,7 +188,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     const int nH = (L - 1) / 64 + 1;
     const int Lp = 1 << pb;
     const int lgRow = ceil_log2(slice_w);
-    const ScanLds lay(L, Lp, (int)sizeof(KeyT), nthr, ncut, nH, lgRow);
+    const ScanLds lay(L, Lp, (int)sizeof(KeyT), nthr, ncut, nH, lgRow, HASH ? lgTS : 0);
     KeyT* keys = reinterpret_cast<KeyT*>(smem + lay.keys);
     uint16_t* chain_start = reinterpret_cast<uint16_t*>(smem + lay.chain_start);
     uint16_t* elem_chain = reinterpret_cast<uint16_t*>(smem + lay.elem_chain);
@@ -196,7 +223,16 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
 #pragma unroll
     for (int r = 0; r < kTablePrefetch; ++r) {
         const int i = threadIdx.x + r * nthr;
-        pre_tab[r] = i < n_tab && table_rate(i) < N ? rhos[table_rate(i)] : 0.f;
+        pre_tab[r] = rhos[min(table_rate(i), N - 1)];
+    }
+    // The four loads issue together and are waited for once, here: left to itself the
+    // compiler moves each load into the guarded computation below and waits for it there,
+    // one memory round trip after the other.
+    settle(pre_tab);
+#pragma unroll
+    for (int r = 0; r < kTablePrefetch; ++r) {
+        const int i = threadIdx.x + r * nthr;
+        if (!(i < n_tab && table_rate(i) < N)) pre_tab[r] = 0.f;
     }
     const int64_t doc0 = DOCS ? doc_ids[(int64_t)b * L] : 0;
 #pragma unroll
@@ -205,6 +241,129 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         pre_tab[r] = i < n_tab ? table_value(i / slice_w, (double)pre_tab[r]) : 0.f;
     }
 
+    if constexpr (HASH) {
+        // 1'. group the positions by token without sorting: a hash table of 2^lgTS >= 2L
+        // slots gives each distinct token a slot (linear probing) and its count; one block
+        // scan of (count, nonempty) packed in an int (low 16 bits: positions before the slot,
+        // high 16 bits: chains before it) gives every token its run [base, base + count) of
+        // the grouped order and its chain number.  The atomic placement leaves a run
+        // unordered, so each position then counts the run's earlier positions (runs are
+        // short except for the most frequent tokens) and lands at base + that rank: every
+        // chain lists its positions in order, as the passes below need.  The key word keeps
+        // the chain number where the sort keeps the token.
+        uint32_t* htab = reinterpret_cast<uint32_t*>(smem + lay.htab);
+        int* hcnt = reinterpret_cast<int*>(smem + lay.hcnt);
+        int* hpre = reinterpret_cast<int*>(smem + lay.hpre);
+        uint16_t* hpos = reinterpret_cast<uint16_t*>(smem + lay.hpos);
+        uint64_t* hbits = reinterpret_cast<uint64_t*>(smem + lay.hbits);
+        uint16_t* hlpre = reinterpret_cast<uint16_t*>(smem + lay.hlpre);
+        int* hnl = reinterpret_cast<int*>(smem + lay.hnl);
+        const int TS = 1 << lgTS;
+        const int W = (L + 63) >> 6;
+        const int T = long_run(L);
+        for (int i = threadIdx.x; i < TS; i += nthr) {
+            htab[i] = kHashEmpty;
+            hcnt[i] = 0;
+        }
+        for (int i = threadIdx.x; i < kMaxLongRuns * W; i += nthr) hbits[i] = 0;
+        if (threadIdx.x == 0) *hnl = 0;
+        __syncthreads();
+        const uint32_t tokmask = 0xFFFFFFFFu >> pb;
+        int slot[MAXR], urank[MAXR];
+#pragma unroll
+        for (int r = 0; r < MAXR; ++r) {
+            const int i = threadIdx.x + r * nthr;
+            slot[r] = 0;
+            urank[r] = 0;
+            if (i < L) {
+                const uint32_t key = (uint32_t)tokv[r] & tokmask;  // never kHashEmpty (pb >= 1)
+                int h = hash_slot(key, lgTS);
+                // ends: at most L of the TS >= 2L slots are ever taken
+                while (true) {
+                    const uint32_t old = atomicCAS(&htab[h], kHashEmpty, key);
+                    if (old == kHashEmpty || old == key) break;
+                    h = (h + 1) & (TS - 1);
+                }
+                slot[r] = h;
+                urank[r] = atomicAdd(&hcnt[h], 1);
+            }
+        }
+        __syncthreads();
+        const int per = (TS + nthr - 1) / nthr;
+        const int s0 = threadIdx.x * per;
+        int sum = 0;
+        for (int q = 0; q < per; ++q) {
+            const int c = s0 + q < TS ? hcnt[s0 + q] : 0;
+            sum += c + (c > 0 ? 1 << 16 : 0);
+        }
+        int total;
+        int run = block_exclusive_scan(sum, scratch, total);
+        for (int q = 0; q < per; ++q) {
+            if (s0 + q < TS) {
+                const int c = hcnt[s0 + q];
+                hpre[s0 + q] = run;
+                run += c + (c > 0 ? 1 << 16 : 0);
+                // a long run gets a bitmap (its number + 1 above the count; at most L / T
+                // <= kMaxLongRuns runs have T positions)
+                if (c >= T) hcnt[s0 + q] = c | ((atomicAdd(hnl, 1) + 1) << 16);
+            }
+        }
+        __syncthreads();
+        // short runs: unordered placement; long runs: one bit per position
+#pragma unroll
+        for (int r = 0; r < MAXR; ++r) {
+            const int i = threadIdx.x + r * nthr;
+            if (i < L) {
+                const int lid = hcnt[slot[r]] >> 16;
+                if (lid) atomicOr(&hbits[(lid - 1) * W + (i >> 6)], 1ull << (i & 63));
+                else hpos[(hpre[slot[r]] & 0xFFFF) + urank[r]] = (uint16_t)i;
+            }
+        }
+        __syncthreads();
+        {  // positions of a long run before each of its bitmap words (W <= 64: a wave per run)
+            const int lane = threadIdx.x & 63;
+            const int nl = *hnl;
+            for (int lr = threadIdx.x >> 6; lr < nl; lr += nthr >> 6) {
+                const int c = lane < W ? __popcll(hbits[lr * W + lane]) : 0;
+                const int ex = wave_inclusive_scan(c) - c;
+                if (lane < W) hlpre[lr * W + lane] = (uint16_t)ex;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < MAXR; ++r) {
+            const int i = threadIdx.x + r * nthr;
+            if (i < L) {
+                const int pre = hpre[slot[r]];
+                const int base = pre & 0xFFFF;
+                const int cid = pre >> 16;
+                const int cw = hcnt[slot[r]];
+                int rank = 0;
+                if (cw >> 16) {  // the run's positions below i: bitmap words before, then bits
+                    const int wi = ((cw >> 16) - 1) * W + (i >> 6);
+                    rank = (int)hlpre[wi] + __popcll(hbits[wi] & ((1ull << (i & 63)) - 1ull));
+                } else {  // fewer than T positions: count the earlier ones, eight reads
+                    // in flight at a time (hpos has 8 spare entries past L)
+                    for (int q = 0; q < cw; q += 8) {
+                        uint16_t v[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[e] = hpos[base + q + e];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) rank += (q + e < cw && v[e] < i) ? 1 : 0;
+                    }
+                }
+                const int j = base + rank;
+                keys[j] = (KeyT)cid << pb | (KeyT)i;
+                elem_chain[j] = (uint16_t)cid;
+                if (rank == 0) {
+                    chain_start[cid] = (uint16_t)base;
+                    chain_key[cid] = -1;
+                }
+            }
+        }
+        if (threadIdx.x == 0) chain_start[total >> 16] = (uint16_t)L;
+        for (int i = L + threadIdx.x; i < Lp; i += nthr) keys[i] = ~KeyT(0);
+    } else {
     // 1. sorted (token, position) keys, then all-ones sentinels up to Lp
     {
         const KeyT tokmask = (pb == 0) ? ~KeyT(0) : ((~KeyT(0)) >> pb);
@@ -224,9 +383,12 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         for (int i = L + threadIdx.x; i < Lp; i += nthr) keys[i] = ~KeyT(0);
     }
 
-    // 2. chain ids from one scan of head counts, element -> chain map, chain starts; the
-    // power tables (highT follows lowT: entry j >= 64 is rho^(64 (j - 64)))
+    }
+
+    // 2. chain ids from one scan of head counts, element -> chain map, chain starts (from
+    // the sort); the power tables (highT follows lowT: entry j >= 64 is rho^(64 (j - 64)))
     {
+        if constexpr (!HASH) {
         const int per = (L + nthr - 1) / nthr;
         const int i0 = threadIdx.x * per;
         const int i1 = min(i0 + per, L);
@@ -244,6 +406,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
             elem_chain[i] = (uint16_t)(c - 1);
         }
         if (threadIdx.x == 0) chain_start[n_chains] = (uint16_t)L;
+        }
         auto table_slot = [&](int i) { return ((i / slice_w) << lgRow) + i % slice_w; };
 #pragma unroll
         for (int r = 0; r < kTablePrefetch; ++r) {
@@ -264,6 +427,28 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     // Token ids compare in KeyT.  A key id that no sorted token can equal (negative, or
     // wider than the key layout's token field) searches for all-ones and is never matched.
     const uint64_t tok_lim = (uint64_t)(KeyT)~KeyT(0) >> pb;  // largest token the keys hold
+    if constexpr (HASH) {
+        // probe the token table; every taken slot holds a token of the sequence
+        const uint32_t* htab = reinterpret_cast<const uint32_t*>(smem + lay.htab);
+        const int* hpre = reinterpret_cast<const int*>(smem + lay.hpre);
+        const int TS = 1 << lgTS;
+        for (int kb = threadIdx.x; kb < K; kb += kKeyPrefetch * nthr) {
+#pragma unroll
+            for (int r = 0; r < kKeyPrefetch; ++r) {
+                const int k = kb + r * nthr;
+                const int64_t u = kb == (int)threadIdx.x ? pre_key[r]
+                                                         : (k < K ? c_init_keys[(int64_t)b * K + k] : (int64_t)-1);
+                if (k < K && u >= 0 && (uint64_t)u <= tok_lim) {
+                    const uint32_t key = (uint32_t)u;
+                    int h = hash_slot(key, lgTS);
+                    uint32_t cur;
+                    // ends at an empty slot: at most L of the TS >= 2L slots are taken
+                    while ((cur = htab[h]) != kHashEmpty && cur != key) h = (h + 1) & (TS - 1);
+                    if (cur == key) atomicMax(&chain_key[hpre[h] >> 16], k);
+                }
+            }
+        }
+    } else
     for (int kb = threadIdx.x; kb < K; kb += kKeyPrefetch * nthr) {
         KeyT tok[kKeyPrefetch];
         int lo[kKeyPrefetch];
@@ -636,35 +821,52 @@ extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x
     while (((L - 1) >> lgS) + 1 > groups) ++lgS;
     const int ncut = (L - 1) >> lgS;
     const int nH = (L - 1) / 64 + 1;
-    const ScanLds lay(L, 1 << pb, wide ? 8 : 4, kScanThreads, ncut, nH, ceil_log2(slice_w));
+    // Grouping by hash when the token keys are 32-bit and its tables fit beside the index
+    // (2^lgTS >= 2L slots); otherwise by the radix sort.
+    const int lgTS = pb + 1;
+    const ScanLds lay_hash(L, 1 << pb, 4, kScanThreads, ncut, nH, ceil_log2(slice_w), lgTS);
+    const bool hash = !wide && pb >= 1 && L <= 64 * 64 && lay_hash.total <= kMaxLds;
+    const ScanLds lay = hash ? lay_hash : ScanLds(L, 1 << pb, wide ? 8 : 4, kScanThreads, ncut, nH, ceil_log2(slice_w));
     if (lay.total > kMaxLds)
         return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d with vocab %lld needs %zu B of LDS",
                     L, (long long)vocab_size, lay.total);
     dim3 grid(B, ns);
     hipStream_t st = (hipStream_t)stream;
-#define MB_LAUNCH_SCAN(KT, V, DOCS)                                                            \
+#define MB_LAUNCH_SCAN_H(KT, V, DOCS, HASH)                                                    \
     do {                                                                                       \
         auto kfn = L <= 64 * kScanRoundsSmall * (kScanThreads / 64)                            \
-                       ? ema_query_scan_kernel<KT, V, DOCS, kScanRoundsSmall>                  \
-                       : ema_query_scan_kernel<KT, V, DOCS, kScanRoundsLarge>;                 \
+                       ? ema_query_scan_kernel<KT, V, DOCS, kScanRoundsSmall, HASH>            \
+                       : ema_query_scan_kernel<KT, V, DOCS, kScanRoundsLarge, HASH>;           \
         int rc = set_lds(kfn, lay.total);                                                      \
         if (rc) return rc;                                                                     \
         hipLaunchKernelGGL(kfn, grid, dim3(kScanThreads), lay.total, st, x, x_stride_b,        \
                            x_stride_l, L, rhos, N, c_init, c_init_keys, K, doc_ids, C_seq,     \
-                           state_out, stamp_out, pb, tok_bits, slice_w, lgS, ncut);           \
+                           state_out, stamp_out, pb, tok_bits, slice_w, lgS, ncut, lgTS);     \
+    } while (0)
+#define MB_LAUNCH_SCAN(KT, V, DOCS)                                                            \
+    do {                                                                                       \
+        if (hash) MB_LAUNCH_SCAN_H(KT, V, DOCS, true);                                         \
+        else MB_LAUNCH_SCAN_H(KT, V, DOCS, false);                                             \
     } while (0)
 #define MB_LAUNCH_SCAN_D(KT, V)                                     \
     do {                                                            \
         if (doc_ids) MB_LAUNCH_SCAN(KT, V, true);                   \
         else MB_LAUNCH_SCAN(KT, V, false);                          \
     } while (0)
-    if (wide) {
-        if (vec4) MB_LAUNCH_SCAN_D(uint64_t, 4); else MB_LAUNCH_SCAN_D(uint64_t, 1);
+    if (wide) {  // (never hashed)
+#define MB_LAUNCH_SCAN_W(V, DOCS) MB_LAUNCH_SCAN_H(uint64_t, V, DOCS, false)
+        if (vec4) {
+            if (doc_ids) MB_LAUNCH_SCAN_W(4, true); else MB_LAUNCH_SCAN_W(4, false);
+        } else {
+            if (doc_ids) MB_LAUNCH_SCAN_W(1, true); else MB_LAUNCH_SCAN_W(1, false);
+        }
+#undef MB_LAUNCH_SCAN_W
     } else {
         if (vec4) MB_LAUNCH_SCAN_D(uint32_t, 4); else MB_LAUNCH_SCAN_D(uint32_t, 1);
     }
 #undef MB_LAUNCH_SCAN_D
 #undef MB_LAUNCH_SCAN
+#undef MB_LAUNCH_SCAN_H
     return check_launch("mb_ema_query_scan");
 }
 
