@@ -9,9 +9,10 @@ dO N(0, 1) (synthetic, seeded).  One step = key-side chunk states (mb_ema_bounda
 + forward (mb_flash_ema_fwd) + backward (mb_flash_ema_bwd), all inputs resident in HBM.
 
 Prints one JSON line.  `roofline` is for the dominant kernel (the backward): algorithmic
-flops per launch, sum_b L*K_b*(4*N*D + 10*D) (gate recompute, dW_pe and the five
-per-element products; only valid (t, k) pairs count), over its mean launch time measured
-with HIP events on the launch stream, against the dense bf16/fp16 MFMA peak of 2516.6 TFLOP/s.
+flops per launch, sum_b L*K_b*(4*N*D + 10*D) (gate recompute, dW_pe and five
+per-element products: dO . (e_v g), dQ, dE_k, dE_v and dpre; the scores come from the
+forward, as FlashEMAFunction keeps them; only valid (t, k) pairs count), over its mean launch
+time measured with HIP events on the launch stream, against the dense bf16/fp16 MFMA peak of 2516.6 TFLOP/s.
 `cpu_baseline` times the CPU restatement of the reference algorithm (the oracle, a port
 of the reference's PyTorch path) on a bounded slice of the same workload on this host.
 
@@ -116,17 +117,22 @@ def attention_case(seed=0, config="cfg2"):
 
 
 def attention_step(c, timers=None, precision="bf16"):
-    from mathbrain.triton_flash_ema import flash_ema_backward, flash_ema_forward, precompute_boundaries
+    from mathbrain.triton_flash_ema import (flash_ema_backward, flash_ema_forward, keep_scores,
+                                            precompute_boundaries)
+    # the forward keeps its scores for the backward when FlashEMAFunction would
+    keep = keep_scores(c["B"], c["H"], c["K"], c["L"])
     Cb = precompute_boundaries(c["x"], c["unique"], c["rhos"], 64, c["c_base"])
     if timers is not None:
         timers["fwd"][0].record()
-    O, LSE, *_ = flash_ema_forward(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
-                                   c["unique"], c["K"], Cb, precision=precision)
+    res = flash_ema_forward(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
+                            c["unique"], c["K"], Cb, precision=precision, return_scores=keep)
+    O, LSE = res[0], res[1]
     if timers is not None:
         timers["fwd"][1].record()
         timers["bwd"][0].record()
     grads = flash_ema_backward(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
-                               c["unique"], Cb, O, LSE, c["dO"], precision=precision)
+                               c["unique"], Cb, O, LSE, c["dO"], precision=precision,
+                               scores=res[5] if keep else None)
     if timers is not None:
         timers["bwd"][1].record()
     return grads

@@ -329,11 +329,18 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
 
 
 # With SAVE_SCORES, FlashEMAFunction keeps the forward's scores ([B, H, K_max, L] fp32,
-# 1.4 GB at B=56, T=512, H=8, K_max=1638) and the backward skips recomputing them.  Off by
-# default: on gfx950 the extra live registers of that variant cost more than the skipped
-# score arithmetic (configuration 2: backward 23.0 ms recomputing vs 23.5 ms reading them,
-# and 0.3 ms more in the forward to write them).  Traced graphs never save them.
-SAVE_SCORES = False
+# 1.5 GB at B=56, T=512, H=8, K_max=1638) when they take at most SAVE_SCORES_MAX_BYTES, and
+# the backward reads them instead of recomputing them: configuration 2 measured forward
+# 9.09 -> 9.45 ms (writing them) and backward 22.49 -> 21.05 ms (no score products and half
+# the cross-lane sums), 31.6 -> 30.5 ms per layer.  Traced graphs never save them.
+SAVE_SCORES = True
+SAVE_SCORES_MAX_BYTES = 16 << 30
+
+
+def keep_scores(B, H, K_max, L):
+    """Whether FlashEMAFunction keeps the forward's scores for a call of this shape."""
+    return (SAVE_SCORES and not torch.compiler.is_compiling()
+            and 4 * int(B) * int(H) * int(K_max) * int(L) <= SAVE_SCORES_MAX_BYTES)
 
 
 class FlashEMAFunction(torch.autograd.Function):
@@ -350,13 +357,13 @@ class FlashEMAFunction(torch.autograd.Function):
     @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float32)
     def forward(ctx, Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
                 C_bounds, use_silu=True, Br=64, absent_mass=True, precision="bf16"):
-        keep_scores = SAVE_SCORES and not torch.compiler.is_compiling()
+        keep = keep_scores(Q.shape[0], Q.shape[1], unique_tensor.shape[1], Q.shape[2])
         res = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
-                                K_max, C_bounds, use_silu, Br, absent_mass, return_scores=keep_scores,
+                                K_max, C_bounds, use_silu, Br, absent_mass, return_scores=keep,
                                 precision=precision)
         O, LSE, C_bounds, E_k, E_v = res[:5]
         ctx.save_for_backward(Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE,
-                              res[5] if keep_scores else None)
+                              res[5] if keep else None)
         ctx.V_total = V_total
         ctx.use_silu = use_silu
         ctx.Br = Br
