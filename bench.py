@@ -59,10 +59,10 @@ PEAK_HBM_GBS = 8000.0
 # FETCH_SIZE and WRITE_SIZE passes scaled by a 1 GiB copy (profiles/flash_ema_cfg2.md,
 # profiles/flash_ema_cfg4.md); re-measured whenever the kernel changes.
 TRAFFIC_BYTES = {
-    "cfg2": 13261.7e6,
-    "cfg4": 45724.7e6,
+    "cfg2": 14705.3e6,
+    "cfg4": 50700.7e6,
     "corpus": 19654.0e6,   # the three mb_corpus_states launches (profiles/corpus_states_64M_tokens.md)
-    "scan": 110.3e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
+    "scan": 110.2e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
     "gating": 387.3e6,     # gating_fwd_kernel + gating_bwd_kernel (profiles/gating_cfg2_rows.md)
 }
 
