@@ -104,3 +104,15 @@ def test_factored_and_data_cpu_tensors_are_rejected():
     with pytest.raises(NotImplementedError, match="no CPU path"):
         factored_ema_forward(torch.zeros(1, 4, 8), torch.zeros(1, 4, dtype=torch.long),
                              torch.zeros(5, 8), torch.zeros(5, 8), torch.ones(2), torch.zeros(2, 8), 2)
+
+
+def test_scores_are_kept_up_to_the_memory_cap(monkeypatch):
+    """FlashEMAFunction keeps the forward's scores for its backward only while the
+    [B, H, K_max, L] fp32 tensor fits under SAVE_SCORES_MAX_BYTES, and never when switched off."""
+    from mathbrain import triton_flash_ema as tfe
+    assert tfe.keep_scores(56, 8, 1638, 512)                    # 1.47 GB
+    cap_elems = tfe.SAVE_SCORES_MAX_BYTES // 4
+    assert tfe.keep_scores(1, 1, cap_elems, 1)
+    assert not tfe.keep_scores(1, 1, cap_elems + 1, 1)
+    monkeypatch.setattr(tfe, "SAVE_SCORES", False)
+    assert not tfe.keep_scores(56, 8, 1638, 512)
