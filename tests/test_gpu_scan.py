@@ -119,6 +119,46 @@ def test_gpu_scan_lengths(L):
     _close(_scan(x, rhos, V).cpu().numpy(), oscan.query_scan(x, rhos, V))
 
 
+@pytest.mark.parametrize("L,V,pattern", [(4096, 97, "uniform"), (2048, 3, "uniform"),
+                                          (4096, 1, "uniform"), (4096, 1 << 19, "distinct"),
+                                          (3000, 200, "zipf"), (2048, 50257, "zipf"),
+                                          (100, 7, "uniform")])
+def test_gpu_scan_hash_grouping_runs(L, V, pattern):
+    """Grouping positions by token: the hash path (32-bit token keys and its tables in LDS,
+    L <= 2048 at this N) with runs counted position by position, runs long enough for the
+    position bitmaps (up to a few runs of ~700) and Zipf streams; the sort path for the longer
+    sequences (one run of all 4096 positions, no repeats at all).  Every output element, the
+    final state and the stamps against the oracle, with c_init keys."""
+    rng = np.random.default_rng(L + V)
+    B, N, K = 2, 8, 64
+    if pattern == "uniform":
+        x = rng.integers(0, V, size=(B, L))
+    elif pattern == "distinct":
+        x = np.stack([rng.permutation(V)[:L] for _ in range(B)])
+    else:
+        x = np.minimum(rng.zipf(1.1, size=(B, L)) - 1, V - 1)
+    rhos = np.exp(-np.log(2.0) / np.logspace(0, np.log10(4096), N)).astype(np.float32)
+    keys = np.stack([np.concatenate([rng.choice(x[b], K // 2), rng.integers(0, V, K - K // 2)])
+                     for b in range(B)])
+    keys[0, -3:] = -1
+    c_init = (rng.random((B, K, N)) * 3).astype(np.float32)
+    got, st, sp = _scan(x, rhos, V, c_init, keys, return_state=True)
+    want = oscan.query_scan(x, rhos, V, c_init, keys)
+    _close(got.cpu().numpy(), want)
+    sp = sp.cpu().numpy()
+    st = st.cpu().numpy()
+    for b in range(B):
+        for k in range(K):
+            if keys[b, k] < 0 or (keys[b, k + 1:] == keys[b, k]).any():
+                continue
+            occ = np.nonzero(x[b] == keys[b, k])[0]
+            if occ.size:
+                assert sp[b, k] == occ[-1]
+                _close(st[b, k], want[b, occ[-1]].astype(np.float64) + 1.0)
+            else:
+                assert sp[b, k] == -1
+
+
 @pytest.mark.parametrize("L,V,N,docs", [(2048, 1 << 30, 128, False), (2048, 1 << 30, 20, True),
                                          (8192, 20000, 16, False), (4096, 1 << 30, 64, True)])
 def test_gpu_scan_more_tokens_than_lds_state(L, V, N, docs):
