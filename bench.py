@@ -17,7 +17,7 @@ time measured with HIP events on the launch stream, against the dense bf16/fp16 
 of the reference's PyTorch path) on a bounded slice of the same workload on this host.
 
 After the headline measurement the default run adds `secondary`: the cfg3 query scan, the
-query gating at cfg2's rows and the cfg5 training step, each measured the way its own
+query gating at cfg2's rows, the cfg4 attention step and the cfg5 training step, each measured the way its own
 `--workload` measures it (fewer steps, no CPU baseline); `--no-secondary` skips them.
 
 `--workload cfg4` runs the same step at configuration 4 (B=16, T=4096, N=128, a random
@@ -739,15 +739,17 @@ def run_factored(args):
 
 def secondary(args):
     """The other configurations' numbers, measured in the same run after the headline one
-    (its timed region is over): the cfg3 query scan, the query gating at cfg2's rows and
-    the cfg5 training step, each its own workload's measurement at fewer steps and without a
-    CPU baseline.  Each entry keeps that workload's value, unit, ms and roofline."""
+    (its timed region is over): the cfg3 query scan, the query gating at cfg2's rows, the
+    cfg4 attention step and the cfg5 training step, each its own workload's measurement at
+    fewer steps and without a CPU baseline.  Each entry keeps that workload's value, unit, ms and roofline."""
     out = {}
-    for name, fn, steps in (("cfg3_scan", run_scan, 50), ("gating_cfg2_rows", run_gating, 20),
-                            ("cfg5_training_step", run_model, 10)):
+    for name, fn, steps, workload in (("cfg3_scan", run_scan, 50, "scan"),
+                                      ("gating_cfg2_rows", run_gating, 20, "gating"),
+                                      ("cfg4_attention", run_attention, 3, "cfg4"),
+                                      ("cfg5_training_step", run_model, 10, "model")):
         sub = argparse.Namespace(**vars(args))
-        sub.steps, sub.warmup, sub.no_cpu_baseline = steps, 3, True
-        sub.workload = name
+        sub.steps, sub.warmup, sub.no_cpu_baseline = steps, 1 if workload == "cfg4" else 3, True
+        sub.workload = workload
         r = fn(sub)
         entry = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "steps": steps,
                  "ms_per_step": r["ms_per_step"]}
@@ -772,7 +774,7 @@ def main():
                     help="attention gate operands: fp16 (bf16 mode, the default) or fp16 hi + lo "
                          "pairs (fp32 mode); attention, cfg4 and model workloads")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="default workload: skip the secondary measurements (cfg3 scan, gating, "
+                    help="default workload: skip the secondary measurements (cfg3 scan, gating, cfg4, "
                          "cfg5 training step) that follow the headline one in the same run")
     ap.add_argument("--fold-query-gating", action="store_true",
                     help="model workload: compute the queries inside the attention kernel "
