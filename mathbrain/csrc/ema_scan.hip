@@ -241,6 +241,44 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         pre_tab[r] = i < n_tab ? table_value(i / slice_w, (double)pre_tab[r]) : 0.f;
     }
 
+    // Power tables into LDS (highT follows lowT: entry j >= 64 is rho^(64 (j - 64))).
+    auto store_tables = [&]() {
+        auto table_slot = [&](int i) { return ((i / slice_w) << lgRow) + i % slice_w; };
+#pragma unroll
+        for (int r = 0; r < kTablePrefetch; ++r) {
+            const int i = threadIdx.x + r * nthr;
+            if (i < n_tab) lowT[table_slot(i)] = pre_tab[r];
+        }
+        for (int i = threadIdx.x + kTablePrefetch * nthr; i < n_tab; i += nthr)
+            lowT[table_slot(i)] = table_rate(i) < N ? table_value(i / slice_w, (double)rhos[table_rate(i)]) : 0.f;
+    };
+    // 3'. (hash path) each key row seeds the chain of its token by probing the token table
+    // (every taken slot holds a token of the sequence); the last duplicate key wins, as a
+    // sequential scatter_ leaves it (triton_ema_query.py:146-149).  Token ids compare as the
+    // keys hold them: a key id above tok_lim or negative is never matched.
+    auto hash_lookup = [&]() {
+        const uint64_t tok_lim = (uint64_t)(KeyT)~KeyT(0) >> pb;
+        const uint32_t* htab = reinterpret_cast<const uint32_t*>(smem + lay.htab);
+        const int* hpre = reinterpret_cast<const int*>(smem + lay.hpre);
+        const int TS = 1 << lgTS;
+        for (int kb = threadIdx.x; kb < K; kb += kKeyPrefetch * nthr) {
+#pragma unroll
+            for (int r = 0; r < kKeyPrefetch; ++r) {
+                const int k = kb + r * nthr;
+                const int64_t u = kb == (int)threadIdx.x ? pre_key[r]
+                                                         : (k < K ? c_init_keys[(int64_t)b * K + k] : (int64_t)-1);
+                if (k < K && u >= 0 && (uint64_t)u <= tok_lim) {
+                    const uint32_t key = (uint32_t)u;
+                    int h = hash_slot(key, lgTS);
+                    uint32_t cur;
+                    // ends at an empty slot: at most L of the TS >= 2L slots are taken
+                    while ((cur = htab[h]) != kHashEmpty && cur != key) h = (h + 1) & (TS - 1);
+                    if (cur == key) atomicMax(&chain_key[hpre[h] >> 16], k);
+                }
+            }
+        }
+    };
+
     if constexpr (HASH) {
         // 1'. group the positions by token without sorting: a hash table of 2^lgTS >= 2L
         // slots gives each distinct token a slot (linear probing) and its count; one block
@@ -267,6 +305,11 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         }
         for (int i = threadIdx.x; i < kMaxLongRuns * W; i += nthr) hbits[i] = 0;
         if (threadIdx.x == 0) *hnl = 0;
+        // the power tables and the stamps' initial -1 now: nothing of the grouping overlaps
+        // them, and their stores then need no phase (and barrier) of their own
+        store_tables();
+        if (stamp_out && slice == 0)
+            for (int k = threadIdx.x; k < K; k += nthr) stamp_out[(int64_t)b * K + k] = -1;
         __syncthreads();
         const uint32_t tokmask = 0xFFFFFFFFu >> pb;
         int slot[MAXR], urank[MAXR];
@@ -306,9 +349,16 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
                 // a long run gets a bitmap (its number + 1 above the count; at most L / T
                 // <= kMaxLongRuns runs have T positions)
                 if (c >= T) hcnt[s0 + q] = c | ((atomicAdd(hnl, 1) + 1) << 16);
+                if (c > 0) {  // this token's chain: its start and, until a key claims it, no key
+                    const int pre = hpre[s0 + q];
+                    chain_start[pre >> 16] = (uint16_t)(pre & 0xFFFF);
+                    chain_key[pre >> 16] = -1;
+                }
             }
         }
+        if (threadIdx.x == 0) chain_start[total >> 16] = (uint16_t)L;
         __syncthreads();
+        hash_lookup();
         // short runs: unordered placement; long runs: one bit per position
 #pragma unroll
         for (int r = 0; r < MAXR; ++r) {
@@ -355,13 +405,8 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
                 const int j = base + rank;
                 keys[j] = (KeyT)cid << pb | (KeyT)i;
                 elem_chain[j] = (uint16_t)cid;
-                if (rank == 0) {
-                    chain_start[cid] = (uint16_t)base;
-                    chain_key[cid] = -1;
-                }
             }
         }
-        if (threadIdx.x == 0) chain_start[total >> 16] = (uint16_t)L;
         for (int i = L + threadIdx.x; i < Lp; i += nthr) keys[i] = ~KeyT(0);
     } else {
     // 1. sorted (token, position) keys, then all-ones sentinels up to Lp
@@ -407,16 +452,11 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         }
         if (threadIdx.x == 0) chain_start[n_chains] = (uint16_t)L;
         }
-        auto table_slot = [&](int i) { return ((i / slice_w) << lgRow) + i % slice_w; };
-#pragma unroll
-        for (int r = 0; r < kTablePrefetch; ++r) {
-            const int i = threadIdx.x + r * nthr;
-            if (i < n_tab) lowT[table_slot(i)] = pre_tab[r];
+        if constexpr (!HASH) {
+            store_tables();
+            if (stamp_out && slice == 0)
+                for (int k = threadIdx.x; k < K; k += nthr) stamp_out[(int64_t)b * K + k] = -1;
         }
-        for (int i = threadIdx.x + kTablePrefetch * nthr; i < n_tab; i += nthr)
-            lowT[table_slot(i)] = table_rate(i) < N ? table_value(i / slice_w, (double)rhos[table_rate(i)]) : 0.f;
-        if (stamp_out && slice == 0)
-            for (int k = threadIdx.x; k < K; k += nthr) stamp_out[(int64_t)b * K + k] = -1;
         __syncthreads();
     }
 
@@ -427,28 +467,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     // Token ids compare in KeyT.  A key id that no sorted token can equal (negative, or
     // wider than the key layout's token field) searches for all-ones and is never matched.
     const uint64_t tok_lim = (uint64_t)(KeyT)~KeyT(0) >> pb;  // largest token the keys hold
-    if constexpr (HASH) {
-        // probe the token table; every taken slot holds a token of the sequence
-        const uint32_t* htab = reinterpret_cast<const uint32_t*>(smem + lay.htab);
-        const int* hpre = reinterpret_cast<const int*>(smem + lay.hpre);
-        const int TS = 1 << lgTS;
-        for (int kb = threadIdx.x; kb < K; kb += kKeyPrefetch * nthr) {
-#pragma unroll
-            for (int r = 0; r < kKeyPrefetch; ++r) {
-                const int k = kb + r * nthr;
-                const int64_t u = kb == (int)threadIdx.x ? pre_key[r]
-                                                         : (k < K ? c_init_keys[(int64_t)b * K + k] : (int64_t)-1);
-                if (k < K && u >= 0 && (uint64_t)u <= tok_lim) {
-                    const uint32_t key = (uint32_t)u;
-                    int h = hash_slot(key, lgTS);
-                    uint32_t cur;
-                    // ends at an empty slot: at most L of the TS >= 2L slots are taken
-                    while ((cur = htab[h]) != kHashEmpty && cur != key) h = (h + 1) & (TS - 1);
-                    if (cur == key) atomicMax(&chain_key[hpre[h] >> 16], k);
-                }
-            }
-        }
-    } else
+    if constexpr (!HASH)  // (the hash path matched its keys right after the grouping's scan)
     for (int kb = threadIdx.x; kb < K; kb += kKeyPrefetch * nthr) {
         KeyT tok[kKeyPrefetch];
         int lo[kKeyPrefetch];
@@ -474,7 +493,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
                 atomicMax(&chain_key[elem_chain[lo[r]]], kb + r * nthr);
         }
     }
-    __syncthreads();
+    if constexpr (!HASH) __syncthreads();
 
     const int lanes = slice_w / VEC;
     const int groups = nthr / lanes;
