@@ -258,14 +258,18 @@ int mb_flash_ema_fwd_gq(const float *x_q, int64_t xq_sb, int64_t xq_sl, const fl
  *           (pe_proj.weight transposed): used when p_pre is NULL
  *   y       [rows, D] contiguous output; mu, rstd [rows] outputs (LayerNorm statistics,
  *           consumed by mb_gating_bwd)
+ *   pre_out [rows, D] contiguous output, or NULL: the pre-activation pre[r,d], kept for
+ *           the backward as the reference keeps its gate (written at
+ *           triton_fused_gating.py:38, read back at :90); passed to mb_gating_bwd as p_pre
+ *           with a NULL bias, it spares the backward the projection
  *
- * Supported: D <= 1024, N <= 1024.
+ * bias may be NULL with p_pre (read as zero).  Supported: D <= 1024, N <= 1024.
  */
 int mb_gating_fwd(const float *x_q, int64_t xq_row_stride, const float *p_pre,
                   int64_t pp_row_stride, const float *bias, const float *C_seq,
                   int64_t c_row_stride, const float *W_pe, int N, const float *ln_w,
                   const float *ln_b, int64_t rows, int D, int use_silu, float eps, float *y,
-                  float *mu, float *rstd, void *stream);
+                  float *mu, float *rstd, float *pre_out, void *stream);
 
 /*
  * Fused symmetric query gating, backward.  Replaces _fused_gating_bwd and the backward of
@@ -279,7 +283,9 @@ int mb_gating_fwd(const float *x_q, int64_t xq_row_stride, const float *p_pre,
  *   dbias, dln_w, dln_b [D]  column sums of dp_pre, dy * x_hat and dy
  *
  * The column sums are cleared by the call (fill kernel) and accumulated with fp32
- * atomics, one per column and workgroup: their summation order is not fixed.
+ * atomics, one per column and workgroup: their summation order is not fixed.  With p_pre
+ * given (bias may be NULL) and D a multiple of 256 (16-byte aligned rows), one wave
+ * takes each row.
  */
 int mb_gating_bwd(const float *dy, const float *x_q, int64_t xq_row_stride, const float *p_pre,
                   int64_t pp_row_stride, const float *bias, const float *C_seq,

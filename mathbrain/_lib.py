@@ -40,7 +40,7 @@ SIGNATURES = {
     "mb_flash_ema_fwd_gq": ([_p, _i64, _i64, _p, _i64, _i64, _p, _p, _f, _p, _p, _i64, _i64, _p, _p, _p,
                              _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i64, _i, _p, _p, _p], _i),
     "mb_gating_fwd": ([_p, _i64, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _i64, _i, _i, _f, _p, _p,
-                       _p, _p], _i),
+                       _p, _p, _p], _i),
     "mb_gating_bwd": ([_p, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _p, _i64, _i, _i, _p,
                        _p, _p, _p, _p, _p], _i),
     "mb_corpus_states_workspace": ([_i64, _i], _i64),

@@ -48,6 +48,7 @@ struct GateArgs {
     float* y;
     float* mu;
     float* rstd;
+    float* pre_out;  // optional [rows, D]: the forward's pre-activation, kept for the backward
     // backward
     const float* dy;
     float* dxq;
@@ -97,7 +98,7 @@ __device__ inline void gate_pre_all(const GateArgs& a, int64_t r0, int nr, int t
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int col = tid + j * kGateThreads;
-            const float bv = col < a.D ? a.bias[col] : 0.f;
+            const float bv = col < a.D && a.bias ? a.bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < kGateRows; ++r)
                 pre[j][r] = (r < nr && col < a.D) ? a.pp[(r0 + r) * a.pp_sr + col] + bv : 0.f;
@@ -153,6 +154,7 @@ gating_fwd_kernel(GateArgs a) {
 #pragma unroll
             for (int r = 0; r < kGateRows; ++r) {
                 if (r >= nr) break;
+                if (a.pre_out) a.pre_out[(r0 + r) * a.D + col] = pre[j][r];
                 const float g = SILU ? pre[j][r] * sigmoidf_(pre[j][r]) : pre[j][r];
                 xe[r * a.D + col] = xv[j][r] * g;
             }
@@ -302,6 +304,111 @@ gating_bwd_kernel(GateArgs a) {
     }
 }
 
+// Backward with the pre-activation given (p_pre + bias; bias may be NULL, as for the
+// forward's kept pre-activation): one wave per row, lane l owning columns 4 l + 256 q + e,
+// so every load and store is a coalesced float4 and the LayerNorm row sums are wave
+// reductions (no LDS, no barrier per row).  A wave walks rows r, r + stride, ...; the next
+// row's inputs are requested before the current row is computed.  The column sums (dln_w,
+// dln_b, dbias) accumulate in registers over the wave's rows, go through LDS once per
+// workgroup and are added with one atomic per column and workgroup.
+template <int Q4, bool SILU>
+__global__ void __launch_bounds__(kGateThreads)
+gating_bwd_rows_kernel(GateArgs a) {
+    extern __shared__ __align__(16) float csm[];  // [3][kGateThreads / 64][D]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    constexpr int NW = kGateThreads / 64;
+    const int D = a.D;
+    float4 bias4[Q4], lnw4[Q4], accw[Q4], accb[Q4], accp[Q4];
+#pragma unroll
+    for (int q = 0; q < Q4; ++q) {
+        const int c = 4 * lane + 256 * q;
+        bias4[q] = a.bias ? *reinterpret_cast<const float4*>(a.bias + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        lnw4[q] = *reinterpret_cast<const float4*>(a.lnw + c);
+        accw[q] = accb[q] = accp[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int64_t stride = (int64_t)gridDim.x * NW;
+    int64_t r = (int64_t)blockIdx.x * NW + wave;
+    float4 xv[Q4], dyv[Q4], ppv[Q4];
+    auto load_row = [&](int64_t rr) {
+#pragma unroll
+        for (int q = 0; q < Q4; ++q) {
+            const int c = 4 * lane + 256 * q;
+            xv[q] = *reinterpret_cast<const float4*>(a.xq + rr * a.xq_sr + c);
+            dyv[q] = *reinterpret_cast<const float4*>(a.dy + rr * D + c);
+            ppv[q] = *reinterpret_cast<const float4*>(a.pp + rr * a.pp_sr + c);
+        }
+    };
+    if (r < a.rows) load_row(r);
+    for (; r < a.rows; r += stride) {
+        const float mu = a.mu[r], rs = a.rstd[r];
+        float xh[Q4][4], dxh[Q4][4], gg[Q4][4], xds[Q4][4];
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int q = 0; q < Q4; ++q) {
+            const float xe[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+            const float de[4] = {dyv[q].x, dyv[q].y, dyv[q].z, dyv[q].w};
+            const float pe[4] = {ppv[q].x + bias4[q].x, ppv[q].y + bias4[q].y, ppv[q].z + bias4[q].z,
+                                 ppv[q].w + bias4[q].w};
+            const float we[4] = {lnw4[q].x, lnw4[q].y, lnw4[q].z, lnw4[q].w};
+            float aw[4], ab[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float g = pe[e], dsil = 1.f;
+                if (SILU) {
+                    const float sg = sigmoidf_(pe[e]);
+                    g = pe[e] * sg;
+                    dsil = g + sg * (1.0f - g);  // SiLU' (triton_fused_gating.py:113-114)
+                }
+                gg[q][e] = g;
+                xds[q][e] = xe[e] * dsil;
+                xh[q][e] = (xe[e] * g - mu) * rs;
+                dxh[q][e] = de[e] * we[e];
+                s1 += dxh[q][e];
+                s2 = __builtin_fmaf(dxh[q][e], xh[q][e], s2);
+                aw[e] = de[e] * xh[q][e];
+                ab[e] = de[e];
+            }
+            accw[q].x += aw[0]; accw[q].y += aw[1]; accw[q].z += aw[2]; accw[q].w += aw[3];
+            accb[q].x += ab[0]; accb[q].y += ab[1]; accb[q].z += ab[2]; accb[q].w += ab[3];
+        }
+        // the next row's inputs while this one's sums reduce
+        if (r + stride < a.rows) load_row(r + stride);
+        const float c1 = wave_sum(s1) / (float)D;
+        const float c2 = wave_sum(s2) / (float)D;
+#pragma unroll
+        for (int q = 0; q < Q4; ++q) {
+            const int c = 4 * lane + 256 * q;
+            float dq[4], dp[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float dxe = (dxh[q][e] - c1 - xh[q][e] * c2) * rs;
+                dq[e] = dxe * gg[q][e];
+                dp[e] = dxe * xds[q][e];
+            }
+            *reinterpret_cast<float4*>(a.dxq + r * D + c) = make_float4(dq[0], dq[1], dq[2], dq[3]);
+            *reinterpret_cast<float4*>(a.dpp + r * D + c) = make_float4(dp[0], dp[1], dp[2], dp[3]);
+            accp[q].x += dp[0]; accp[q].y += dp[1]; accp[q].z += dp[2]; accp[q].w += dp[3];
+        }
+    }
+    // column sums: the workgroup's waves through LDS, then one atomic per column
+#pragma unroll
+    for (int q = 0; q < Q4; ++q) {
+        const int c = 4 * lane + 256 * q;
+        *reinterpret_cast<float4*>(csm + (0 * NW + wave) * D + c) = accw[q];
+        *reinterpret_cast<float4*>(csm + (1 * NW + wave) * D + c) = accb[q];
+        *reinterpret_cast<float4*>(csm + (2 * NW + wave) * D + c) = accp[q];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 3 * D; i += blockDim.x) {
+        const int k = i / D, c = i % D;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += csm[(k * NW + w) * D + c];
+        atomicAdd((k == 0 ? a.dlnw : k == 1 ? a.dlnb : a.dbias) + c, v);
+    }
+}
+
 __global__ void gate_zero_kernel(float* p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0.f;
 }
@@ -347,6 +454,27 @@ static int gate_launch(const GateArgs& a, bool fused, bool silu, hipStream_t st)
     return check_launch(BWD ? "mb_gating_bwd" : "mb_gating_fwd");
 }
 
+static int gate_rows_bwd_launch(const GateArgs& a, bool silu, hipStream_t st) {
+    constexpr int NW = kGateThreads / 64;
+    const int64_t waves = (a.rows + NW - 1) / NW;
+    const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(waves, 512)));
+    const size_t lds = (size_t)3 * NW * a.D * sizeof(float);
+#define MB_GATE_ROWS(Q)                                                                            \
+    do {                                                                                           \
+        auto k = silu ? gating_bwd_rows_kernel<Q, true> : gating_bwd_rows_kernel<Q, false>;        \
+        hipLaunchKernelGGL(k, grid, dim3(kGateThreads), lds, st, a);                               \
+    } while (0)
+    switch (a.D / 256) {
+        case 1: MB_GATE_ROWS(1); break;
+        case 2: MB_GATE_ROWS(2); break;
+        case 3: MB_GATE_ROWS(3); break;
+        case 4: MB_GATE_ROWS(4); break;
+        default: return fail(MB_ERR_UNSUPPORTED, "mb_gating_bwd: D=%d", a.D);
+    }
+#undef MB_GATE_ROWS
+    return check_launch("mb_gating_bwd");
+}
+
 static int gate_validate(const char* who, const GateArgs& a, bool fused) {
     MB_REQUIRE(a.rows >= 0, "%s: negative rows %lld", who, (long long)a.rows);
     MB_REQUIRE(a.D >= 1, "%s: D=%d must be >= 1", who, a.D);
@@ -369,18 +497,17 @@ extern "C" int mb_gating_fwd(const float* x_q, int64_t xq_row_stride, const floa
                              int64_t pp_row_stride, const float* bias, const float* C_seq,
                              int64_t c_row_stride, const float* W_pe, int N, const float* ln_w,
                              const float* ln_b, int64_t rows, int D, int use_silu, float eps,
-                             float* y, float* mu, float* rstd, void* stream) {
+                             float* y, float* mu, float* rstd, float* pre_out, void* stream) {
     GateArgs a{};
     a.xq = x_q; a.xq_sr = xq_row_stride; a.pp = p_pre; a.pp_sr = pp_row_stride; a.bias = bias;
     a.C = C_seq; a.c_sr = c_row_stride; a.W = W_pe; a.N = N; a.lnw = ln_w; a.lnb = ln_b;
-    a.rows = rows; a.D = D; a.eps = eps; a.y = y; a.mu = mu; a.rstd = rstd;
+    a.rows = rows; a.D = D; a.eps = eps; a.y = y; a.mu = mu; a.rstd = rstd; a.pre_out = pre_out;
     const bool fused = p_pre == nullptr;
     int rc = gate_validate("mb_gating_fwd", a, fused);
     if (rc) return rc;
     if (rows == 0) return MB_OK;
     MB_REQUIRE(x_q && ln_w && ln_b && y && mu && rstd, "mb_gating_fwd: null pointer");
-    MB_REQUIRE(fused ? (C_seq && W_pe) : (bias != nullptr),
-               "mb_gating_fwd: need p_pre and bias, or C_seq and W_pe");
+    MB_REQUIRE(fused ? (C_seq && W_pe) : true, "mb_gating_fwd: need p_pre, or C_seq and W_pe");
     return gate_launch<false>(a, fused, use_silu != 0, (hipStream_t)stream);
 }
 
@@ -408,7 +535,12 @@ extern "C" int mb_gating_bwd(const float* dy, const float* x_q, int64_t xq_row_s
     if ((rc = check_launch("mb_gating_bwd: clear"))) return rc;
     if (rows == 0) return MB_OK;
     MB_REQUIRE(dy && x_q && ln_w && mu && rstd && dx_q && dp_pre, "mb_gating_bwd: null pointer");
-    MB_REQUIRE(fused ? (C_seq && W_pe) : (bias != nullptr),
-               "mb_gating_bwd: need p_pre and bias, or C_seq and W_pe");
+    MB_REQUIRE(fused ? (C_seq && W_pe) : true, "mb_gating_bwd: need p_pre, or C_seq and W_pe");
+    // with the pre-activation given: the row kernel, when its float4 lanes fit the layout
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!fused && D % 256 == 0 && D <= 1024 && xq_row_stride % 4 == 0 && pp_row_stride % 4 == 0 &&
+        al16(x_q) && al16(p_pre) && al16(dy) && al16(dx_q) && al16(dp_pre) && al16(ln_w) &&
+        (!bias || al16(bias)))
+        return gate_rows_bwd_launch(a, use_silu != 0, st);
     return gate_launch<true>(a, fused, use_silu != 0, st);
 }

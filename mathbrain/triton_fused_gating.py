@@ -4,8 +4,9 @@ Drop-in for mathbrain/triton_fused_gating.py: ``FusedGatingFunction`` (:122-177)
 the reference's autograd signature (x_q, p_pre, bias, ln_w, ln_b, use_silu), and
 ``fused_apply_symmetric_query_gating`` (:179-197) keeps its call signature.  The latter
 folds the pe_proj projection (a K = N contraction) and its bias into the gating kernel
-(``GatedQueryFunction``), so the [B, L, D] pre-activation is never written in the
-forward; q_proj stays a library GEMM.  The row kernels are the gfx950 ones behind
+(``GatedQueryFunction``), so the pre-activation is never a separate GEMM's output; the
+forward keeps it for the backward (as the reference keeps its gate, :38 and :90), whose
+kernel then takes one row per wave without the projection; q_proj stays a library GEMM.  The row kernels are the gfx950 ones behind
 ``mb_gating_fwd`` / ``mb_gating_bwd``, registered as torch ops (mathbrain::gating_fwd /
 gating_bwd) for tracing.
 """
@@ -30,12 +31,7 @@ def _gate_fwd_fake(x_q, p_pre, bias, C_seq, W_pe, ln_w, ln_b, use_silu, eps):
     return x_q.new_empty(x_q.shape, dtype=torch.float32), mu, mu.new_empty((rows,))
 
 
-@_lib.traced_op("gating_fwd", _gate_fwd_fake)
-def gating_fwd(x_q: torch.Tensor, p_pre: Optional[torch.Tensor], bias: Optional[torch.Tensor],
-               C_seq: Optional[torch.Tensor], W_pe: Optional[torch.Tensor], ln_w: torch.Tensor,
-               ln_b: torch.Tensor, use_silu: bool, eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(y, mu, rstd): y = LayerNorm_eps(x_q * gate(pre)) * ln_w + ln_b with pre = p_pre + bias
-    (p_pre given) or (C_seq + 1) @ W_pe (W_pe [N, D] = pe_proj.weight transposed)."""
+def _gating_fwd(x_q, p_pre, bias, C_seq, W_pe, ln_w, ln_b, use_silu, eps, keep_pre):
     dev = _lib.require_gpu(x_q, p_pre, bias, C_seq, W_pe, ln_w, ln_b, what="query gating")
     D = x_q.shape[-1]
     xq, xs = _rows(x_q.to(torch.float32), D)
@@ -44,7 +40,7 @@ def gating_fwd(x_q: torch.Tensor, p_pre: Optional[torch.Tensor], bias: Optional[
     N = 0
     if p_pre is not None:
         pp, ps = _rows(p_pre.to(torch.float32), D)
-        bias = bias.to(torch.float32).contiguous()
+        bias = bias.to(torch.float32).contiguous() if bias is not None else None
     else:
         N = C_seq.shape[-1]
         if W_pe.shape != (N, D):
@@ -58,12 +54,37 @@ def gating_fwd(x_q: torch.Tensor, p_pre: Optional[torch.Tensor], bias: Optional[
     y = torch.empty(x_q.shape, dtype=torch.float32, device=dev)
     mu = torch.empty(rows, dtype=torch.float32, device=dev)
     rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    pre = torch.empty(rows if keep_pre else 0, D, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         _lib.call("mb_gating_fwd", _lib.ptr(xq), xs, _lib.ptr(pp), ps or 0, _lib.ptr(bias),
                   _lib.ptr(cs), css or 0, _lib.ptr(W), N, _lib.ptr(ln_w), _lib.ptr(ln_b), rows, D,
                   int(bool(use_silu)), float(eps), _lib.ptr(y), _lib.ptr(mu), _lib.ptr(rstd),
-                  _lib.stream(dev))
-    return y, mu, rstd
+                  _lib.ptr(pre) if keep_pre else None, _lib.stream(dev))
+    return y, mu, rstd, pre
+
+
+@_lib.traced_op("gating_fwd", _gate_fwd_fake)
+def gating_fwd(x_q: torch.Tensor, p_pre: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+               C_seq: Optional[torch.Tensor], W_pe: Optional[torch.Tensor], ln_w: torch.Tensor,
+               ln_b: torch.Tensor, use_silu: bool, eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(y, mu, rstd): y = LayerNorm_eps(x_q * gate(pre)) * ln_w + ln_b with pre = p_pre + bias
+    (p_pre given; a None bias is zero) or (C_seq + 1) @ W_pe (W_pe [N, D] =
+    pe_proj.weight transposed)."""
+    return _gating_fwd(x_q, p_pre, bias, C_seq, W_pe, ln_w, ln_b, use_silu, eps, False)[:3]
+
+
+def _gate_fwd_keep_fake(x_q, C_seq, W_pe, ln_w, ln_b, use_silu, eps):
+    y, mu, rstd = _gate_fwd_fake(x_q, None, None, C_seq, W_pe, ln_w, ln_b, use_silu, eps)
+    return y, mu, rstd, y.new_empty((mu.shape[0], x_q.shape[-1]))
+
+
+@_lib.traced_op("gating_fwd_keep_pre", _gate_fwd_keep_fake)
+def gating_fwd_keep_pre(x_q: torch.Tensor, C_seq: torch.Tensor, W_pe: torch.Tensor, ln_w: torch.Tensor,
+                        ln_b: torch.Tensor, use_silu: bool,
+                        eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """gating_fwd with the projection folded in, also returning the pre-activation
+    (C_seq + 1) @ W_pe as [rows, D] for the backward (which then needs no projection)."""
+    return _gating_fwd(x_q, None, None, C_seq, W_pe, ln_w, ln_b, use_silu, eps, True)
 
 
 def _gate_bwd_fake(dy, x_q, p_pre, bias, C_seq, W_pe, ln_w, mu, rstd, use_silu):
@@ -89,7 +110,7 @@ def gating_bwd(dy: torch.Tensor, x_q: torch.Tensor, p_pre: Optional[torch.Tensor
     N = 0
     if p_pre is not None:
         pp, ps = _rows(p_pre.to(torch.float32), D)
-        bias = bias.to(torch.float32).contiguous()
+        bias = bias.to(torch.float32).contiguous() if bias is not None else None
     else:
         N = C_seq.shape[-1]
         cs, css = _rows(C_seq.to(torch.float32), N)
@@ -141,16 +162,18 @@ class GatedQueryFunction(torch.autograd.Function):
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float32)
     def forward(ctx, x_q, C_seq, W_pe, ln_w, ln_b, use_silu=True, eps=1e-5):
-        y, mu, rstd = gating_fwd(x_q, None, None, C_seq, W_pe, ln_w, ln_b, bool(use_silu), float(eps))
-        ctx.save_for_backward(x_q, C_seq, W_pe, ln_w, mu, rstd)
+        # the pre-activation is kept ([rows, D] fp32, as the reference keeps its gate): the
+        # backward then runs on it instead of recomputing the projection
+        y, mu, rstd, pre = gating_fwd_keep_pre(x_q, C_seq, W_pe, ln_w, ln_b, bool(use_silu), float(eps))
+        ctx.save_for_backward(x_q, C_seq, W_pe, ln_w, mu, rstd, pre)
         ctx.use_silu = bool(use_silu)
         return y
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, dy):
-        x_q, C_seq, W_pe, ln_w, mu, rstd = ctx.saved_tensors
-        dxq, dpre, dbias, dlnw, dlnb = gating_bwd(dy, x_q, None, None, C_seq, W_pe, ln_w, mu, rstd,
+        x_q, C_seq, W_pe, ln_w, mu, rstd, pre = ctx.saved_tensors
+        dxq, dpre, dbias, dlnw, dlnb = gating_bwd(dy, x_q, pre, None, None, None, ln_w, mu, rstd,
                                                   ctx.use_silu)
         N, D = W_pe.shape
         dW = None

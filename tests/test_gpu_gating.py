@@ -49,7 +49,8 @@ def oracle_grads(c, use_silu):
     return y.detach(), grads
 
 
-@pytest.mark.parametrize("D,N", [(128, 16), (512, 64), (384, 128), (1000, 7)])
+@pytest.mark.parametrize("D,N", [(128, 16), (512, 64), (384, 128), (1000, 7), (256, 32), (768, 64),
+                                 (1024, 16)])
 @pytest.mark.parametrize("use_silu", [True, False])
 def test_folded_projection_fwd_bwd(D, N, use_silu):
     from mathbrain.triton_fused_gating import GatedQueryFunction
@@ -70,11 +71,13 @@ def test_folded_projection_fwd_bwd(D, N, use_silu):
 
 
 @pytest.mark.parametrize("use_silu", [True, False])
-def test_fused_gating_function_matches_reference_formulas(use_silu):
+@pytest.mark.parametrize("D", [512, 200])
+def test_fused_gating_function_matches_reference_formulas(use_silu, D):
     """FusedGatingFunction keeps the reference autograd signature: gradients of
-    (x_q, p_pre, bias, ln_w, ln_b) equal the reference kernel's closed form."""
+    (x_q, p_pre, bias, ln_w, ln_b) equal the reference kernel's closed form (D = 512: the
+    one-row-per-wave backward; D = 200: the tiled one)."""
     from mathbrain.triton_fused_gating import FusedGatingFunction
-    c = case(3, 41, 512, 64, seed=7)
+    c = case(3, 41, D, 64, seed=7)
     dt = torch.float64
     p_pre = c["C"] @ c["W"].t()
     bias = c["W"].sum(1)
