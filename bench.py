@@ -401,7 +401,7 @@ def run_gating(args):
             "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
             "config": {"workload": "gating fwd+bwd, pe_proj folded in, pre-activation kept for the backward", "rows": rows, "D": D, "N": N,
                        "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4)},
-            "roofline": {"bound": "hbm", "kernel": "gating_fwd_kernel + gating_bwd_rows_kernel",
+            "roofline": {"bound": "hbm", "kernel": "gating_fwd_rows_kernel + gating_bwd_rows_kernel",
                          "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES["gating"]}}
 

@@ -304,6 +304,125 @@ gating_bwd_kernel(GateArgs a) {
     }
 }
 
+// Forward with the projection folded in, R rows per wave: lane l owns columns 4 l + 256 q + e
+// of every row of the wave's tile, so the LayerNorm row sums are wave reductions (no LDS
+// pass, no barrier) and every load and store is a coalesced float4.  The tile's (C_seq + 1)
+// rows sit in the wave's own LDS area, read back as broadcasts; each W_pe row a lane needs
+// is loaded once per tile (from L2) and applied to all R rows, R times fewer W reads per row
+// than one row at a time.
+template <int Q4, bool SILU, int R>
+__global__ void __launch_bounds__(kGateThreads)
+gating_fwd_rows_kernel(GateArgs a) {
+    extern __shared__ __align__(16) float rsm[];  // [wave][R][NP]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    constexpr int NW = kGateThreads / 64;
+    const int D = a.D;
+    const int N = a.N;
+    const int NP = (N + 3) & ~3;
+    float* mc = rsm + wave * R * NP;
+    float4 lnw4[Q4], lnb4[Q4];
+#pragma unroll
+    for (int q = 0; q < Q4; ++q) {
+        lnw4[q] = *reinterpret_cast<const float4*>(a.lnw + 4 * lane + 256 * q);
+        lnb4[q] = *reinterpret_cast<const float4*>(a.lnb + 4 * lane + 256 * q);
+    }
+    const int64_t ntiles = (a.rows + R - 1) / R;
+    for (int64_t tile = (int64_t)blockIdx.x * NW + wave; tile < ntiles; tile += (int64_t)gridDim.x * NW) {
+        const int64_t r0 = tile * R;
+        const int nr = (int)std::min<int64_t>(R, a.rows - r0);
+        // every lane is done reading the previous tile's counts
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        for (int i = lane; i < R * NP; i += 64) {
+            const int r = i / NP, n = i % NP;
+            mc[i] = (r < nr && n < N) ? a.C[(r0 + r) * a.c_sr + n] + 1.0f : 0.f;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float4 pre[R][Q4];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int q = 0; q < Q4; ++q) pre[r][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 2
+        for (int n = 0; n < NP; n += 4) {
+            float4 w[4][Q4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int q = 0; q < Q4; ++q)
+                    w[k][q] = n + k < N ? *reinterpret_cast<const float4*>(a.W + (int64_t)(n + k) * D + 4 * lane + 256 * q)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float4 cv = *reinterpret_cast<const float4*>(mc + r * NP + n);
+                const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+#pragma unroll
+                    for (int q = 0; q < Q4; ++q) {
+                        pre[r][q].x = __builtin_fmaf(cc[k], w[k][q].x, pre[r][q].x);
+                        pre[r][q].y = __builtin_fmaf(cc[k], w[k][q].y, pre[r][q].y);
+                        pre[r][q].z = __builtin_fmaf(cc[k], w[k][q].z, pre[r][q].z);
+                        pre[r][q].w = __builtin_fmaf(cc[k], w[k][q].w, pre[r][q].w);
+                    }
+            }
+        }
+        float4 xv[Q4];
+        auto load_x = [&](int r) {
+#pragma unroll
+            for (int q = 0; q < Q4; ++q)
+                xv[q] = *reinterpret_cast<const float4*>(a.xq + (r0 + r) * a.xq_sr + 4 * lane + 256 * q);
+        };
+        load_x(0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r >= nr) continue;  // (uniform; keeps the loop unrolled, pre[] in registers)
+            const int64_t row = r0 + r;
+            float xe[Q4][4];
+            float s = 0.f;
+#pragma unroll
+            for (int q = 0; q < Q4; ++q) {
+                const float pe[4] = {pre[r][q].x, pre[r][q].y, pre[r][q].z, pre[r][q].w};
+                const float xx[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+                if (a.pre_out) *reinterpret_cast<float4*>(a.pre_out + row * D + 4 * lane + 256 * q) = pre[r][q];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float g = SILU ? pe[e] * sigmoidf_(pe[e]) : pe[e];
+                    xe[q][e] = xx[e] * g;
+                    s += xe[q][e];
+                }
+            }
+            if (r + 1 < nr) load_x(r + 1);  // the next row's x_q while this row's sums reduce
+            const float mean = wave_sum(s) / (float)D;
+            float v = 0.f;
+#pragma unroll
+            for (int q = 0; q < Q4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float dd = xe[q][e] - mean;
+                    v = __builtin_fmaf(dd, dd, v);
+                }
+            const float rs = 1.0f / sqrtf(wave_sum(v) / (float)D + a.eps);
+#pragma unroll
+            for (int q = 0; q < Q4; ++q) {
+                const float wv[4] = {lnw4[q].x, lnw4[q].y, lnw4[q].z, lnw4[q].w};
+                const float bv[4] = {lnb4[q].x, lnb4[q].y, lnb4[q].z, lnb4[q].w};
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (xe[q][e] - mean) * rs * wv[e] + bv[e];
+                *reinterpret_cast<float4*>(a.y + row * D + 4 * lane + 256 * q) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+            if (lane == 0) {
+                a.mu[row] = mean;
+                a.rstd[row] = rs;
+            }
+        }
+    }
+}
+
 // Backward with the pre-activation given (p_pre + bias; bias may be NULL, as for the
 // forward's kept pre-activation): one wave per row, lane l owning columns 4 l + 256 q + e,
 // so every load and store is a coalesced float4 and the LayerNorm row sums are wave
@@ -454,6 +573,29 @@ static int gate_launch(const GateArgs& a, bool fused, bool silu, hipStream_t st)
     return check_launch(BWD ? "mb_gating_bwd" : "mb_gating_fwd");
 }
 
+constexpr int kGateRowsPerWave = 4;
+
+static int gate_rows_fwd_launch(const GateArgs& a, bool silu, hipStream_t st) {
+    constexpr int NW = kGateThreads / 64;
+    constexpr int R = kGateRowsPerWave;
+    const int64_t tiles = (a.rows + R - 1) / R;
+    const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>((tiles + NW - 1) / NW, 1024)));
+    const size_t lds = (size_t)NW * R * ((a.N + 3) & ~3) * sizeof(float);
+#define MB_GATE_FROWS(Q)                                                                           \
+    do {                                                                                           \
+        auto k = silu ? gating_fwd_rows_kernel<Q, true, R> : gating_fwd_rows_kernel<Q, false, R>;  \
+        hipLaunchKernelGGL(k, grid, dim3(kGateThreads), lds, st, a);                               \
+    } while (0)
+    switch (a.D / 256) {
+        case 1: MB_GATE_FROWS(1); break;
+        case 2: MB_GATE_FROWS(2); break;
+        case 3: MB_GATE_FROWS(3); break;
+        default: return fail(MB_ERR_UNSUPPORTED, "mb_gating_fwd: D=%d", a.D);
+    }
+#undef MB_GATE_FROWS
+    return check_launch("mb_gating_fwd");
+}
+
 static int gate_rows_bwd_launch(const GateArgs& a, bool silu, hipStream_t st) {
     constexpr int NW = kGateThreads / 64;
     const int64_t waves = (a.rows + NW - 1) / NW;
@@ -508,6 +650,11 @@ extern "C" int mb_gating_fwd(const float* x_q, int64_t xq_row_stride, const floa
     if (rows == 0) return MB_OK;
     MB_REQUIRE(x_q && ln_w && ln_b && y && mu && rstd, "mb_gating_fwd: null pointer");
     MB_REQUIRE(fused ? (C_seq && W_pe) : true, "mb_gating_fwd: need p_pre, or C_seq and W_pe");
+    // with the projection folded in: the rows kernel, when its float4 lanes fit the layout
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (fused && D % 256 == 0 && D <= 768 && N <= 128 && xq_row_stride % 4 == 0 && al16(x_q) &&
+        al16(W_pe) && al16(ln_w) && al16(ln_b) && al16(y) && (!pre_out || al16(pre_out)))
+        return gate_rows_fwd_launch(a, use_silu != 0, (hipStream_t)stream);
     return gate_launch<false>(a, fused, use_silu != 0, (hipStream_t)stream);
 }
 
