@@ -27,6 +27,16 @@ int check_launch(const char* what);
 
 // ---- small device utilities -----------------------------------------------------------------
 
+// Streaming stores (global_store ... nt) for outputs that no later access of the same kernel
+// reads: the lines leave the L2 early instead of staying dirty there, so the write-back at
+// the kernel's end has less to do.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+__device__ inline void st_stream(float* dst, float v) { __builtin_nontemporal_store(v, dst); }
+__device__ inline void st_stream4(float* dst, float4 v) {
+    const f32x4v q = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(q, reinterpret_cast<f32x4v*>(dst));
+}
+
 __host__ __device__ inline int next_pow2(int v) {
     int p = 1;
     while (p < v) p <<= 1;

@@ -61,11 +61,11 @@ __device__ inline Vec<VEC> load_vec(const float* src, bool ok, int n0, int N) {
 template <int VEC>
 __device__ inline void store_vec(float* dst, const float* v, int n0, int N) {
     if (VEC == 4) {
-        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        st_stream4(dst, make_float4(v[0], v[1], v[2], v[3]));
     } else {
 #pragma unroll
         for (int i = 0; i < VEC; ++i)
-            if (n0 + i < N) dst[i] = v[i];
+            if (n0 + i < N) st_stream(dst + i, v[i]);
     }
 }
 
@@ -752,7 +752,7 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
 #pragma unroll
             for (int r = 0; r < RPL; ++r) {
                 const int n = lane + 64 * r;
-                if (n < Np) dst[n] = n < N ? c[r] : 0.f;
+                if (n < Np) st_stream(dst + n, n < N ? c[r] : 0.f);
             }
         };
         store(o);

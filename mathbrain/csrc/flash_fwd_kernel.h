@@ -314,7 +314,7 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
 #pragma unroll
                 for (int tt = 0; tt < TW; ++tt) {
                     const int t = t0 + 16 * (tile0 + tt) + c16;
-                    if (t < a.L) srow[t] = s[tt];
+                    if (t < a.L) st_stream(srow + t, s[tt]);
                 }
             }
         }

@@ -387,7 +387,7 @@ gating_fwd_rows_kernel(GateArgs a) {
             for (int q = 0; q < Q4; ++q) {
                 const float pe[4] = {pre[r][q].x, pre[r][q].y, pre[r][q].z, pre[r][q].w};
                 const float xx[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
-                if (a.pre_out) *reinterpret_cast<float4*>(a.pre_out + row * D + 4 * lane + 256 * q) = pre[r][q];
+                if (a.pre_out) st_stream4(a.pre_out + row * D + 4 * lane + 256 * q, pre[r][q]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float g = SILU ? pe[e] * sigmoidf_(pe[e]) : pe[e];
@@ -413,7 +413,7 @@ gating_fwd_rows_kernel(GateArgs a) {
                 float o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o[e] = (xe[q][e] - mean) * rs * wv[e] + bv[e];
-                *reinterpret_cast<float4*>(a.y + row * D + 4 * lane + 256 * q) = make_float4(o[0], o[1], o[2], o[3]);
+                st_stream4(a.y + row * D + 4 * lane + 256 * q, make_float4(o[0], o[1], o[2], o[3]));
             }
             if (lane == 0) {
                 a.mu[row] = mean;
@@ -505,8 +505,8 @@ gating_bwd_rows_kernel(GateArgs a) {
                 dq[e] = dxe * gg[q][e];
                 dp[e] = dxe * xds[q][e];
             }
-            *reinterpret_cast<float4*>(a.dxq + r * D + c) = make_float4(dq[0], dq[1], dq[2], dq[3]);
-            *reinterpret_cast<float4*>(a.dpp + r * D + c) = make_float4(dp[0], dp[1], dp[2], dp[3]);
+            st_stream4(a.dxq + r * D + c, make_float4(dq[0], dq[1], dq[2], dq[3]));
+            st_stream4(a.dpp + r * D + c, make_float4(dp[0], dp[1], dp[2], dp[3]));
             accp[q].x += dp[0]; accp[q].y += dp[1]; accp[q].z += dp[2]; accp[q].w += dp[3];
         }
     }
