@@ -62,8 +62,8 @@ TRAFFIC_BYTES = {
     "cfg2": 14705.3e6,
     "cfg4": 50700.7e6,
     "corpus": 19654.0e6,   # the three mb_corpus_states launches (profiles/corpus_states_64M_tokens.md)
-    "scan": 110.2e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
-    "gating": 485.3e6,     # gating_fwd_rows_kernel + gating_bwd_rows_kernel (profiles/gating_cfg2_rows.md)
+    "scan": 109.3e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
+    "gating": 484.0e6,     # gating_fwd_rows_kernel + gating_bwd_rows_kernel (profiles/gating_cfg2_rows.md)
 }
 
 
