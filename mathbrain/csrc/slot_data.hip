@@ -86,7 +86,7 @@ corpus_unit_kernel(const int64_t* __restrict__ order, const int64_t* __restrict_
                 if (!WALK) A[q] *= a;
                 S[q] = __builtin_fmaf(a, S[q], 1.0f);
                 const int n = lane + 64 * q;
-                if (WALK && pj >= 0 && n < N) states[(int64_t)pj * N + n] = S[q];
+                if (WALK && pj >= 0 && n < N) st_stream(states + (int64_t)pj * N + n, S[q]);
             }
         }
     }
