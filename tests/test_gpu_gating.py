@@ -50,7 +50,7 @@ def oracle_grads(c, use_silu):
 
 
 @pytest.mark.parametrize("D,N", [(128, 16), (512, 64), (384, 128), (1000, 7), (256, 32), (768, 64),
-                                 (1024, 16)])
+                                 (1024, 16), (512, 30), (256, 1)])
 @pytest.mark.parametrize("use_silu", [True, False])
 def test_folded_projection_fwd_bwd(D, N, use_silu):
     from mathbrain.triton_fused_gating import GatedQueryFunction
