@@ -83,9 +83,9 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     const int cbi = t0 / a.Br;
     const int cb = cbi * a.Br;
 
-    // LDS: 2 staging buffers (cdec | E | scores [SB][heads][kTB]) | W fragments |
+    // LDS: 2 staging buffers (cdec | E | probabilities [SB][heads][kTB]) | W fragments |
     // meta ring | window | power table | slot info
-    constexpr int SCN = HAS_S ? SB * kBwdHeads * kTB : 0;  // staged scores per buffer
+    constexpr int SCN = HAS_S ? SB * kBwdHeads * kTB : 0;  // staged probabilities per buffer
     static_assert(SCN <= 2 * kBwdHeads * 64, "one staged score per thread");
     const int stage_bytes = (int)S::bytes(WID) + SCN * 4;
     f16x8* wfr = reinterpret_cast<f16x8*>(smem + 2 * stage_bytes);
@@ -207,8 +207,18 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     Producer<NPAD, SB, MAXI, MAXE> prod;
     const int col0 = hg * hpg * HD;  // WID columns from here are staged (zeros past D)
     // Forward scores of a batch, one float per thread (SCN <= blockDim.x): one register held
-    // across the slot loop, not four.
+    // across the slot loop, not four.  The thread's (head, step) is the same in every batch,
+    // so its LSE is read once, and the staged value is the probability p = 2^(s2 - lse2):
+    // one exp per (step, slot, head) here instead of one in each of the 16 lanes (dims) of
+    // a row that needs it; the same operation on the same operands as in the lanes.
     float s2pre = 0.f;
+    float lse2s = INFINITY;
+    if (HAS_S && (int)threadIdx.x < SCN) {
+        const int hh = (threadIdx.x / kTB) % kBwdHeads;
+        const int t = t0 + threadIdx.x % kTB;
+        const int hs = SUB ? hg * (hpg >> 1) + (hh >> 1) : hg * hpg + hh;
+        if (t < a.L && hh < hpg) lse2s = a.LSEin[((int64_t)b * a.H + hs) * a.L + t] * kLog2e;
+    }
     auto load_scores = [&](int batch) {
         if (!HAS_S || (int)threadIdx.x >= SCN) return;
         const int j = threadIdx.x / (kBwdHeads * kTB);
@@ -221,7 +231,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                     : 0.f;
     };
     auto store_scores = [&](float* dst) {
-        if (HAS_S && (int)threadIdx.x < SCN) dst[threadIdx.x] = s2pre;
+        if (HAS_S && (int)threadIdx.x < SCN) dst[threadIdx.x] = __builtin_amdgcn_exp2f(s2pre - lse2s);
     };
     if (nb > 0) {
         flash_batch_meta<SB>(a, b, 0, kend, win, meta_of(0));
@@ -254,7 +264,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                 if (XH) __syncthreads();
                 continue;
             }
-            // Forward scores of this lane's 4 steps, staged in LDS with the batch.
+            // Probabilities of this lane's 4 steps, staged in LDS with the batch.
             f32x4 s2v = {0.f, 0.f, 0.f, 0.f};
             if (HAS_S)
                 s2v = *reinterpret_cast<const f32x4*>(S2_of(cur) + (j * kBwdHeads + hl) * kTB + 16 * th + 4 * g);
@@ -341,9 +351,8 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             float p[4], ds[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s2 = HAS_S ? s2v[i] : s[i];  // score * log2 e
-                const float dpt = dp[i] * kLn2;         // dO . v
-                p[i] = __builtin_amdgcn_exp2f(s2 - lse2[i]);
+                const float dpt = dp[i] * kLn2;  // dO . v
+                p[i] = HAS_S ? s2v[i] : __builtin_amdgcn_exp2f(s[i] - lse2[i]);  // s: score * log2 e
                 ds[i] = p[i] * (dpt - Dv[i]);
             }
             // Phase 2: gradients.  With xq = ds q, yd = p dO:
