@@ -419,7 +419,10 @@ def run_model(args):
     if args.fold_query_gating:  # queries inside the attention kernel (off by default)
         for layer in model.layers:
             layer.attn.fold_query_gating = True
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
+    # train.py:245-253: AdamW with weight decay 0.01 and a linear warmup over the first 200
+    # steps (the cosine decay after it is never reached by a benchmark run)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=0.01)
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda s: s / 200 if s < 200 else 1.0)
     x, uniq, cb, tgt = (d[k].to(dev) for k in ("x", "unique", "c_base", "targets"))
     pm = uniq >= 0
 
@@ -431,6 +434,7 @@ def run_model(args):
         loss.backward()
         torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
         opt.step()
+        sched.step()
         return loss
 
     for _ in range(args.warmup):
