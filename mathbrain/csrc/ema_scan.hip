@@ -715,6 +715,24 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int nw = blockDim.x >> 6;
+    constexpr int SPW = kBoundSlots / (kBoundThreads / 64);  // slots per wave
+    static_assert(kBoundSlots % (kBoundThreads / 64) == 0, "whole slots per wave");
+
+    // The wave's slot ids and initial states first: vector-memory waits count loads and
+    // stores in one in-order counter, so a slot's loads issued after the previous slot's
+    // stores would wait for those stores too.
+    int64_t uu[SPW];
+    float ci[SPW][RPL];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+        const int k = k0 + wave + s * (kBoundThreads / 64);
+        uu[s] = k < K ? unique[(int64_t)b * K + k] : (int64_t)-1;
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) {
+            const int n = lane + 64 * r;
+            ci[s][r] = (c_init && k < K && n < N) ? c_init[((int64_t)b * K + k) * cis + n] : 0.f;
+        }
+    }
 
     for (int i = threadIdx.x; i < L; i += blockDim.x) tok[i] = x[(int64_t)b * sb + (int64_t)i * sl];
     // bit p: the document changes at step p (doc[p] != doc[p - 1], p >= 1)
@@ -737,22 +755,20 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
     __syncthreads();
 
     const int64_t cstride = (int64_t)K * Np;
-    for (int kk = wave; kk < kBoundSlots; kk += nw) {
-        const int k = k0 + kk;
-        if (k >= K) break;
-        const int64_t u = unique[(int64_t)b * K + k];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+        const int k = k0 + wave + s * (kBoundThreads / 64);
+        if (k >= K) continue;  // (uniform; keeps the loop unrolled and uu, ci in registers)
+        const int64_t u = uu[s];
         float c[RPL];
 #pragma unroll
-        for (int r = 0; r < RPL; ++r) {
-            const int n = lane + 64 * r;
-            c[r] = (c_init && n < N) ? c_init[((int64_t)b * K + k) * cis + n] : 0.f;
-        }
+        for (int r = 0; r < RPL; ++r) c[r] = ci[s][r];
         float* o = out + ((int64_t)b * nc * K + k) * Np;
         auto store = [&](float* dst) {
 #pragma unroll
             for (int r = 0; r < RPL; ++r) {
                 const int n = lane + 64 * r;
-                if (n < Np) st_stream(dst + n, n < N ? c[r] : 0.f);
+                if (n < Np) dst[n] = n < N ? c[r] : 0.f;
             }
         };
         store(o);
