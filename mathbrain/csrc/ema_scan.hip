@@ -752,52 +752,75 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
         const int n = lane + 64 * r;
         if (n < N) log2_split(rhos[n], hi[r], lo[r]);
     }
+    float p64[RPL];  // rho^64, the decay over a whole piece
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) p64[r] = pow_steps(hi[r], lo[r], 64);
     __syncthreads();
 
     const int64_t cstride = (int64_t)K * Np;
+    // Chunk-outer, slot-inner: the wave advances its SPW slots (independent chains) by one
+    // chunk at a time, so the workgroup writes chunk j's 32 consecutive rows together and
+    // one token read per piece serves all SPW slots.  Each slot's state sees the same
+    // operations in the same order as a slot walked alone.
+    float c[SPW][RPL];
+    float* o[SPW];
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
         const int k = k0 + wave + s * (kBoundThreads / 64);
-        if (k >= K) continue;  // (uniform; keeps the loop unrolled and uu, ci in registers)
-        const int64_t u = uu[s];
-        float c[RPL];
+        o[s] = k < K ? out + ((int64_t)b * nc * K + k) * Np : nullptr;
 #pragma unroll
-        for (int r = 0; r < RPL; ++r) c[r] = ci[s][r];
-        float* o = out + ((int64_t)b * nc * K + k) * Np;
-        auto store = [&](float* dst) {
+        for (int r = 0; r < RPL; ++r) c[s][r] = ci[s][r];
+    }
+    auto store = [&](int s, int64_t off) {
+        if (!o[s]) return;  // (uniform: a slot past K)
 #pragma unroll
-            for (int r = 0; r < RPL; ++r) {
-                const int n = lane + 64 * r;
-                if (n < Np) dst[n] = n < N ? c[r] : 0.f;
-            }
-        };
-        store(o);
-        for (int j = 1; j < nc; ++j) {
-            for (int ps = (j - 1) * Br; ps < j * Br; ps += 64) {
-                const int len = min(64, j * Br - ps);
-                const bool hit = lane < len && u >= 0 && tok[ps + lane] == u;
-                uint64_t m = __ballot(hit);
-                bool drop = false;
-                if (doc_ids) {
-                    uint64_t rb = bits64_at(rbits, ps);
-                    if (len < 64) rb &= (1ull << len) - 1;
-                    if (rb) {
-                        const int rl = 63 - __builtin_clzll(rb);  // last change in the piece
-                        drop = true;
-                        m &= ~((1ull << rl) - 1);
-                    }
+        for (int r = 0; r < RPL; ++r) {
+            const int n = lane + 64 * r;
+            if (n < Np) o[s][off + n] = n < N ? c[s][r] : 0.f;
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) store(s, 0);
+    // Pieces run back to back (the next starts at ps + len); each piece's tokens are read
+    // one piece ahead, so the LDS read is not on the chain of state updates.
+    const int pend = (nc - 1) * Br;
+    int64_t tnext = (pend > 0 && lane < L) ? tok[lane] : (int64_t)-1;
+    for (int j = 1; j < nc; ++j) {
+        for (int ps = (j - 1) * Br; ps < j * Br; ps += 64) {
+            const int len = min(64, j * Br - ps);
+            const int64_t tv = tnext;
+            const int pn = ps + len;
+            tnext = (pn < pend && pn + lane < L) ? tok[pn + lane] : (int64_t)-1;
+            bool drop = false;
+            uint64_t keep = ~0ull;
+            if (doc_ids) {
+                uint64_t rb = bits64_at(rbits, ps);
+                if (len < 64) rb &= (1ull << len) - 1;
+                if (rb) {
+                    const int rl = 63 - __builtin_clzll(rb);  // last change in the piece
+                    drop = true;
+                    keep = ~((1ull << rl) - 1);
                 }
+            }
+            float pw[RPL];
 #pragma unroll
-                for (int r = 0; r < RPL; ++r) c[r] = drop ? 0.f : c[r] * pow_steps(hi[r], lo[r], len);
+            for (int r = 0; r < RPL; ++r) pw[r] = len == 64 ? p64[r] : pow_steps(hi[r], lo[r], len);
+#pragma unroll
+            for (int s = 0; s < SPW; ++s) {
+                const bool hit = lane < len && uu[s] >= 0 && tv == uu[s];
+                uint64_t m = __ballot(hit) & keep;
+#pragma unroll
+                for (int r = 0; r < RPL; ++r) c[s][r] = drop ? 0.f : c[s][r] * pw[r];
                 while (m) {  // uniform across the wave
                     const int p = __builtin_ctzll(m);
                     m &= m - 1;
 #pragma unroll
-                    for (int r = 0; r < RPL; ++r) c[r] += pow_steps(hi[r], lo[r], len - 1 - p);
+                    for (int r = 0; r < RPL; ++r) c[s][r] += pow_steps(hi[r], lo[r], len - 1 - p);
                 }
             }
-            store(o + j * cstride);
         }
+#pragma unroll
+        for (int s = 0; s < SPW; ++s) store(s, j * cstride);
     }
 }
 
