@@ -685,10 +685,13 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
 //   C <- C rho^len + sum_{p in mask} rho^(len - 1 - p)
 // (an occurrence adds 1 after its step's decay: triton_flash_ema.py:56-78).  A document
 // change at r zeroes the state before step r (:69-75): the piece drops the carried state
-// and the occurrences before its last change.  No sort is needed.
+// and the occurrences before its last change.  No sort is needed.  A wave advances its
+// eight slots together, chunk by chunk, so the workgroup writes each chunk's 64
+// consecutive state rows (16 KB) at about the same time (measured at configuration 2:
+// 32 slots per workgroup 48.2 us, 64 slots 39.9 us, 128 slots 42.5 us).
 
 constexpr int kBoundThreads = 512;
-constexpr int kBoundSlots = 32;
+constexpr int kBoundSlots = 64;
 
 // 64 bits of the bitmask `bits` starting at bit `pos` (bits beyond the array read as 0:
 // the array carries one spare word).
