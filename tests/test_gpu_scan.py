@@ -288,6 +288,26 @@ def test_gpu_boundary_doc_ids_and_padded_c_init():
     _close(got.cpu().numpy()[..., :N], want, 2e-5)
 
 
+@pytest.mark.parametrize("N,Br", [(100, 48), (200, 150), (128, 64), (33, 200)])
+def test_gpu_boundary_wide_rates_ragged_slots(N, Br):
+    """Two and four rates per lane, pieces shorter than 64 steps and chunks of several
+    pieces, document resets, and a slot count that leaves part of the last 64-slot
+    workgroup without slots."""
+    from mathbrain.triton_flash_ema import precompute_boundaries
+    rng = np.random.default_rng(N + Br)
+    B, L, V, K = 2, 300, 90, 70
+    x = rng.integers(0, V, size=(B, L))
+    doc = np.sort(rng.integers(0, 3, size=(B, L)), axis=1)
+    unique = np.stack([rng.permutation(V)[:K] for _ in range(B)])
+    unique[1, -9:] = -1
+    rhos = np.exp(-np.log(2.0) / np.logspace(0, 3, N)).astype(np.float32)
+    c_init = (rng.random((B, K, N)) * 3).astype(np.float32)
+    got = precompute_boundaries(_dev(x), _dev(unique), _dev(rhos), Br, _dev(c_init), _dev(doc)).cpu().numpy()
+    want = oscan.boundary_states(x, unique, rhos, Br, c_init, doc)
+    assert np.all(got[..., N:] == 0)
+    _close(got[..., :N], want, 2e-5)
+
+
 def test_gpu_boundary_cfg2_zipf():
     from mathbrain.triton_flash_ema import precompute_boundaries
     from mathbrain.synthetic import make_batch
