@@ -58,6 +58,14 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes per backward (its flash_ema_bwd_kernel dispatches), from the rocprofv3
 # FETCH_SIZE and WRITE_SIZE passes scaled by a 1 GiB copy (profiles/flash_ema_cfg2.md,
 # profiles/flash_ema_cfg4.md); re-measured whenever the kernel changes.
+# the attention's arithmetic per --precision (the default splits the gate operands where
+# N <= 64 and head_dim <= 64, and takes single fp16 operands beyond)
+GATE_DTYPES = {
+    "bf16": "fp16 hi+lo split gate MFMA (3 products), bf16 dW_pe MFMA, fp32 state/softmax/accumulate",
+    "fp16": "fp16 gate MFMA (1 product), bf16 dW_pe MFMA, fp32 state/softmax/accumulate",
+    "fp32": "fp32 mode: fp16 hi+lo gate MFMA (bf16 hi+lo dW_pe MFMA), fp32 state/softmax/accumulate",
+}
+
 TRAFFIC_BYTES = {
     "cfg2": 14705.3e6,
     "cfg4": 50700.7e6,
@@ -243,9 +251,7 @@ def run_attention(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("fp16 gate MFMA (bf16 dW_pe MFMA), fp32 state/softmax/accumulate"
-                  if args.precision == "bf16" else
-                  "fp32 mode: fp16 hi+lo gate MFMA (bf16 hi+lo dW_pe MFMA), fp32 state/softmax/accumulate"),
+        "dtype": GATE_DTYPES[args.precision] if N <= 64 or args.precision != "bf16" else GATE_DTYPES["fp16"],
         "data": "synthetic Zipf(1.1) tokens, seeded; random N(0,0.02) weights",
         "config": {"workload": workload,
                    "B": c["B"], "T": L, "d_model": D, "heads": c["H"], "head_dim": c["hd"],
@@ -453,8 +459,7 @@ def run_model(args):
             "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None,
-            "dtype": ("bf16 autocast (attention fp32 state, fp16 gate MFMA)" if args.precision == "bf16"
-                      else "bf16 autocast (attention fp32 mode: fp16 hi+lo gate MFMA)"),
+            "dtype": "bf16 autocast; attention: " + GATE_DTYPES[args.precision],
             "data": "synthetic lognormal(median 1500) Zipf(1.1) documents, chunked, random init",
             "config": {"workload": "cfg5 full training step", "layers": n_layers, "d_model": D,
                        "heads": H, "N": N, "V": V, "B": B, "T": T, "params": n_params,
@@ -778,9 +783,10 @@ def main():
                                            "corpus", "batch", "factored"),
                     default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--precision", choices=("bf16", "fp32"), default="bf16",
-                    help="attention gate operands: fp16 (bf16 mode, the default) or fp16 hi + lo "
-                         "pairs (fp32 mode); attention, cfg4 and model workloads")
+    ap.add_argument("--precision", choices=("bf16", "fp16", "fp32"), default="bf16",
+                    help="attention gate arithmetic (triton_flash_ema.PRECISIONS): split fp16 hi + lo "
+                         "gate operands (bf16, the default), single fp16 operands (fp16), or the split "
+                         "gate and a split dW_pe product (fp32); attention, cfg4 and model workloads")
     ap.add_argument("--no-secondary", action="store_true",
                     help="default workload: skip the secondary measurements (cfg3 scan, gating, cfg4, "
                          "cfg5 training step) that follow the headline one in the same run")

@@ -114,8 +114,11 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
                                   the slot's token id instead of [B, K, H*hd] gathered rows */
 #define MB_FLASH_FP32 8        /* fp32 mode: the gate GEMM takes fp16 hi + lo operand pairs (three
                                   products, ~2^-22 relative) and the dW_pe product bf16 hi + lo
-                                  pairs (~2^-16); otherwise fp16 gate and bf16 dW_pe operands.
-                                  Needs N <= 64. */
+                                  pairs (~2^-16).  Needs N <= 64 and hd <= 64. */
+#define MB_FLASH_FAST_GATE 16  /* the gate GEMM takes single fp16 operands (one product, 2^-11
+                                  relative each): faster, and accurate only while the scores
+                                  stay small enough that the softmax does not amplify that
+                                  rounding (see the forward's comment) */
 
 /*
  * Flash-EMA gated cross-attention forward.  Replaces flash_ema_forward and its kernel
@@ -156,9 +159,16 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
  *             on 256 CUs).  Without it (or when smaller) the launch runs unsplit; O and LSE
  *             agree either way up to the order of the softmax sums.
  *
- * The gate operands are fp16: c_dec (chunk-start states above 65440 saturate there;
- * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to
- * ~45,000 steps) and W_pe * log2(e), with fp32 accumulation.
+ * Gate arithmetic.  By default (N <= 64 and hd <= 64) the gate GEMM splits both operands,
+ * c_dec and W_pe * log2(e), into fp16 hi + lo pairs and takes three products (W_lo c_hi +
+ * W_hi c_lo + W_hi c_hi) with fp32 accumulation, ~2^-22 relative: where scores reach
+ * ~100 (a model's own initialisation can do that) the softmax turns a relative gate error
+ * e into ~100 e of the weights, and single fp16 operands (2^-11) moved a 6-layer model's
+ * logits by 2e-2 and its gradients by 0.1 from the exact model.  With MB_FLASH_FAST_GATE,
+ * and by default for N > 64 or hd 128 (where the lo tiles do not fit in LDS), the gate
+ * takes single fp16 operands.  The fp16 counters are clamped to 65440 at the chunk start;
+ * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to ~45,000
+ * steps, which the Python entry points check (faster rates are refused there).
  *
  * Supported: hd in {32, 64, 128} (32 or 64 with MB_FLASH_FP32), 1 <= H <= 64, N <= 128 (N <= 64
  * with MB_FLASH_FP32), Br <= 32 or Br == 64.  At hd 128 each head takes two waves, one per
@@ -195,8 +205,9 @@ int64_t mb_flash_ema_fwd_workspace(int B, int H, int L, int hd, int K, int N, in
  * dQ is written once per element.  dE_k, dE_v and dW_pe are cleared by the call (with a
  * fill kernel, no memset) and then accumulated with fp32 atomics, so their summation
  * order is not fixed, as in the reference's tl.atomic_add.  The gate is recomputed as
- * in the forward; the dW_pe product takes bf16 c_dec and bf16 dpre (as the reference's
- * triton_flash_ema.py:463-465 does) with fp32 accumulation.  Supported: as
+ * in the forward (the same arithmetic for the same flags); the dW_pe product takes bf16
+ * c_dec and bf16 dpre (as the reference's triton_flash_ema.py:463-465 does), or with
+ * MB_FLASH_FP32 bf16 hi + lo pairs of both, with fp32 accumulation.  Supported: as
  * mb_flash_ema_fwd.  At hd 128 each head runs as two 64-dim halves on two waves that add
  * their score and dO . v partial sums through LDS.
  */

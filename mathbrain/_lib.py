@@ -67,6 +67,7 @@ MB_FLASH_SILU = 1
 MB_FLASH_ABSENT_MASS = 2
 MB_FLASH_VOCAB_ROWS = 4
 MB_FLASH_FP32 = 8
+MB_FLASH_FAST_GATE = 16
 MB_DTYPE_F32 = 0
 MB_DTYPE_BF16 = 1
 

@@ -48,15 +48,16 @@ static int zero_fill(float* p, int64_t n, hipStream_t st) {
 // a wave holds, so the two half-waves of a head swap their dpre tiles through LDS and each
 // multiplies all 32 steps into its own half of the tiles [NTW th, NTW th + NTW).
 // VR: E_k / E_v and dE_k / dE_v are vocabulary tables indexed by the slot's token id.
-// PREC (MB_FLASH_FP32): the gate GEMM takes fp16 hi + lo operand pairs (W_lo c_hi + W_hi
-// c_lo + W_hi c_hi) and the dW_pe product bf16 hi + lo pairs (dpre_lo c_hi + dpre_hi c_lo
-// + dpre_hi c_hi), both with fp32 accumulation; the producer writes the lo tiles beside
-// the hi ones and W_lo's fragments sit beside W_hi's in LDS.
+// PG (the default mode's split gate, and the fp32 mode's): the gate GEMM takes fp16 hi + lo
+// operand pairs (W_lo c_hi + W_hi c_lo + W_hi c_hi, fp32 accumulation); the producer writes
+// the lo tile beside the hi one and W_lo's fragments sit beside W_hi's in LDS.
+// PW (MB_FLASH_FP32, with PG): the dW_pe product takes bf16 hi + lo pairs too (dpre_lo c_hi +
+// dpre_hi c_lo + dpre_hi c_hi); without PW it takes bf16 c_dec and bf16 dpre.
 // SUB (head_dim 128 = 2 HD): a wave takes one 64-dim half ("sub-head") of a head, waves hl
 // and hl ^ 1 the two halves of one; everything is per dim except the score and dO . v sums
 // (and D = dO . O), which the pair adds through LDS: one barrier per slot.
 template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool HAS_S, int NTW, bool XH, bool VR,
-          bool PREC = false, bool SUB = false>
+          bool PG = false, bool PW = false, bool SUB = false>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     constexpr int NPAD = 32 * NS;
@@ -66,12 +67,13 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     // (TT) when more than one slot shares a batch or when every wave reads both halves' steps
     // (XH); otherwise the copy costs more on the producer's critical path than the per-wave
     // fp16 -> bf16 conversion it saves (measured), and the waves convert instead.
-    constexpr bool TT = SB > 1 || XH || PREC;
+    constexpr bool TT = SB > 1 || XH || PG;
     static_assert(!XH || SB == 1, "the dpre exchange buffer is reused slot after slot");
-    static_assert(!(XH && PREC), "the fp32 mode takes N <= 64");
-    static_assert(!(SUB && PREC), "head_dim 128: default mode only");
+    static_assert(!(XH && PG), "the split gate takes N <= 64");
+    static_assert(!(SUB && PG), "the split gate takes head_dim <= 64");
+    static_assert(!PW || PG, "the split dW_pe product comes with the split gate");
     constexpr int HDR = SUB ? 2 * HD : HD;  // the head's dims
-    using S = Stage<NPAD, SB, TT, PREC>;
+    using S = Stage<NPAD, SB, TT, PG, PW>;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int D = a.H * HDR;
@@ -89,8 +91,8 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
     static_assert(SCN <= 2 * kBwdHeads * 64, "one staged score per thread");
     const int stage_bytes = (int)S::bytes(WID) + SCN * 4;
     f16x8* wfr = reinterpret_cast<f16x8*>(smem + 2 * stage_bytes);
-    f16x8* wfl = wfr + kBwdHeads * DT * NS * 64;  // PREC: the W_lo fragments
-    BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + (PREC ? 2 : 1) * kBwdHeads * DT * NS * 64);
+    f16x8* wfl = wfr + kBwdHeads * DT * NS * 64;  // PG: the W_lo fragments
+    BatchMeta* metas = reinterpret_cast<BatchMeta*>(wfr + (PG ? 2 : 1) * kBwdHeads * DT * NS * 64);
     int64_t* win = reinterpret_cast<int64_t*>(metas + kMetaRing * SB);
     float* powt = reinterpret_cast<float*>(win + kMaxWin);
     int* kinfo = reinterpret_cast<int*>(powt + 65 * NPAD);
@@ -161,12 +163,12 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         for (int e = 0; e < 8; ++e) {
             const int n = 32 * ns + 8 * (ln >> 4) + e;
             float ws = n < a.N ? w[e] * kLog2e : 0.f;
-            if (PREC) asm volatile("" : "+v"(ws));  // hi and lo of one float32 product
+            if (PG) asm volatile("" : "+v"(ws));  // hi and lo of one float32 product
             v[e] = (_Float16)ws;
             vl[e] = (_Float16)(ws - (float)v[e]);
         }
         wfr[f] = v;
-        if (PREC) wfl[f] = vl;
+        if (PG) wfl[f] = vl;
     }
     flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
     const int kend = kinfo[1];
@@ -240,7 +242,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         load_scores(0);
         __syncthreads();
         store_scores(S2_of(0));
-        prod.template store<TT, S::CROW, S::TROW, PREC, S::CDEC, S::CT>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0), E_of(0), WID);
+        prod.template store<TT, S::CROW, S::TROW, PG, PW, S::CDEC, S::CT>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0), E_of(0), WID);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         __syncthreads();
     }
@@ -280,7 +282,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                 ev[dt] = E[(j * 2 + 1) * WID + hl * HD + 16 * dt + c16];
             }
             f16x8 cfl[NS];
-            if (PREC) {
+            if (PG) {
 #pragma unroll
                 for (int ns = 0; ns < NS; ++ns)
                     cfl[ns] = *reinterpret_cast<const f16x8*>(crow + S::CDEC + c16 * S::CROW + 32 * ns + 8 * g);
@@ -289,7 +291,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 f32x4 accg = {0.f, 0.f, 0.f, 0.f};
-                if (PREC) {  // small terms first
+                if (PG) {  // small terms first
 #pragma unroll
                     for (int ns = 0; ns < NS; ++ns)
                         accg = mfma16x16x32(cf[ns], wfl[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
@@ -329,7 +331,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             }
             // The 16 lanes' sums (dims), both quantities' chains interleaved (the fp32 mode
             // keeps one chain after the other: interleaved, its larger live set spills).
-            if (!SUB && PREC) {
+            if (!SUB && PW) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     if (!HAS_S) s[i] = row_sum16(s[i]);
@@ -381,7 +383,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                     }
                     dvv[i] = av * dsil;
                 }
-                if (PREC) {  // bf16 hi + lo of each value
+                if (PW) {  // bf16 hi + lo of each value
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         dpre[dt][i] = (__bf16)dvv[i];
@@ -450,7 +452,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt) {
                     const bf16x4 cb4 = cop(th, nt);
-                    if (PREC) {  // small terms first; the lo tile sits S::CT entries after the hi one
+                    if (PW) {  // small terms first; the lo tile sits S::CT entries after the hi one
                         const __bf16* ccol = cdecT_of(cur) + S::CT + (j * NPAD + c16) * S::TROW + 16 * th + 4 * g;
                         const bf16x4 cl4 = *reinterpret_cast<const bf16x4*>(ccol + 16 * nt * S::TROW);
 #pragma unroll
@@ -465,7 +467,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             }
         }
         if (bi + 1 < nb) {
-            prod.template store<TT, S::CROW, S::TROW, PREC, S::CDEC, S::CT>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), cdecT_of(cur ^ 1),
+            prod.template store<TT, S::CROW, S::TROW, PG, PW, S::CDEC, S::CT>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), cdecT_of(cur ^ 1),
                                                 E_of(cur ^ 1), WID);
             store_scores(S2_of(cur ^ 1));
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
@@ -500,16 +502,16 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
 #undef meta_of
 }
 
-template <int HD, int NS, int SB, bool XH, bool PREC, bool SUB = false>
+template <int HD, int NS, int SB, bool XH, bool PG, bool PW, bool SUB = false>
 static size_t bwd_lds_bytes() {
     constexpr int WID = kBwdHeads * HD;
-    return 2 * (Stage<32 * NS, SB, (SB > 1 || XH || PREC), PREC>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
-           (size_t)(PREC ? 2 : 1) * kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
+    return 2 * (Stage<32 * NS, SB, (SB > 1 || XH || PG), PG, PW>::bytes(WID) + (size_t)SB * kBwdHeads * kTB * 4) +
+           (size_t)(PG ? 2 : 1) * kBwdHeads * (HD / 16) * NS * 64 * 16 + kMetaRing * SB * sizeof(BatchMeta) +
            kMaxWin * 8 + 65 * 32 * NS * 4 + 16 + (XH ? (size_t)kBwdHeads * 2 * (HD / 16) * 64 * 8 : 0) +
            (SUB ? (size_t)2 * kBwdHeads * 2 * 32 * 4 : 0);
 }
 
-template <int HD, int NS, int SB, bool PREC = false, bool SUB = false>
+template <int HD, int NS, int SB, bool PG = false, bool PW = false, bool SUB = false>
 static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     FlashArgsV a = a0;
     // heads per group: the largest divisor of H that is at most four (with SUB two heads,
@@ -529,16 +531,16 @@ static int launch_bwd(const FlashArgsV& a0, bool vr, hipStream_t st) {
     constexpr int NTW = NT < 256 / HD ? NT : 256 / HD;
     constexpr bool XH = NT > NTW;
     static_assert(NT == NTW || NT == 2 * NTW, "at most two half-waves per head");
-    const size_t lds = bwd_lds_bytes<HD, NS, SB, XH, PREC, SUB>();
+    const size_t lds = bwd_lds_bytes<HD, NS, SB, XH, PG, PW, SUB>();
     if (lds > 160 * 1024)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: hd=%d, N=%d needs %zu B of LDS", HD, a.N, lds);
     const int ntb = (a.L + kTB - 1) / kTB;
     dim3 grid(a.B * ntb * a.head_groups);
 #define MB_BWD_PICK(MI, ME, VR)                                                                  \
-    (a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH, VR, PREC, SUB>       \
-                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH, VR, PREC, SUB>)     \
-            : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH, VR, PREC, SUB>      \
-                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH, VR, PREC, SUB>))
+    (a.S2in ? (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, true, NTW, XH, VR, PG, PW, SUB>       \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, true, NTW, XH, VR, PG, PW, SUB>)     \
+            : (a.silu ? flash_ema_bwd_kernel<HD, NS, SB, MI, ME, true, false, NTW, XH, VR, PG, PW, SUB>      \
+                      : flash_ema_bwd_kernel<HD, NS, SB, MI, ME, false, false, NTW, XH, VR, PG, PW, SUB>))
     const FlashArgs& base = a;
 #define MB_BWD(MI, ME)                                                                            \
     do {                                                                                          \
@@ -604,17 +606,21 @@ extern "C" int mb_flash_ema_bwd(const float* Q, int64_t q_sb, int64_t q_sh, int6
                "mb_flash_ema_bwd: null pointer");
     MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_bwd: null slot pointer");
     const int NS = (N + 31) / 32;
-    if (flags & MB_FLASH_FP32) {
-        // hi + lo operand tiles and both W fragment sets in LDS: one slot per batch
-        if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
-        if (hd == 128) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_bwd: MB_FLASH_FP32 needs head_dim <= 64");
-        if (hd == 64) return NS == 1 ? launch_bwd<64, 1, 1, true>(a, vr, st) : launch_bwd<64, 2, 1, true>(a, vr, st);
-        return NS == 1 ? launch_bwd<32, 1, 1, true>(a, vr, st) : launch_bwd<32, 2, 1, true>(a, vr, st);
+    const int gm = flash_gate_mode("mb_flash_ema_bwd", flags, N, hd);
+    if (gm < 0) return gm;
+    if (gm == 2) {
+        // hi + lo tiles of both kinds and both W fragment sets in LDS: one slot per batch
+        if (hd == 64) return NS == 1 ? launch_bwd<64, 1, 1, true, true>(a, vr, st) : launch_bwd<64, 2, 1, true, true>(a, vr, st);
+        return NS == 1 ? launch_bwd<32, 1, 1, true, true>(a, vr, st) : launch_bwd<32, 2, 1, true, true>(a, vr, st);
+    }
+    if (gm == 1) {  // the gate's lo tile and W_lo beside the hi ones
+        if (hd == 64) return NS == 1 ? launch_bwd<64, 1, 4, true>(a, vr, st) : launch_bwd<64, 2, 2, true>(a, vr, st);
+        return NS == 1 ? launch_bwd<32, 1, 4, true>(a, vr, st) : launch_bwd<32, 2, 2, true>(a, vr, st);
     }
     if (hd == 128) {  // two 64-dim sub-heads per head
-        if (NS == 1) return launch_bwd<64, 1, 4, false, true>(a, vr, st);
-        if (NS == 2) return launch_bwd<64, 2, 4, false, true>(a, vr, st);
-        return launch_bwd<64, 4, 1, false, true>(a, vr, st);
+        if (NS == 1) return launch_bwd<64, 1, 4, false, false, true>(a, vr, st);
+        if (NS == 2) return launch_bwd<64, 2, 4, false, false, true>(a, vr, st);
+        return launch_bwd<64, 4, 1, false, false, true>(a, vr, st);
     }
     if (hd == 64) {
         if (NS == 1) return launch_bwd<64, 1, 4>(a, vr, st);

@@ -182,25 +182,42 @@ __device__ inline int xcd_major(int bid, int G) {
 
 // LDS carve-up of the per-batch staging buffers: cdec (fp16), with BF the transposed bf16
 // copy cdecT ([SB][NPAD][TROW], steps contiguous, for the backward's dW_pe product), then E.
-// With PR (the fp32 gate mode) each counter tile has a second, "lo" tile right after it:
-// cdec_lo = fp16(c - cdec) and cdecT_lo = bf16(c - cdecT), so that hi + lo carries the
-// counter to ~2^-22 (fp16 pair) or ~2^-16 (bf16 pair) relative.
-template <int NPAD, int SB, bool BF = false, bool PR = false>
+// With PG (the split gate) the cdec tile has a second, "lo" tile right after it,
+// cdec_lo = fp16(c - cdec), so that hi + lo carries the counter to ~2^-22 relative; with PW
+// (the split dW_pe product) the cdecT tile has one too, cdecT_lo = bf16(c - cdecT) (~2^-16).
+template <int NPAD, int SB, bool BF = false, bool PG = false, bool PW = false>
 struct Stage {
+    static_assert(!PW || (BF && PG), "the split dW_pe product comes with the split gate's tiles");
     static constexpr int CROW = NPAD + 8;  // 16-bit entries per cdec row (16 B pad against conflicts)
     static constexpr int CDEC = SB * kTB * CROW;  // entries per tile
-    static constexpr int NT = PR ? 2 : 1;         // tiles of each kind (hi, lo)
+    static constexpr int NTC = PG ? 2 : 1;        // cdec tiles (hi, lo)
+    static constexpr int NTT = PW ? 2 : 1;        // cdecT tiles (hi, lo)
     // cdecT row: kTB steps + 4 entries of padding, so that 16 rates x 4 step groups read by
     // one wave start on 64 distinct LDS banks
     static constexpr int TROW = kTB + 4;
     static constexpr int CT = BF ? SB * NPAD * TROW : 0;
-    static constexpr int CTOFF = NT * CDEC * 2;          // byte offset of cdecT
-    static constexpr int EOFF = (NT * CDEC + NT * CT) * 2;  // byte offset of E
+    static constexpr int CTOFF = NTC * CDEC * 2;             // byte offset of cdecT
+    static constexpr int EOFF = (NTC * CDEC + NTT * CT) * 2;  // byte offset of E
     // width: embedding columns staged per slot
     __host__ __device__ static size_t bytes(int width) {
         return (size_t)EOFF + (size_t)SB * 2 * width * 4;
     }
 };
+
+// Gate arithmetic of a flash-EMA call, the same in the forward and the backward:
+// 2 = MB_FLASH_FP32 (split gate and split dW_pe product), 1 = the default's split gate with
+// bf16 dW_pe operands, 0 = single fp16 gate products (MB_FLASH_FAST_GATE, and the default
+// where the lo tiles do not fit in LDS: N > 64 or head_dim 128).  Negative: MB_FLASH_FP32
+// with a shape it does not take (the error is set).
+static inline int flash_gate_mode(const char* who, int flags, int N, int hd) {
+    if (flags & MB_FLASH_FP32) {
+        if (N > 64) return fail(MB_ERR_UNSUPPORTED, "%s: MB_FLASH_FP32 needs N <= 64 (N=%d)", who, N);
+        if (hd > 64) return fail(MB_ERR_UNSUPPORTED, "%s: MB_FLASH_FP32 needs head_dim <= 64 (hd=%d)", who, hd);
+        return 2;
+    }
+    if (flags & MB_FLASH_FAST_GATE) return 0;
+    return N <= 64 && hd <= 64 ? 1 : 0;
+}
 
 // Row of slot (b, k), token id u, in E_k / E_v / dE_k / dE_v: b*K + k, or with VR
 // the token id (padding slots, -1, read row 0; ids are clamped to the table).  u comes from
@@ -333,9 +350,11 @@ struct Producer {
     }
 
     // Builds cdec ([SB][kTB][CROW], fp16), with BF also cdecT ([SB][NPAD][TROW], bf16), and E
-    // ([SB][2][width]) of the batch into the staging buffer.  With PR also the lo tiles,
-    // CLO entries after cdec and CTLO entries after cdecT (see Stage).
-    template <bool BF, int CROW, int TROW, bool PR = false, int CLO = 0, int CTLO = 0>
+    // ([SB][2][width]) of the batch into the staging buffer.  With PG also cdec's lo tile, CLO
+    // entries after cdec, and with PW cdecT's, CTLO entries after cdecT (see Stage).  With PG
+    // the bf16 copy rounds the float32 counter; without, the gate's fp16 counter (the gate and
+    // the dW_pe product then see one c_dec).
+    template <bool BF, int CROW, int TROW, bool PG = false, bool PW = false, int CLO = 0, int CTLO = 0>
     __device__ void store(int t0, int cb, const float* powt, const BatchMeta* meta,
                           _Float16* cdec, __bf16* cdecT, float* E, int width) {
         const int tid = threadIdx.x;
@@ -368,7 +387,7 @@ struct Producer {
                     c2 += q.z;
                     c3 += q.w;
                 }
-                if (PR) {
+                if (PG) {
                     // hi and lo come from one materialised float32 counter: a conversion the
                     // compiler fused with the last add would round hi from a different value
                     asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
@@ -379,7 +398,7 @@ struct Producer {
                 w[2] = (_Float16)c2;
                 w[3] = (_Float16)c3;
                 *reinterpret_cast<f16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
-                if (PR) {  // the fp16 rounding remainder
+                if (PG) {  // the fp16 rounding remainder
                     f16x4 wl;
                     wl[0] = (_Float16)(c0 - (float)w[0]);
                     wl[1] = (_Float16)(c1 - (float)w[1]);
@@ -387,13 +406,13 @@ struct Producer {
                     wl[3] = (_Float16)(c3 - (float)w[3]);
                     *reinterpret_cast<f16x4*>(cdec + CLO + (j * kTB + tl) * CROW + n0) = wl;
                 }
-                if (BF && PR) {  // bf16 hi + lo of the float32 counter
+                if (BF && PG) {  // bf16 (with PW hi + lo) of the float32 counter
                     const float cv[4] = {c0, c1, c2, c3};
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const __bf16 h = (__bf16)cv[q];
                         tb[q][r] = h;
-                        tl4[q][r] = (__bf16)(cv[q] - (float)h);
+                        if (PW) tl4[q][r] = (__bf16)(cv[q] - (float)h);
                     }
                 } else if (BF) {  // bf16 of the gate's fp16 counter (the gate and dW_pe see one c_dec)
                     tb[0][r] = (__bf16)(float)w[0];
@@ -406,7 +425,7 @@ struct Producer {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     *reinterpret_cast<bf16x4*>(cdecT + (j * NPAD + n0 + q) * TROW + 4 * tq) = tb[q];
-                    if (PR)
+                    if (PW)
                         *reinterpret_cast<bf16x4*>(cdecT + CTLO + (j * NPAD + n0 + q) * TROW + 4 * tq) = tl4[q];
                 }
             }

@@ -31,15 +31,16 @@ using namespace mb;
 static int fwd_dispatch(const FlashArgsV& a, int hd, int N, int flags, bool vr, hipStream_t st, float* part,
                         int64_t ws_bytes, int64_t* ws_need) {
     const int NS = (N + 31) / 32;
-    if (flags & MB_FLASH_FP32) {
-        // hi + lo operand tiles and the W_lo fragments in LDS: two slots per batch
-        if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
-        if (hd == 128) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: MB_FLASH_FP32 needs head_dim <= 64");
+    const int gm = flash_gate_mode("mb_flash_ema_fwd", flags, N, hd);
+    if (gm < 0) return gm;
+    if (gm > 0) {
+        // the split gate (both modes take it in the forward): hi + lo counter tiles and each
+        // wave's W_lo fragments in LDS; three slots per batch fill LDS at N = 64, head_dim 64
         if (hd == 64)
             return NS == 1 ? launch_fwd<64, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
-                           : launch_fwd<64, 2, 2, true>(a, vr, st, part, ws_bytes, ws_need);
+                           : launch_fwd<64, 2, 3, true>(a, vr, st, part, ws_bytes, ws_need);
         return NS == 1 ? launch_fwd<32, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
-                       : launch_fwd<32, 2, 2, true>(a, vr, st, part, ws_bytes, ws_need);
+                       : launch_fwd<32, 2, 4, true>(a, vr, st, part, ws_bytes, ws_need);
     }
     if (hd == 128) {  // two waves per head, one 16-step tile each
         if (NS == 1) return launch_fwd<128, 1, 4>(a, vr, st, part, ws_bytes, ws_need);

@@ -55,7 +55,7 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     constexpr int DT = HD / 16;
     constexpr int TW = HD > 64 ? 1 : 2;
     static_assert(TW == 2 || (!GQ && !PREC), "head_dim 128: default mode only");
-    using S = Stage<NPAD, SB, false, PREC>;
+    using S = Stage<NPAD, SB, false, PREC, false>;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int D = a.H * HD;
@@ -196,7 +196,7 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
         if (VR) __syncthreads();  // the load reads the batch's token ids
         prod.template load<VR>(a, b, cbi, bi0, kend, D, col0, WIDF, meta_of(bi0));
         __syncthreads();
-        prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(bi0), cdec_of(0), nullptr, E_of(0), WIDF);
+        prod.template store<false, S::CROW, S::TROW, PREC, false, S::CDEC>(t0, cb, powt, meta_of(bi0), cdec_of(0), nullptr, E_of(0), WIDF);
         if (bi0 + 1 < bi1) flash_batch_meta<SB>(a, b, bi0 + 1, kend, win, meta_of(bi0 + 1));
         __syncthreads();
     }
@@ -319,7 +319,7 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
             }
         }
         if (bi + 1 < bi1) {
-            prod.template store<false, S::CROW, S::TROW, PREC, S::CDEC>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
+            prod.template store<false, S::CROW, S::TROW, PREC, false, S::CDEC>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
                                               E_of(cur ^ 1), WIDF);
             if (bi + 2 < bi1) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
@@ -443,7 +443,7 @@ static int64_t fwd_part_bytes(int ks, int B, int H, int L, int hd) {
 // nfrag: W fragment sets in LDS (PREC: one W_lo set per wave; head_dim 128: one W set per head)
 template <int HD, int NS, int SB, bool PREC>
 static size_t fwd_lds_bytes(int width, int nfrag) {
-    return 2 * Stage<32 * NS, SB, false, PREC>::bytes(width) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
+    return 2 * Stage<32 * NS, SB, false, PREC, false>::bytes(width) + 3 * SB * sizeof(BatchMeta) + kMaxWin * 8 +
            65 * 32 * NS * 4 + 16 + (size_t)nfrag * (HD / 16) * NS * 64 * 16;
 }
 

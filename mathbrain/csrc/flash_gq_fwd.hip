@@ -62,8 +62,9 @@ extern "C" int mb_flash_ema_fwd_gq(const float* x_q, int64_t xq_sb, int64_t xq_s
     MB_REQUIRE(K == 0 || (E_k && E_v && C_bounds), "mb_flash_ema_fwd_gq: null slot pointer");
     hipStream_t st = (hipStream_t)stream;
     const int NS = (N + 31) / 32;
-    if (flags & MB_FLASH_FP32) {
-        if (NS > 2) return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd_gq: MB_FLASH_FP32 needs N <= 64 (N=%d)", N);
+    const int gm = flash_gate_mode("mb_flash_ema_fwd_gq", flags, N, hd);
+    if (gm < 0) return gm;
+    if (gm > 0) {
         if (hd == 64)
             return NS == 1 ? launch_fwd<64, 1, 4, true, true>(a, vr, st) : launch_fwd<64, 2, 2, true, true>(a, vr, st);
         return NS == 1 ? launch_fwd<32, 1, 4, true, true>(a, vr, st) : launch_fwd<32, 2, 2, true, true>(a, vr, st);

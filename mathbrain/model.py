@@ -18,7 +18,7 @@ import torch.nn.functional as F
 
 from .triton_ema_query import compute_query_ema_history
 from .triton_flash_ema import (FlashEMAFunction, GatedQueryFlashEMAFunction, _build_unique_index,
-                               precompute_boundaries)
+                               check_counter_range, precompute_boundaries)
 from .triton_fused_gating import fused_apply_symmetric_query_gating
 from .layernorm import layer_norm
 from .rmsnorm import rms_norm
@@ -76,7 +76,8 @@ class SlotAttentionLayer(nn.Module):
         # softmax over all V slots (the dense PyTorch reference) or over the valid slots only
         # (the reference's Triton kernel): see FlashEMAFunction
         self.absent_mass = absent_mass
-        # the attention's gate operands: fp16 ("bf16" mode) or fp16 hi + lo pairs ("fp32")
+        # the attention's gate arithmetic (triton_flash_ema.PRECISIONS): "bf16" (split fp16
+        # gate operands, bf16 dW_pe), "fp16" (single fp16 gate operands) or "fp32"
         self.precision = precision
         # True: compute the queries (gating, ln_q, q_proj) inside the attention kernel
         # (GatedQueryFlashEMAFunction) when the shapes allow it.  Off by default: measured at
@@ -173,6 +174,9 @@ class SlotTransformerLM(nn.Module):
         self.ema_dropout = ema_dropout
         half_lives = torch.logspace(math.log10(min_hl), math.log10(max_hl), self.n_scales)
         rhos = torch.exp(-torch.log(torch.tensor(2.0)) / half_lives)
+        # the attention's gate takes the key counters as fp16 operands: refuse half-lives
+        # whose counters could leave that range, here rather than at the first step
+        check_counter_range(rhos, "SlotTransformerLM")
         self.register_buffer("ema_rhos", rhos)
         self.embed = nn.Embedding(vocab_size, d_model)
         d_ff = 256 * ((int(8 * d_model / 3) + 255) // 256)

@@ -9,6 +9,9 @@ flash_ema_bwd) so that torch.compile traces through the attention instead of bre
 the graph at the ctypes call.
 """
 import functools
+import math
+import threading
+import weakref
 from typing import Optional
 
 import torch
@@ -108,18 +111,79 @@ def _build_unique_index(x, device, width=None):
     return ids[:, :K_max].contiguous().to(x.dtype), K_max
 
 
-PRECISIONS = ("bf16", "fp32")
+# The gate GEMM takes the decayed key counters as fp16 operands (both precision modes: the
+# fp32 mode splits them into fp16 hi + lo parts).  A slot's counter at a chunk start is an
+# EMA of at most one occurrence per step, so it never exceeds 1 / (1 - rho) when c_base is
+# itself such a count (as the data pipeline's states are), and a window adds at most 64
+# occurrences on top.  COUNTER_MAX is fp16's largest finite value less those 64; rates with
+# 1 / (1 - rho) above it (half-lives above MAX_HALF_LIFE steps: 1 / (1 - rho) is about
+# hl / ln 2 + 1/2) are refused, because their counters could leave the fp16 range.
+COUNTER_MAX = 65504.0 - 64
+MAX_HALF_LIFE = math.log(2.0) / -math.log1p(-1.0 / COUNTER_MAX)
+_rates_checked = {}  # id(tensor) -> (weak reference, version) of rate tensors found in range
+_rates_lock = threading.Lock()
 
 
-def _fp32(precision):
+def check_counter_range(rhos, what="flash-EMA attention"):
+    """Raises HipKernelError if a rate's counters can exceed the gate operands' fp16 range.
+
+    ``rhos``: a tensor (any device) or a sequence of floats.  The check reads the largest
+    rate once per tensor object and version (a device tensor is read back the first time
+    only), and is skipped while torch.compile traces or a CUDA graph is captured."""
+    if isinstance(rhos, torch.Tensor):
+        if torch.compiler.is_compiling():
+            return
+        if rhos.device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            return
+        with _rates_lock:
+            seen = _rates_checked.get(id(rhos))
+        if seen is not None and seen[0]() is rhos and seen[1] == rhos._version:
+            return
+        rho_max = float(rhos.detach().max()) if rhos.numel() else 0.0
+    else:
+        rho_max = max((float(r) for r in rhos), default=0.0)
+    if not rho_max < 1.0 or 1.0 / (1.0 - rho_max) > COUNTER_MAX:
+        hl = math.inf if not rho_max < 1.0 else math.log(2.0) / -math.log(rho_max)
+        raise _lib.HipKernelError(
+            f"{what}: the slowest EMA rate (rho = {rho_max!r}, half-life {hl:.6g} steps) lets the "
+            f"key counters reach 1/(1 - rho) = {1.0 / max(1.0 - rho_max, 1e-300):.6g}, above the "
+            f"{COUNTER_MAX:g} that the gate's fp16 operands hold; half-lives up to "
+            f"{MAX_HALF_LIFE:.0f} steps are supported")
+    if isinstance(rhos, torch.Tensor):
+        key = id(rhos)
+        with _rates_lock:
+            if key not in _rates_checked:
+                weakref.finalize(rhos, _forget_rates, key)
+            _rates_checked[key] = (weakref.ref(rhos), rhos._version)
+
+
+def _forget_rates(key):
+    with _rates_lock:
+        _rates_checked.pop(key, None)
+
+
+# Gate arithmetic of the attention kernels:
+#   "bf16" (default)  the gate GEMM splits c_dec and W_pe * log2 e into fp16 hi + lo pairs
+#                     (three products, ~2^-22 relative) where the kernels take it (N <= 64,
+#                     head_dim <= 64; single fp16 operands otherwise); dW_pe from bf16
+#                     operands, as the reference's kernel takes it;
+#   "fp16"            single fp16 gate operands (2^-11): faster, for models whose scores stay
+#                     small (the softmax multiplies a relative gate error by the score scale);
+#   "fp32"            the split gate and a split dW_pe product (bf16 hi + lo), everything else
+#                     fp32: north_star's 1e-4 mode (N <= 64, head_dim <= 64).
+PRECISIONS = ("bf16", "fp16", "fp32")
+
+
+def _prec(precision):
+    """The C ABI flag bits of a precision name."""
     if precision not in PRECISIONS:
         raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
-    return precision == "fp32"
+    return {"bf16": 0, "fp16": _lib.MB_FLASH_FAST_GATE, "fp32": _lib.MB_FLASH_FP32}[precision]
 
 
-def _flash_flags(use_silu, absent_mass, vocab_rows=False, fp32=False):
+def _flash_flags(use_silu, absent_mass, vocab_rows=False, prec=0):
     return ((_lib.MB_FLASH_SILU if use_silu else 0) | (_lib.MB_FLASH_ABSENT_MASS if absent_mass else 0)
-            | (_lib.MB_FLASH_VOCAB_ROWS if vocab_rows else 0) | (_lib.MB_FLASH_FP32 if fp32 else 0))
+            | (_lib.MB_FLASH_VOCAB_ROWS if vocab_rows else 0) | int(prec))
 
 
 def _slot_rows(E, B, K, D, V_total, what):
@@ -139,9 +203,10 @@ def _slot_rows(E, B, K, D, V_total, what):
 
 
 def _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br,
-              absent_mass, return_scores, fp32=False):
+              absent_mass, return_scores, prec=0):
     dev = _lib.require_gpu(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds,
                            what="flash_ema_forward")
+    check_counter_range(rhos, "flash_ema_forward")
     B, H, L, hd = Q.shape
     K = unique_tensor.shape[1]
     N = rhos.shape[0]
@@ -164,7 +229,7 @@ def _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_
     O = torch.empty(B, H, L, hd, dtype=torch.float32, device=dev)
     LSE = torch.empty(B, H, L, dtype=torch.float32, device=dev)
     S2 = torch.empty(B, H, K, L, dtype=torch.float32, device=dev) if return_scores else None
-    flags = _flash_flags(use_silu, absent_mass, table, fp32)
+    flags = _flash_flags(use_silu, absent_mass, table, prec)
     with torch.cuda.device(dev):
         nws = _fwd_workspace_bytes(B, H, L, hd, K, N, flags, dev.index)
         ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws > 0 else None
@@ -187,7 +252,7 @@ def _fwd_workspace_bytes(B, H, L, hd, K, N, flags, device_index):
 
 
 def _fwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br, absent_mass,
-              fp32):
+              prec):
     B, H, L, hd = Q.shape
     return Q.new_empty((B, H, L, hd), dtype=torch.float32), Q.new_empty((B, H, L), dtype=torch.float32)
 
@@ -196,11 +261,11 @@ def _fwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_
 def flash_ema_fwd(Q: torch.Tensor, x: torch.Tensor, E_k: torch.Tensor, E_v: torch.Tensor,
                   W_pe: torch.Tensor, rhos: torch.Tensor, unique_tensor: torch.Tensor,
                   C_bounds: torch.Tensor, V_total: int, use_silu: bool, Br: int,
-                  absent_mass: bool, fp32: bool) -> tuple[torch.Tensor, torch.Tensor]:
+                  absent_mass: bool, prec: int) -> tuple[torch.Tensor, torch.Tensor]:
     """(O, LSE) of flash_ema_forward (mb_flash_ema_fwd: one launch, and a merge launch when it
     splits the slots into parts)."""
     O, LSE = _fwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, V_total, use_silu, Br,
-                       absent_mass, False, fp32)[:2]
+                       absent_mass, False, prec)[:2]
     return O, LSE
 
 
@@ -224,33 +289,35 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
     kernel's softmax over the valid slots only (triton_flash_ema.py:215-229).  With
     ``return_scores`` a sixth element holds the scores * log2(e) as [B, H, K_max, L]
     (what ``flash_ema_backward(scores=...)`` consumes instead of recomputing them).
-    ``precision``: "bf16" (default) feeds the gate GEMM fp16 operands; "fp32" feeds it fp16
-    hi + lo pairs (three products, ~2^-22 relative, N <= 64), the mode to use where scores
-    are large enough that the softmax amplifies operand rounding.
+    ``precision``: the gate arithmetic (see PRECISIONS): "bf16" (default) splits the gate
+    operands into fp16 hi + lo pairs (N <= 64, head_dim <= 64; single fp16 operands
+    beyond), "fp16" takes single fp16 operands (faster; for small scores only), "fp32" also
+    splits the backward's dW_pe product.
     """
-    fp32 = _fp32(precision)
+    prec = _prec(precision)
     B, H, L, hd = Q.shape
     K = unique_tensor.shape[1]
     if K != K_max:
         raise ValueError(f"unique_tensor has {K} slots but K_max={K_max}")
     if not return_scores:
         O, LSE = flash_ema_fwd(Q, x, E_k_active, E_v_active, W_pe, rhos, unique_tensor, C_bounds,
-                               int(V_total), bool(use_silu), int(Br), bool(absent_mass), fp32)
+                               int(V_total), bool(use_silu), int(Br), bool(absent_mass), prec)
         Ek, Ev = E_k_active.to(torch.float32), E_v_active.to(torch.float32)
         if Ek.dim() == 2:
             return O, LSE, C_bounds, Ek, Ev
         return O, LSE, C_bounds, Ek.reshape(B, K, H, hd), Ev.reshape(B, K, H, hd)
     O, LSE, S2, Ek, Ev, table = _fwd_impl(Q, x, E_k_active, E_v_active, W_pe, rhos, unique_tensor,
-                                          C_bounds, V_total, use_silu, Br, absent_mass, True, fp32)
+                                          C_bounds, V_total, use_silu, Br, absent_mass, True, prec)
     if table:
         return O, LSE, C_bounds, Ek, Ev, S2
     return O, LSE, C_bounds, Ek.view(B, K, H, hd), Ev.view(B, K, H, hd), S2
 
 
 def _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total, use_silu,
-              Br, absent_mass, scores, fp32=False):
+              Br, absent_mass, scores, prec=0):
     dev = _lib.require_gpu(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO,
                            what="flash_ema_backward")
+    check_counter_range(rhos, "flash_ema_backward")
     B, H, L, hd = Q.shape
     K = unique_tensor.shape[1]
     N = rhos.shape[0]
@@ -283,13 +350,13 @@ def _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V
                   xl.stride(0), xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W),
                   _lib.ptr(rh), _lib.ptr(uniq), _lib.ptr(Cb), _lib.ptr(Of), _lib.ptr(Lf), B, H, L,
                   hd, K, N, Cb.shape[3], Cb.shape[1], int(Br), int(V_total),
-                  _flash_flags(use_silu, absent_mass, table, fp32), _lib.ptr(scores), _lib.ptr(dQ),
+                  _flash_flags(use_silu, absent_mass, table, prec), _lib.ptr(scores), _lib.ptr(dQ),
                   _lib.ptr(dEk), _lib.ptr(dEv), _lib.ptr(dW), _lib.stream(dev))
     return dQ, dEk, dEv, dW
 
 
 def _bwd_fake(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total, use_silu,
-              Br, absent_mass, fp32):
+              Br, absent_mass, prec):
     B, H, L, hd = Q.shape
     D = H * hd
     rows = (E_k.shape[0], D) if E_k.dim() == 2 else (B, unique_tensor.shape[1], D)
@@ -303,10 +370,10 @@ def flash_ema_bwd(Q: torch.Tensor, x: torch.Tensor, E_k: torch.Tensor, E_v: torc
                   W_pe: torch.Tensor, rhos: torch.Tensor, unique_tensor: torch.Tensor,
                   C_bounds: torch.Tensor, O: torch.Tensor, LSE: torch.Tensor, dO: torch.Tensor,
                   V_total: int, use_silu: bool, Br: int, absent_mass: bool,
-                  fp32: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+                  prec: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dQ, dE_k, dE_v, dW_pe) of flash_ema_backward (fills and one mb_flash_ema_bwd launch)."""
     return _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total,
-                     use_silu, Br, absent_mass, None, fp32)
+                     use_silu, Br, absent_mass, None, prec)
 
 
 def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bounds, O, LSE, dO,
@@ -320,27 +387,77 @@ def flash_ema_backward(Q, x, E_k, E_v, W_pe, rhos, V_total, unique_tensor, C_bou
     ``precision`` as in flash_ema_forward ("fp32" also takes the dW_pe product from bf16
     hi + lo pairs of both operands).
     """
-    fp32 = _fp32(precision)
+    prec = _prec(precision)
     if scores is None:
         return flash_ema_bwd(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO,
-                             int(V_total), bool(use_silu), int(Br), bool(absent_mass), fp32)
+                             int(V_total), bool(use_silu), int(Br), bool(absent_mass), prec)
     return _bwd_impl(Q, x, E_k, E_v, W_pe, rhos, unique_tensor, C_bounds, O, LSE, dO, V_total,
-                     use_silu, Br, absent_mass, scores, fp32)
+                     use_silu, Br, absent_mass, scores, prec)
 
 
 # With SAVE_SCORES, FlashEMAFunction keeps the forward's scores ([B, H, K_max, L] fp32,
-# 1.5 GB at B=56, T=512, H=8, K_max=1638) when they take at most SAVE_SCORES_MAX_BYTES, and
-# the backward reads them instead of recomputing them: configuration 2 measured forward
-# 9.09 -> 9.45 ms (writing them) and backward 22.49 -> 21.05 ms (no score products and half
-# the cross-lane sums), 31.6 -> 30.5 ms per layer.  Traced graphs never save them.
+# 1.5 GB at B=56, T=512, H=8, K_max=1638) and the backward reads them instead of recomputing
+# them: configuration 2 measured forward 9.09 -> 9.45 ms (writing them) and backward 22.49 ->
+# 21.05 ms (no score products and half the cross-lane sums), 31.6 -> 30.5 ms per layer.
+# SAVE_SCORES_MAX_BYTES is a budget per device shared by every saved score tensor still
+# alive (a model's layers each keep theirs until the backward reaches them): a call whose
+# scores would take the held total past it recomputes them in the backward instead.  A
+# saved tensor returns its bytes when it is freed (after the backward, or when the graph is
+# dropped).  Traced graphs never save them.
 SAVE_SCORES = True
 SAVE_SCORES_MAX_BYTES = 16 << 30
 
 
+class ScoreBudget:
+    """Bytes of saved score tensors held per device, against a shared limit."""
+
+    def __init__(self):
+        self._held = {}
+        self._lock = threading.Lock()
+
+    def held(self, device):
+        with self._lock:
+            return self._held.get(str(device), 0)
+
+    def reserve(self, device, nbytes, limit):
+        """Takes ``nbytes`` for ``device`` if the total stays within ``limit``; returns whether
+        it did."""
+        key = str(device)
+        with self._lock:
+            held = self._held.get(key, 0)
+            if held + nbytes > limit:
+                return False
+            self._held[key] = held + nbytes
+            return True
+
+    def release(self, device, nbytes):
+        key = str(device)
+        with self._lock:
+            self._held[key] = max(self._held.get(key, 0) - nbytes, 0)
+
+    def hold(self, tensor, nbytes):
+        """Returns ``nbytes`` reserved for ``tensor``'s device when ``tensor`` is freed."""
+        weakref.finalize(tensor, self.release, tensor.device, nbytes)
+
+
+score_budget = ScoreBudget()
+
+
 def keep_scores(B, H, K_max, L):
-    """Whether FlashEMAFunction keeps the forward's scores for a call of this shape."""
+    """Whether FlashEMAFunction would keep the forward's scores for a call of this shape with
+    nothing else held (the budget check of a real call also counts the scores already held)."""
     return (SAVE_SCORES and not torch.compiler.is_compiling()
             and 4 * int(B) * int(H) * int(K_max) * int(L) <= SAVE_SCORES_MAX_BYTES)
+
+
+def _reserve_scores(Q, K_max):
+    """Reserves the score bytes of this call in the shared budget; returns the byte count, or
+    0 when the scores are to be recomputed by the backward instead."""
+    B, H, L = Q.shape[0], Q.shape[1], Q.shape[2]
+    if not keep_scores(B, H, K_max, L):
+        return 0
+    nbytes = 4 * int(B) * int(H) * int(K_max) * int(L)
+    return nbytes if score_budget.reserve(Q.device, nbytes, SAVE_SCORES_MAX_BYTES) else 0
 
 
 class FlashEMAFunction(torch.autograd.Function):
@@ -357,10 +474,18 @@ class FlashEMAFunction(torch.autograd.Function):
     @torch.amp.custom_fwd(device_type="cuda", cast_inputs=torch.float32)
     def forward(ctx, Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, K_max,
                 C_bounds, use_silu=True, Br=64, absent_mass=True, precision="bf16"):
-        keep = keep_scores(Q.shape[0], Q.shape[1], unique_tensor.shape[1], Q.shape[2])
-        res = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
-                                K_max, C_bounds, use_silu, Br, absent_mass, return_scores=keep,
-                                precision=precision)
+        nbytes = _reserve_scores(Q, unique_tensor.shape[1])
+        keep = nbytes > 0
+        try:
+            res = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
+                                    K_max, C_bounds, use_silu, Br, absent_mass, return_scores=keep,
+                                    precision=precision)
+        except BaseException:
+            if keep:
+                score_budget.release(Q.device, nbytes)
+            raise
+        if keep:
+            score_budget.hold(res[5], nbytes)
         O, LSE, C_bounds, E_k, E_v = res[:5]
         ctx.save_for_backward(Q, x, E_k, E_v, W_pe, rhos, C_bounds, unique_tensor, O, LSE,
                               res[5] if keep else None)
@@ -414,7 +539,7 @@ def _rows_f32(t, width):
 
 
 def _fwd_gq_fake(x_q, C_seq, W_pe, ln_w, ln_b, W_q, eps, x, E_k, E_v, rhos, unique_tensor, C_bounds,
-                 V_total, n_heads, use_silu, Br, absent_mass, fp32):
+                 V_total, n_heads, use_silu, Br, absent_mass, prec):
     B, L, D = x_q.shape
     hd = D // n_heads
     return (x_q.new_empty((B, n_heads, L, hd), dtype=torch.float32),
@@ -426,11 +551,12 @@ def flash_ema_fwd_gq(x_q: torch.Tensor, C_seq: torch.Tensor, W_pe: torch.Tensor,
                      ln_b: torch.Tensor, W_q: torch.Tensor, eps: float, x: torch.Tensor, E_k: torch.Tensor,
                      E_v: torch.Tensor, rhos: torch.Tensor, unique_tensor: torch.Tensor,
                      C_bounds: torch.Tensor, V_total: int, n_heads: int, use_silu: bool, Br: int,
-                     absent_mass: bool, fp32: bool) -> tuple[torch.Tensor, torch.Tensor]:
+                     absent_mass: bool, prec: int) -> tuple[torch.Tensor, torch.Tensor]:
     """(O, LSE) of the attention on Q = q_proj(LayerNorm(x_q * gate((C_seq + 1) @ W_pe))), the
     queries computed inside the attention kernel (one mb_flash_ema_fwd_gq launch)."""
     dev = _lib.require_gpu(x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k, E_v, rhos, unique_tensor,
                            C_bounds, what="flash_ema_forward (gated queries)")
+    check_counter_range(rhos, "flash_ema_forward (gated queries)")
     B, L, D = x_q.shape
     H = int(n_heads)
     if D % H:
@@ -456,7 +582,7 @@ def flash_ema_fwd_gq(x_q: torch.Tensor, C_seq: torch.Tensor, W_pe: torch.Tensor,
                   C.stride(1), _lib.ptr(lw), _lib.ptr(lb), float(eps), _lib.ptr(Wq), _lib.ptr(xl),
                   xl.stride(0), xl.stride(1), _lib.ptr(Ek), _lib.ptr(Ev), _lib.ptr(W), _lib.ptr(rh),
                   _lib.ptr(uniq), _lib.ptr(Cb), B, H, L, hd, K, N, Cb.shape[3], Cb.shape[1], int(Br),
-                  int(V_total), _flash_flags(use_silu, absent_mass, table, fp32), _lib.ptr(O), _lib.ptr(LSE),
+                  int(V_total), _flash_flags(use_silu, absent_mass, table, prec), _lib.ptr(O), _lib.ptr(LSE),
                   _lib.stream(dev))
     return O, LSE
 
@@ -484,15 +610,15 @@ class GatedQueryFlashEMAFunction(torch.autograd.Function):
     def forward(ctx, x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k_active, E_v_active, rhos, V_total,
                 unique_tensor, K_max, C_bounds, n_heads, use_silu=True, Br=64, absent_mass=True,
                 precision="bf16", eps=1e-5):
-        fp32 = _fp32(precision)
+        prec = _prec(precision)
         if unique_tensor.shape[1] != K_max:
             raise ValueError(f"unique_tensor has {unique_tensor.shape[1]} slots but K_max={K_max}")
         O, LSE = flash_ema_fwd_gq(x_q, C_seq, W_pe, ln_w, ln_b, W_q, float(eps), x, E_k_active, E_v_active,
                                   rhos, unique_tensor, C_bounds, int(V_total), int(n_heads), bool(use_silu),
-                                  int(Br), bool(absent_mass), fp32)
+                                  int(Br), bool(absent_mass), prec)
         ctx.save_for_backward(x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k_active, E_v_active, rhos,
                               unique_tensor, C_bounds, O, LSE)
-        ctx.cfg = (int(V_total), bool(use_silu), int(Br), bool(absent_mass), fp32, float(eps), int(n_heads))
+        ctx.cfg = (int(V_total), bool(use_silu), int(Br), bool(absent_mass), prec, float(eps), int(n_heads))
         return O
 
     @staticmethod
@@ -501,7 +627,7 @@ class GatedQueryFlashEMAFunction(torch.autograd.Function):
         from .triton_fused_gating import gating_bwd, gating_fwd
         (x_q, C_seq, W_pe, ln_w, ln_b, W_q, x, E_k, E_v, rhos, unique_tensor, C_bounds, O,
          LSE) = ctx.saved_tensors
-        V_total, use_silu, Br, absent_mass, fp32, eps, H = ctx.cfg
+        V_total, use_silu, Br, absent_mass, prec, eps, H = ctx.cfg
         B, L, D = x_q.shape
         hd = D // H
         N = rhos.shape[0]
@@ -510,7 +636,7 @@ class GatedQueryFlashEMAFunction(torch.autograd.Function):
         xr = x_ln.reshape(B * L, D)
         Q = (xr @ W_q.t()).view(B, L, H, hd).transpose(1, 2)
         dQ, dEk, dEv, dWa = flash_ema_bwd(Q, x, E_k, E_v, Wpe, rhos, unique_tensor, C_bounds, O, LSE,
-                                          dO.contiguous(), V_total, use_silu, Br, absent_mass, fp32)
+                                          dO.contiguous(), V_total, use_silu, Br, absent_mass, prec)
         dQr = dQ.transpose(1, 2).reshape(B * L, D)  # row (b, t), column h hd + d
         dW_q = dQr.t() @ xr
         dx_ln = dQr @ W_q

@@ -14,10 +14,9 @@ Three forms of the same attention, all in torch on the CPU:
                is SiLU(0) = 0 and their score 0 -- folded into the softmax
                denominator as (V - K_b) * exp(0 - m).  ``absent_mass=False`` gives
                the Triton kernel as executed (triton_flash_ema.py:215-229 wipes the
-               absent mass).  ``gate_round="bf16"`` rounds the gate operands to
-               bfloat16 as triton_flash_ema.py:188-190 does; ``gate_round="f16"``
-               rounds c_dec and W_pe * log2(e) to float16 instead, as the HIP
-               kernel feeds its MFMA (weights pre-scaled for base-2 exponentials).
+               absent mass).  ``gate_round`` (GATE_ROUNDS) rounds the gate operands
+               as the reference's Triton kernel ("bf16", triton_flash_ema.py:188-190)
+               or the HIP kernels ("f16", "split") feed their matrix products.
 ``sparse_backward_formulas``
                the reference's closed-form gradients (triton_flash_ema.py:336-350
                and :446-465), evaluated loop by loop; autograd of ``sparse`` must
@@ -74,23 +73,39 @@ def dense(Q, x, E_k_slots, E_v_slots, rhos, pe_weight, n_heads, use_silu=True, c
     return O.transpose(1, 2).reshape(B, L, D)                       # :84
 
 
+# ``gate_round``: how the gate GEMM's operands are rounded and how the dW_pe product takes
+# its operands.  None: exact everywhere.  "bf16": both gate operands bf16 (the reference's
+# triton_flash_ema.py:188-190).  "f16": both fp16, W pre-scaled by log2 e (the HIP kernels'
+# single-product gate).  "split": the gate exact (the HIP kernels' fp16 hi + lo split leaves
+# ~2^-22, below what a float64 check resolves at these bars).  "f16c" / "f16w": only the
+# counter / only W_pe rounded to fp16 (for measuring which rounding matters).  Every mode but
+# None takes the dW_pe product from bf16 c_dec and bf16 dpre (triton_flash_ema.py:463-465).
+GATE_ROUNDS = (None, "bf16", "f16", "split", "f16c", "f16w")
+
+
 def _round_gate_operands(W, gate_round):
-    """W_pe as the gate GEMM sees it: exact, bf16-rounded, or f16(W * log2 e) / log2 e."""
-    if gate_round is None:
+    """W_pe as the gate GEMM sees it: exact, bf16-rounded, or f16(W * log2 e) / log2 e
+    ("f16" and "f16w"; "f16c" and "split" leave W exact)."""
+    if gate_round not in GATE_ROUNDS:
+        raise ValueError(f"gate_round={gate_round!r}")
+    if gate_round in (None, "f16c", "split"):
         return W
     if gate_round == "bf16":
         return W.to(torch.bfloat16).to(W.dtype)
-    if gate_round == "f16":
+    if gate_round in ("f16", "f16w"):
         l2e = 1.0 / math.log(2.0)
         return (W.float() * l2e).to(torch.float16).to(W.dtype) / l2e
     raise ValueError(f"gate_round={gate_round!r}")
 
 
 def _round_gate_counter(c, gate_round):
-    """c_dec as the gate GEMM sees it (rounded through float32, as computed on device)."""
-    if gate_round is None:
+    """c_dec as the gate GEMM sees it (rounded through float32, as computed on device):
+    exact for None, "f16w" and "split", else fp16 ("f16", "f16c") or bf16 ("bf16")."""
+    if gate_round not in GATE_ROUNDS:
+        raise ValueError(f"gate_round={gate_round!r}")
+    if gate_round in (None, "f16w", "split"):
         return c
-    return c.float().to(torch.float16 if gate_round == "f16" else torch.bfloat16).to(c.dtype)
+    return c.float().to(torch.float16 if gate_round != "bf16" else torch.bfloat16).to(c.dtype)
 
 
 def _steps(L, t_eval):
@@ -165,8 +180,8 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     dW_pe[:, head] = sum c_dec^T dpre (:465).
     Returns dQ [B,H,L,hd], dE_k [B,K,D], dE_v [B,K,D], dW_pe [N,D].
     With ``gate_round`` the gate operands are rounded as in ``sparse`` and the dW_pe
-    product takes bf16 c_dec (of the gate's rounded c_dec) and bf16 dpre, as
-    triton_flash_ema.py:463-465 does.
+    product takes bf16 c_dec (of the gate's rounded c_dec; of the float32 counter with
+    "split") and bf16 dpre, as triton_flash_ema.py:463-465 does.
     With ``t_eval`` only those steps contribute (exact when dO is zero elsewhere); dQ
     is zero at the other steps.
     """
@@ -214,7 +229,8 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
         dEk += ds.unsqueeze(-1) * q_t * g * scale
         dEv += p.unsqueeze(-1) * do_t * g
         dpre = (ds.unsqueeze(-1) * q_t * scale * Ek + p.unsqueeze(-1) * do_t * Ev) * gp
-        dW += torch.einsum("bkn,bkd->nd", bf(cg), bf(dpre.reshape(B, K, D)))
+        cw = c_dec.float().to(dt) if gate_round == "split" else cg  # the kernel's float32 counter
+        dW += torch.einsum("bkn,bkd->nd", bf(cw), bf(dpre.reshape(B, K, D)))
         match = (x[:, t].unsqueeze(1) == unique) & valid
         C = c_dec + match.unsqueeze(-1).to(dt)
     return dQ, dEk.reshape(B, K, D), dEv.reshape(B, K, D), dW

@@ -116,3 +116,59 @@ def test_scores_are_kept_up_to_the_memory_cap(monkeypatch):
     assert not tfe.keep_scores(1, 1, cap_elems + 1, 1)
     monkeypatch.setattr(tfe, "SAVE_SCORES", False)
     assert not tfe.keep_scores(56, 8, 1638, 512)
+
+
+def test_score_budget_is_shared_by_the_tensors_still_alive(monkeypatch):
+    """The saved-score limit is one budget per device for every score tensor still held:
+    six cfg2-sized layers (1.47 GB each) fit 16 GiB, a twelfth does not while eleven are
+    alive, and a freed tensor gives its bytes back."""
+    import gc
+    import torch
+    from mathbrain import triton_flash_ema as tfe
+    budget = tfe.ScoreBudget()
+    monkeypatch.setattr(tfe, "score_budget", budget)
+    Q = torch.empty(56, 8, 512, 0)      # the shape is all _reserve_scores reads
+    held = []
+    for _ in range(11):
+        nb = tfe._reserve_scores(Q, 1638)
+        assert nb == 4 * 56 * 8 * 1638 * 512
+        t = torch.empty(1)
+        budget.hold(t, nb)
+        held.append(t)
+    assert budget.held("cpu") == 11 * nb
+    assert tfe._reserve_scores(Q, 1638) == 0            # 12 x 1.47 GB > 16 GiB
+    del t
+    held.pop()
+    gc.collect()
+    assert budget.held("cpu") == 10 * nb
+    nb2 = tfe._reserve_scores(Q, 1638)
+    assert nb2 == nb
+    budget.release("cpu", nb2)
+    held.clear()
+    gc.collect()
+    assert budget.held("cpu") == 0
+    monkeypatch.setattr(tfe, "SAVE_SCORES", False)
+    assert tfe._reserve_scores(Q, 1638) == 0
+
+
+def test_counter_range_check_names_the_half_life_limit():
+    """Rates whose key counters could leave the gate operands' fp16 range are refused on the
+    host: the model with train.py's --max_hl 100000 raises at construction, and the
+    functional check reads a rate tensor once per version."""
+    import torch
+    from mathbrain._lib import HipKernelError
+    from mathbrain import triton_flash_ema as tfe
+    from mathbrain.model import SlotTransformerLM
+    assert 45000 < tfe.MAX_HALF_LIFE < 45500
+    with pytest.raises(HipKernelError, match="half-lives up to 45359 steps"):
+        SlotTransformerLM(100, 32, 1, 2, N=8, max_hl=100000.0)
+    SlotTransformerLM(100, 32, 1, 2, N=8, max_hl=45000.0)
+    SlotTransformerLM(100, 32, 1, 2, N=8)                     # train.py's default, 2048
+    rhos = torch.exp(-torch.log(torch.tensor(2.0)) / torch.tensor([4.0, 4096.0]))
+    tfe.check_counter_range(rhos)
+    rhos[1] = 0.99999
+    with pytest.raises(HipKernelError, match="half-life"):
+        tfe.check_counter_range(rhos)
+    with pytest.raises(HipKernelError, match="half-life inf"):
+        tfe.check_counter_range([0.5, 1.0])
+    tfe.check_counter_range([0.5, 0.999])

@@ -35,6 +35,7 @@ import pytest
 import torch
 
 from oracle import attention as att
+from tests.test_gpu_flash import kernel_rounding
 
 pytestmark = pytest.mark.gpu
 
@@ -146,8 +147,9 @@ def oracle_from_chunk_states(w, r, dO, chunks, Cb):
         args = (w["Q"][r][:, :, s].to(dt), d["x"][r][:, s], w["E_k"][r].to(dt),
                 w["E_v"][r].to(dt), w["W"].to(dt), d["rhos"].to(dt), V, d["unique"][r])
         c0 = Cb[r, j].to(dt)
-        O, LSE = att.sparse(*args, c0, return_lse=True, gate_round="f16")
-        g = att.sparse_backward_formulas(*args, dO[r][:, :, s].to(dt), c0, gate_round="f16")
+        # N = 128: the default mode's gate takes single fp16 operands (kernel_rounding)
+        O, LSE = att.sparse(*args, c0, return_lse=True, gate_round=kernel_rounding(N, HD))
+        g = att.sparse_backward_formulas(*args, dO[r][:, :, s].to(dt), c0, gate_round=kernel_rounding(N, HD))
         Os.append(O)
         LSEs.append(LSE)
         dQ[:, :, s] = g[0]

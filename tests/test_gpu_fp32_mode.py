@@ -3,7 +3,7 @@ takes fp16 hi + lo operand pairs (three products) and the dW_pe product bf16 hi 
 everything else is fp32.  Checked against the exact float64 oracle at the task's fp32-mode
 tolerance, 1e-4 norm-wise (max|got - want| / max|want|), for O, LSE and all four gradients:
 at configuration 1's shapes and scales, at the large test scales (queries N(0,1),
-embeddings N(0,0.25), W_pe N(0,0.09): scores ~100, where the default mode's 16-bit gate
+embeddings N(0,0.25), W_pe N(0,0.09): scores ~100, where the fast mode's single fp16 gate
 operands move O by a percent), at N = 64 with 8 x 64 heads, on a configuration-2 slice, with
 both flags, and through the vocabulary-table rows."""
 import pytest
@@ -52,9 +52,9 @@ def check(c, seed=0, use_silu=True, absent_mass=True, table=None, bf16_worse=Fal
     want = exact(c, dO, use_silu, absent_mass)
     errs = {n: norm_err(a, b) for n, a, b in zip(NAMES, got, want)}
     msg = ", ".join(f"{k} {v:.2e}" for k, v in errs.items())
-    if bf16_worse:
-        fast = {n: norm_err(a, b) for n, a, b in zip(NAMES, run(c, dO, "bf16", use_silu, absent_mass, table), want)}
-        msg += " | bf16 mode: " + ", ".join(f"{k} {v:.2e}" for k, v in fast.items())
+    if bf16_worse:  # the single-product fp16 gate is visibly worse at these scales
+        fast = {n: norm_err(a, b) for n, a, b in zip(NAMES, run(c, dO, "fp16", use_silu, absent_mass, table), want)}
+        msg += " | fp16 mode: " + ", ".join(f"{k} {v:.2e}" for k, v in fast.items())
         assert max(fast.values()) > 10 * max(errs.values()), msg
     print(msg)
     assert max(errs.values()) < TOL_FP32, msg

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import model as omodel
-from tests.test_gpu_flash import CFG, check_backward, check_forward, make_case, norm_err
+from tests.test_gpu_flash import CFG, check_backward, check_forward, kernel_rounding, make_case, norm_err
 
 pytestmark = pytest.mark.gpu
 
@@ -97,7 +97,7 @@ def test_hd128_model(kv_table):
     p = {k: v.detach().cpu().double().requires_grad_() for k, v in m.state_dict().items()
          if k not in ("ema_rhos", "lm_head.weight")}
     want = omodel.lm_forward(p, x, 1, H, m.ema_rhos.cpu(), V, unique_slots=uniq, c_base=cb.double(),
-                             pad_mask=pm, gate_round="f16", t_eval=list(range(L)))
+                             pad_mask=pm, gate_round=kernel_rounding(N, D // H), t_eval=list(range(L)))
     (want * R.double()).sum().backward()
     assert norm_err(logits, want) < 1e-4
     grads = dict(m.named_parameters())
