@@ -293,13 +293,43 @@ __device__ void flash_batch_meta(const FlashArgs& a, int b, int bi, int kend, co
     }
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
 // Producer: each thread owns up to MAXI blocks (slot j, 4 steps, 4 rates) of the batch's
-// cdec tiles and up to MAXE float4 of the embedding copy.
+// cdec tiles and up to MAXE float4 of the embedding copy.  MAXE = 0: the embedding rows go
+// from global memory straight into the staging buffer (load_e_lds), without registers.
 template <int NPAD, int SB, int MAXI, int MAXE>
 struct Producer {
     static constexpr int BPS = (kTB / 4) * (NPAD / 4);  // blocks per slot
     float4 s[MAXI];
-    float4 e[MAXE];
+    float4 e[MAXE > 0 ? MAXE : 1];
+
+    // The batch's E_k / E_v rows ([SB][2][width] floats) into E with global_load_lds_dwordx4:
+    // wave w issues the 1 KB pieces w, w + waves, ...; lane l of a piece moves float4 64 c + l,
+    // which lands at E + 4 (64 c + l) (the instruction writes lane l's 16 bytes at the LDS
+    // address in M0 plus 16 l).  Rows of slots past kend are not loaded (no slot reads them).
+    // The caller waits for the loads (vmcnt) before the barrier that publishes E.
+    template <bool VR, class A>
+    __device__ void load_e_lds(const A& a, int b, int bi, int kend, int D, int col0, int width,
+                               const BatchMeta* meta, float* E) const {
+        const int w4 = width / 4;
+        const int nvec = SB * 2 * w4;
+        const int lane = threadIdx.x & 63;
+        const int nw = blockDim.x >> 6;
+        for (int c = threadIdx.x >> 6; c * 64 < nvec; c += nw) {
+            const int i = c * 64 + lane;
+            const int j = i / (2 * w4);
+            const int r = i % (2 * w4);
+            const int which = r / w4;
+            const int c4 = r % w4;
+            const int k = bi * SB + j;
+            if (i < nvec && k < kend && col0 + c4 * 4 < D) {
+                const float* src =
+                    (which ? a.Ev : a.Ek) + e_row<VR>(a, b, k, VR ? meta[j].u : 0) * D + col0 + c4 * 4;
+                __builtin_amdgcn_global_load_lds(src, (lds_void*)(E + 256 * c), 16, 0, 0);
+            }
+        }
+    }
 
     template <bool VR, class A>
     __device__ void load(const A& a, int b, int cbi, int bi, int kend, int D, int col0,
