@@ -59,12 +59,36 @@ int mb_abi_version(void);
  *                rows of other keys are not written.  May alias c_init.
  *   stamp_out    [B, K] int32 or NULL: position of that last occurrence, else -1.
  *
- * Limits: L <= 8192 (the per-sequence index lives in the 160 KB LDS of one CU).
+ * Limits: L <= 8192 (the per-sequence index lives in the 160 KB LDS of one CU); longer
+ * sequences take mb_ema_query_scan_ws.
  */
 int mb_ema_query_scan(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int B, int L,
                       const float *rhos, int N, int64_t vocab_size, const float *c_init,
                       const int64_t *c_init_keys, int K, const int64_t *doc_ids, float *C_seq,
                       float *state_out, int32_t *stamp_out, void *stream);
+
+/*
+ * The same scan for any L.  Replaces compute_query_ema_history (mathbrain/triton_ema_query.py:
+ * 120-169), whose kernel walks any length (:34).  Up to 8192 steps it is mb_ema_query_scan;
+ * longer sequences run as consecutive 2048-step pieces on the stream, each chain of a piece
+ * starting from its token's last occurrence before the piece (C_seq there + 1, decayed), and
+ * need a workspace of mb_ema_query_scan_workspace(B, L, vocab_size) bytes (4-byte aligned,
+ * contents irrelevant): a [B, vocab_size] int32 table of last positions.  Token ids must
+ * then lie in [0, vocab_size) (ids outside count as never seen before).
+ */
+int mb_ema_query_scan_ws(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int B, int L,
+                         const float *rhos, int N, int64_t vocab_size, const float *c_init,
+                         const int64_t *c_init_keys, int K, const int64_t *doc_ids, float *C_seq,
+                         float *state_out, int32_t *stamp_out, void *workspace,
+                         int64_t workspace_bytes, void *stream);
+
+/*
+ * Workspace bytes mb_ema_query_scan_ws needs: 0 for L <= 8192, else B * vocab_size * 4 (-1,
+ * with mb_last_error set, for negative sizes or L > 8192 with vocab_size < 1).  No
+ * counterpart in the reference, whose scan allocates its [B, V+1] tables per call
+ * (triton_ema_query.py:141-143).
+ */
+int64_t mb_ema_query_scan_workspace(int B, int L, int64_t vocab_size);
 
 /*
  * Key-side EMA states at chunk starts.  Replaces precompute_boundaries and its kernel
@@ -83,7 +107,7 @@ int mb_ema_query_scan(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, 
  *   C_bounds [B, nc, K, Np] output, nc = max(1, ceil(L/Br)), Np >= N; columns N..Np-1
  *            are written as 0 (the reference pads N to max(N, 16) for tl.dot).
  *
- * Limits: L <= 8192.
+ * Any L (the sequence's tokens are staged in LDS 8192 at a time).
  */
 int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int B,
                            int L, const int64_t *unique, int K, const float *rhos, int N, int Br,
@@ -102,7 +126,8 @@ int mb_ema_boundary_states(const int64_t *x, int64_t x_stride_b, int64_t x_strid
  *           width >= L keeps all of them)
  *   counts  [B] int32 output: distinct values per row
  *
- * Limits: L <= 8192 (a row is sorted in the LDS of one CU).
+ * Limits: L <= 16384 (a row is sorted in the LDS of one CU); beyond 8192 ids a row whose
+ * values span 2^32 or more gets counts[b] = -1 and an all -1 list (token ids always fit).
  */
 int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int B, int L,
                    int64_t *out, int width, int32_t *counts, void *stream);

@@ -29,6 +29,9 @@ SIGNATURES = {
     "mb_last_error": ([], ctypes.c_char_p),
     "mb_abi_version": ([], _i),
     "mb_ema_query_scan": ([_p, _i64, _i64, _i, _i, _p, _i, _i64, _p, _p, _i, _p, _p, _p, _p, _p], _i),
+    "mb_ema_query_scan_ws": ([_p, _i64, _i64, _i, _i, _p, _i, _i64, _p, _p, _i, _p, _p, _p, _p, _p, _i64,
+                              _p], _i),
+    "mb_ema_query_scan_workspace": ([_i, _i, _i64], _i64),
     "mb_ema_boundary_states": ([_p, _i64, _i64, _i, _i, _p, _i, _p, _i, _i, _p, _i64, _p, _p, _i, _p], _i),
     "mb_unique_rows": ([_p, _i64, _i64, _i, _i, _p, _i, _p, _p], _i),
     "mb_flash_ema_fwd": ([_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p,

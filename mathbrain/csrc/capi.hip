@@ -37,4 +37,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* mb_last_error(void) { return mb::g_last_error.c_str(); }
 
-extern "C" int mb_abi_version(void) { return 7; }
+extern "C" int mb_abi_version(void) { return 8; }

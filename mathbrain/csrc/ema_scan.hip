@@ -107,14 +107,14 @@ constexpr int kMaxLongRuns = 128;
 __host__ __device__ inline int long_run(int L) { return L / kMaxLongRuns > 16 ? (L + kMaxLongRuns - 1) / kMaxLongRuns : 16; }
 
 struct ScanLds {
-    size_t keys, chain_start, elem_chain, chain_key, agg, aggr, lowT, highT, scan_scratch;
+    size_t keys, chain_start, elem_chain, chain_key, agg, aggr, lowT, highT, scan_scratch, chain_prev;
     size_t sort_b, sort_cnt;
     size_t htab, hcnt, hpre, hpos, hbits, hlpre, hnl;  // grouping by hash (lgTS > 0)
     size_t total;
     // rows of the power tables and of the cut aggregates hold 1 << lgRow floats (the slice
     // width rounded up to a power of two, so that row addressing is a shift)
     __host__ __device__ ScanLds(int L, int Lp, int key_bytes, int nthr, int ncut, int nH, int lgRow,
-                                int lgTS = 0) {
+                                int lgTS = 0, bool piece = false) {
         auto al = [](size_t o) { return (o + 15) & ~(size_t)15; };
         keys = 0;
         size_t o = al((size_t)Lp * key_bytes);
@@ -130,6 +130,9 @@ struct ScanLds {
         o = highT + ((size_t)nH * 4 << lgRow);
         scan_scratch = o = al(o);
         o += 64 * 4;
+        // piece mode: per chain, the last position of its token before the piece (or -1)
+        chain_prev = o = al(o);
+        if (piece) o += (size_t)(L + 1) * 4;
         total = al(o);
         sort_b = after_keys;
         sort_cnt = al(sort_b + (size_t)L * key_bytes);
@@ -169,14 +172,21 @@ constexpr uint32_t kHashEmpty = 0xFFFFFFFFu;
 //      and stamp at each chain's last element).
 // rho^d comes from two LDS tables per rate, rho^(d mod 64) * rho^(64 floor(d / 64)),
 // each entry a correctly rounded float of a double-precision power.
-template <typename KeyT, int VEC, bool DOCS, int MAXR, bool HASH>
+// PIECE: the launch scans steps [T0, T0 + L) of sequences of Ltot steps (longer sequences
+// run as consecutive pieces, one launch each): a chain whose token occurred before T0 starts
+// from that occurrence's post-increment state C_seq[b, s] + 1 decayed by rho^(T0 - s), with
+// s = last_pos[b, token] (kept by query_piece_last_kernel between launches), and a key's c0
+// enters decayed by rho^T0; positions and stamps are absolute.  Without PIECE, T0 = 0 and
+// Ltot = L.
+template <typename KeyT, int VEC, bool DOCS, int MAXR, bool HASH, bool PIECE = false>
 __global__ void __launch_bounds__(kScanThreads)
 ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L,
                       const float* __restrict__ rhos, int N, const float* __restrict__ c_init,
                       const int64_t* __restrict__ c_init_keys, int K,
                       const int64_t* __restrict__ doc_ids, float* __restrict__ C_seq,
                       float* state_out, int32_t* __restrict__ stamp_out, int pb, int tok_bits,
-                      int slice_w, int lgS, int ncut, int lgTS) {
+                      int slice_w, int lgS, int ncut, int lgTS, int T0, int Ltot,
+                      const int32_t* __restrict__ last_pos, int64_t V) {
     static_assert(!HASH || sizeof(KeyT) == 4, "hash grouping keys are 32-bit tokens");
     // elements per unrolled chunk of a pass-B walk; their c_init rows (and with doc_ids
     // their documents) sit in registers
@@ -188,7 +198,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     const int nH = (L - 1) / 64 + 1;
     const int Lp = 1 << pb;
     const int lgRow = ceil_log2(slice_w);
-    const ScanLds lay(L, Lp, (int)sizeof(KeyT), nthr, ncut, nH, lgRow, HASH ? lgTS : 0);
+    const ScanLds lay(L, Lp, (int)sizeof(KeyT), nthr, ncut, nH, lgRow, HASH ? lgTS : 0, PIECE);
     KeyT* keys = reinterpret_cast<KeyT*>(smem + lay.keys);
     uint16_t* chain_start = reinterpret_cast<uint16_t*>(smem + lay.chain_start);
     uint16_t* elem_chain = reinterpret_cast<uint16_t*>(smem + lay.elem_chain);
@@ -198,7 +208,16 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     float* lowT = reinterpret_cast<float*>(smem + lay.lowT);
     float* highT = reinterpret_cast<float*>(smem + lay.highT);
     int* scratch = reinterpret_cast<int*>(smem + lay.scan_scratch);
+    int* chain_prev = reinterpret_cast<int*>(smem + lay.chain_prev);
     const int S = 1 << lgS;
+    if (!PIECE) {
+        T0 = 0;
+        Ltot = L;
+    }
+    // last position of `token` before T0, or -1 (ids outside [0, V) count as never seen)
+    auto prev_of = [&](uint64_t token) -> int {
+        return PIECE && token < (uint64_t)V ? last_pos[(int64_t)b * V + (int64_t)token] : -1;
+    };
 
     // 0. early loads: tokens, c_init key ids, rates; then the power-table entries
     // (double-precision work that overlaps the loads' latency)
@@ -206,7 +225,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
 #pragma unroll
     for (int r = 0; r < MAXR; ++r) {
         const int i = threadIdx.x + r * nthr;
-        tokv[r] = i < L ? (uint64_t)x[(int64_t)b * sb + (int64_t)i * sl] : 0;
+        tokv[r] = i < L ? (uint64_t)x[(int64_t)b * sb + (int64_t)(T0 + i) * sl] : 0;
     }
     int64_t pre_key[kKeyPrefetch];
 #pragma unroll
@@ -234,7 +253,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         const int i = threadIdx.x + r * nthr;
         if (!(i < n_tab && table_rate(i) < N)) pre_tab[r] = 0.f;
     }
-    const int64_t doc0 = DOCS ? doc_ids[(int64_t)b * L] : 0;
+    const int64_t doc0 = DOCS ? doc_ids[(int64_t)b * Ltot] : 0;
 #pragma unroll
     for (int r = 0; r < kTablePrefetch; ++r) {
         const int i = threadIdx.x + r * nthr;
@@ -308,7 +327,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         // the power tables and the stamps' initial -1 now: nothing of the grouping overlaps
         // them, and their stores then need no phase (and barrier) of their own
         store_tables();
-        if (stamp_out && slice == 0)
+        if (stamp_out && slice == 0 && T0 == 0)
             for (int k = threadIdx.x; k < K; k += nthr) stamp_out[(int64_t)b * K + k] = -1;
         __syncthreads();
         const uint32_t tokmask = 0xFFFFFFFFu >> pb;
@@ -405,6 +424,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
                 const int j = base + rank;
                 keys[j] = (KeyT)cid << pb | (KeyT)i;
                 elem_chain[j] = (uint16_t)cid;
+                if (PIECE && rank == 0) chain_prev[cid] = prev_of(tokv[r]);  // the chain's head
             }
         }
         for (int i = L + threadIdx.x; i < Lp; i += nthr) keys[i] = ~KeyT(0);
@@ -446,6 +466,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
             if (chain_head(i)) {
                 chain_start[c] = (uint16_t)i;
                 chain_key[c] = -1;
+                if (PIECE) chain_prev[c] = prev_of((uint64_t)(keys[i] >> pb));
                 ++c;
             }
             elem_chain[i] = (uint16_t)(c - 1);
@@ -454,7 +475,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         }
         if constexpr (!HASH) {
             store_tables();
-            if (stamp_out && slice == 0)
+            if (stamp_out && slice == 0 && T0 == 0)
                 for (int k = threadIdx.x; k < K; k += nthr) stamp_out[(int64_t)b * K + k] = -1;
         }
         __syncthreads();
@@ -503,7 +524,8 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     const bool active = n0 < N && g < groups;
     const KeyT posmask = (pb == 0) ? KeyT(0) : ((KeyT(1) << pb) - 1);
     auto pos_of = [&](int j) { return (int)(keys[j] & posmask); };
-    auto doc_of = [&](int pos) { return doc_ids[(int64_t)b * L + pos]; };
+    auto doc_of = [&](int pos) { return doc_ids[(int64_t)b * Ltot + T0 + pos]; };
+    auto doc_abs = [&](int pos) { return doc_ids[(int64_t)b * Ltot + pos]; };
     // rho^d for this lane's VEC rates
     auto powv = [&](int d, float* pw) {
         const float* lo = lowT + ((d & 63) << lgRow) + lane_r;
@@ -519,7 +541,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     };
     // row offsets as 24-bit products from per-sequence bases (the host checks L * N and
     // K * N against 2^31 and K against 2^24)
-    float* const Cb = C_seq + (int64_t)b * L * N;
+    float* const Cb = C_seq + ((int64_t)b * Ltot + T0) * N;
     const float* const c0b = c_init + (int64_t)b * K * N;
     float* const stb = state_out ? state_out + (int64_t)b * K * N : nullptr;
     auto row = [&](int r) { return (int)__umul24((unsigned)r, (unsigned)N) + n0; };
@@ -532,6 +554,10 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     Vec<VEC> c0v[CH];
     int keyv[CH];
     int64_t docv[CH];
+    // PIECE: the chain's previous occurrence before T0 (-1: none) and, with doc_ids, the
+    // document its carry belongs to (that occurrence's, or the sequence's first)
+    int prevv[CH];
+    int64_t pdocv[CH];
     uint32_t startm = 0, lastm = 0;  // bit e: element c + e starts a walk / ends its chain
     auto gather = [&](int c) {
         startm = lastm = 0;
@@ -546,9 +572,14 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
             startm |= (start ? 1u : 0u) << e;
             lastm |= (in && nxt != cid ? 1u : 0u) << e;
             keyv[e] = start ? chain_key[cid] : -1;
-            c0v[e] = load_vec<VEC>(c0b + row(keyv[e] >= 0 ? keyv[e] : 0), start && keyv[e] >= 0 && active,
-                                   n0, N);
+            prevv[e] = PIECE && start ? chain_prev[cid] : -1;
+            if (PIECE && prevv[e] >= 0)  // the carry: C_seq at the previous occurrence
+                c0v[e] = load_vec<VEC>(C_seq + ((int64_t)b * Ltot + prevv[e]) * N + n0, active, n0, N);
+            else
+                c0v[e] = load_vec<VEC>(c0b + row(keyv[e] >= 0 ? keyv[e] : 0), start && keyv[e] >= 0 && active,
+                                       n0, N);
             if (DOCS) docv[e] = in ? doc_of(pos_of(j)) : 0;
+            if (DOCS && PIECE) pdocv[e] = prevv[e] >= 0 ? doc_abs(prevv[e]) : doc0;
             prev = cid;
         }
     };
@@ -570,9 +601,10 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
         int64_t dprev = 0;
         if (DOCS) {
             const bool first = beg == cs;
-            const bool has_prev = !first || chain_key[cc] >= 0;
+            const int cprev = PIECE ? chain_prev[cc] : -1;
+            const bool has_prev = !first || chain_key[cc] >= 0 || cprev >= 0;
             const int64_t dcur = doc_of(tp);
-            const int64_t dref = first ? doc0 : doc_of(pos_of(beg - 1));
+            const int64_t dref = first ? (cprev >= 0 ? doc_abs(cprev) : doc0) : doc_of(pos_of(beg - 1));
             reset = has_prev && dref != dcur;
             dprev = dcur;
         }
@@ -604,13 +636,32 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
     // 5. pass B: the walk, CH elements per chunk; P is the post-increment state at time tp.
     // The range's first element starts from its chain's c0 and, when the range starts inside
     // the chain, the carries through the chain's cuts in (cs, ra].
-    float P[VEC];
+    // PIECE: a chain's start state at the piece's step 0 (tp = 0): its previous occurrence's
+    // C_seq + 1, or its key's c0, decayed over the steps since (log2 rho split in two floats).
+    float l2hi[VEC], l2lo[VEC];
+    if (PIECE) {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) P[v] = c0v[0].v[v];
+        for (int v = 0; v < VEC; ++v) {
+            l2hi[v] = l2lo[v] = 0.f;
+            if (n0 + v < N) log2_split(rhos[n0 + v], l2hi[v], l2lo[v]);
+        }
+    }
+    auto seed = [&](int e, float* Pv) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) Pv[v] = c0v[e].v[v];
+        if (PIECE && T0 > 0) {
+            const bool carry = prevv[e] >= 0;
+            const int d = T0 - (carry ? prevv[e] : 0);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) Pv[v] = (Pv[v] + (carry ? 1.0f : 0.0f)) * pow_steps(l2hi[v], l2lo[v], d);
+        }
+    };
+    float P[VEC];
+    seed(0, P);
     int tp = 0;
     int key = keyv[0];
-    bool has_prev = key >= 0;
-    int64_t dprev = doc0;
+    bool has_prev = key >= 0 || prevv[0] >= 0;
+    int64_t dprev = DOCS && PIECE ? pdocv[0] : doc0;
     if (ra < re) {
         const int cs = chain_start[elem_chain[ra]];
         for (int m = (cs >> lgS) + 1; m <= g; ++m) {
@@ -642,12 +693,11 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
                 const int t = tn;
                 tn = pos_of(min(j + 1, re - 1));  // next position, read one step ahead
                 if ((startm >> e) & 1) {
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) P[v] = c0v[e].v[v];
+                    seed(e, P);
                     tp = 0;
                     key = keyv[e];
-                    has_prev = key >= 0;
-                    dprev = doc0;
+                    has_prev = key >= 0 || prevv[e] >= 0;
+                    dprev = DOCS && PIECE ? pdocv[e] : doc0;
                 }
                 float cv[VEC];
                 powv(t - tp, cv);
@@ -668,7 +718,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
                 tp = t;
                 if (((lastm >> e) & 1) && key >= 0) {
                     if (stb && active) store_vec<VEC>(stb + row(key), P, n0, N);
-                    if (stamp_out && slice == 0 && lane_r == 0) stamp_out[(int64_t)b * K + key] = t;
+                    if (stamp_out && slice == 0 && lane_r == 0) stamp_out[(int64_t)b * K + key] = T0 + t;
                 }
             }
         }
@@ -692,6 +742,7 @@ ema_query_scan_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int
 
 constexpr int kBoundThreads = 512;
 constexpr int kBoundSlots = 64;
+constexpr int kBoundWin = 8192;  // tokens staged in LDS at a time
 
 // 64 bits of the bitmask `bits` starting at bit `pos` (bits beyond the array read as 0:
 // the array carries one spare word).
@@ -710,9 +761,13 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
                     int N, int Br, int nc, const float* __restrict__ c_init, int64_t cis,
                     const int64_t* __restrict__ doc_ids, float* __restrict__ out, int Np) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int nwords = (L >> 6) + 2;
-    int64_t* tok = reinterpret_cast<int64_t*>(smem);                 // [L]
-    uint64_t* rbits = reinterpret_cast<uint64_t*>(tok + L);          // [nwords] document changes
+    // The tokens (and document-change bits) of a window [w0, w0 + WL) of the sequence sit in
+    // LDS: the whole sequence when L <= kBoundWin, else windows that move forward as the
+    // pieces reach their end (all waves walk the same pieces, so they move together).
+    const int WL = min(L, kBoundWin);
+    const int nwords = (WL >> 6) + 2;
+    int64_t* tok = reinterpret_cast<int64_t*>(smem);                 // [WL]
+    uint64_t* rbits = reinterpret_cast<uint64_t*>(tok + WL);         // [nwords] document changes
     const int b = blockIdx.x;
     const int k0 = blockIdx.y * kBoundSlots;
     const int wave = threadIdx.x >> 6;
@@ -737,16 +792,23 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
         }
     }
 
-    for (int i = threadIdx.x; i < L; i += blockDim.x) tok[i] = x[(int64_t)b * sb + (int64_t)i * sl];
-    // bit p: the document changes at step p (doc[p] != doc[p - 1], p >= 1)
-    for (int w = wave; w < nwords; w += nw) {
-        const int p = 64 * w + lane;
-        bool chg = false;
-        if (doc_ids && p >= 1 && p < L)
-            chg = doc_ids[(int64_t)b * L + p] != doc_ids[(int64_t)b * L + p - 1];
-        const uint64_t m = __ballot(chg);
-        if (lane == 0) rbits[w] = m;
-    }
+    // Stages the window starting at w0: tok[i] = x[w0 + i]; bit i: the document changes at
+    // step w0 + i (doc[p] != doc[p - 1], p >= 1).
+    int w0 = 0;
+    auto stage = [&](int start) {
+        w0 = start;
+        for (int i = threadIdx.x; i < WL; i += blockDim.x)
+            tok[i] = w0 + i < L ? x[(int64_t)b * sb + (int64_t)(w0 + i) * sl] : (int64_t)-1;
+        for (int w = wave; w < nwords; w += nw) {
+            const int p = w0 + 64 * w + lane;
+            bool chg = false;
+            if (doc_ids && p >= 1 && p < L)
+                chg = doc_ids[(int64_t)b * L + p] != doc_ids[(int64_t)b * L + p - 1];
+            const uint64_t m = __ballot(chg);
+            if (lane == 0) rbits[w] = m;
+        }
+    };
+    stage(0);
     float hi[RPL], lo[RPL];
 #pragma unroll
     for (int r = 0; r < RPL; ++r) {
@@ -755,9 +817,25 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
         const int n = lane + 64 * r;
         if (n < N) log2_split(rhos[n], hi[r], lo[r]);
     }
-    float p64[RPL];  // rho^64, the decay over a whole piece
+    // rho^64, the decay over a whole piece, as a float pair (hi + lo): the state is scaled by
+    // it once per piece, so a rounding of rho^64 itself would bias it by the same factor every
+    // piece (1.2e-5 relative by step 16384 in a single float); the pair leaves the per-piece
+    // rounding of the product, which does not accumulate in one direction.
+    // A chunk of Br steps is walked as pieces of 64 and one last piece of brem steps, so
+    // these are the only two lengths (brem = 64 when 64 divides Br).
+    const int brem = Br - 64 * ((Br - 1) / 64);
+    float p64[RPL], p64l[RPL], prem[RPL], preml[RPL];
 #pragma unroll
-    for (int r = 0; r < RPL; ++r) p64[r] = pow_steps(hi[r], lo[r], 64);
+    for (int r = 0; r < RPL; ++r) {
+        const int n = lane + 64 * r;
+        const double l2 = n < N ? log2((double)rhos[n]) : 0.0;
+        const double pd = n < N ? exp2(64.0 * l2) : 0.0;
+        const double pr = n < N ? exp2((double)brem * l2) : 0.0;
+        p64[r] = (float)pd;
+        p64l[r] = (float)(pd - (double)p64[r]);
+        prem[r] = (float)pr;
+        preml[r] = (float)(pr - (double)prem[r]);
+    }
     __syncthreads();
 
     const int64_t cstride = (int64_t)K * Np;
@@ -790,14 +868,22 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
     int64_t tnext = (pend > 0 && lane < L) ? tok[lane] : (int64_t)-1;
     for (int j = 1; j < nc; ++j) {
         for (int ps = (j - 1) * Br; ps < j * Br; ps += 64) {
+            // a piece and the next one read [ps, ps + 128): move the window to start at ps
+            // when that runs past it (the current piece's tokens were read one piece ahead;
+            // every wave is done with the old window at the barrier)
+            if (ps + 128 > w0 + WL && w0 + WL < L) {
+                __syncthreads();
+                stage(ps);
+                __syncthreads();
+            }
             const int len = min(64, j * Br - ps);
             const int64_t tv = tnext;
             const int pn = ps + len;
-            tnext = (pn < pend && pn + lane < L) ? tok[pn + lane] : (int64_t)-1;
+            tnext = (pn < pend && pn + lane < L) ? tok[pn + lane - w0] : (int64_t)-1;
             bool drop = false;
             uint64_t keep = ~0ull;
             if (doc_ids) {
-                uint64_t rb = bits64_at(rbits, ps);
+                uint64_t rb = bits64_at(rbits, ps - w0);
                 if (len < 64) rb &= (1ull << len) - 1;
                 if (rb) {
                     const int rl = 63 - __builtin_clzll(rb);  // last change in the piece
@@ -805,15 +891,19 @@ ema_boundary_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int L
                     keep = ~((1ull << rl) - 1);
                 }
             }
-            float pw[RPL];
+            float pw[RPL], pwl[RPL];
 #pragma unroll
-            for (int r = 0; r < RPL; ++r) pw[r] = len == 64 ? p64[r] : pow_steps(hi[r], lo[r], len);
+            for (int r = 0; r < RPL; ++r) {  // len is 64 or brem
+                pw[r] = len == 64 ? p64[r] : prem[r];
+                pwl[r] = len == 64 ? p64l[r] : preml[r];
+            }
 #pragma unroll
             for (int s = 0; s < SPW; ++s) {
                 const bool hit = lane < len && uu[s] >= 0 && tv == uu[s];
                 uint64_t m = __ballot(hit) & keep;
 #pragma unroll
-                for (int r = 0; r < RPL; ++r) c[s][r] = drop ? 0.f : c[s][r] * pw[r];
+                for (int r = 0; r < RPL; ++r)
+                    c[s][r] = drop ? 0.f : __builtin_fmaf(c[s][r], pw[r], c[s][r] * pwl[r]);
                 while (m) {  // uniform across the wave
                     const int p = __builtin_ctzll(m);
                     m &= m - 1;
@@ -845,23 +935,35 @@ static int set_lds(F kernel, size_t bytes) {
 
 using namespace mb;
 
-extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x_stride_l, int B,
-                                 int L, const float* rhos, int N, int64_t vocab_size,
-                                 const float* c_init, const int64_t* c_init_keys, int K,
-                                 const int64_t* doc_ids, float* C_seq, float* state_out,
-                                 int32_t* stamp_out, void* stream) {
-    MB_REQUIRE(B >= 0 && L >= 0, "mb_ema_query_scan: negative B=%d or L=%d", B, L);
-    MB_REQUIRE(N >= 1, "mb_ema_query_scan: N=%d must be >= 1", N);
-    if (!c_init || !c_init_keys) K = 0;
-    MB_REQUIRE(K >= 0, "mb_ema_query_scan: negative K=%d", K);
-    if (B == 0 || L == 0) return MB_OK;
-    MB_REQUIRE(x && rhos && C_seq, "mb_ema_query_scan: x, rhos and C_seq must be non-null");
-    if (L > kMaxScanL)
-        return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d exceeds the on-chip limit %d", L,
-                    kMaxScanL);
-    if ((int64_t)L * N >= (1ll << 31) || (int64_t)K * N >= (1ll << 31) || K >= (1 << 24))
-        return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d, K=%d, N=%d: rows of one sequence must "
-                    "stay below 2^31 elements (and K below 2^24)", L, K, N);
+namespace mb {
+
+// Pieces of a long query scan: steps [T0, T0 + kScanPiece) per launch (hash grouping fits LDS
+// at this length); kMaxScanL and shorter sequences run in one launch.
+constexpr int kScanPiece = 2048;
+
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
+// last_pos[b, x[b, t]] = the largest t in [T0, T0 + Lp) (ids outside [0, V) are skipped).
+__global__ void query_piece_last_kernel(const int64_t* __restrict__ x, int64_t sb, int64_t sl, int T0,
+                                        int Lp, int64_t V, int32_t* __restrict__ last_pos) {
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= Lp) return;
+    const int64_t u = x[(int64_t)b * sb + (int64_t)(T0 + i) * sl];
+    if (u >= 0 && u < V) atomicMax(&last_pos[(int64_t)b * V + u], T0 + i);
+}
+
+// One launch of the query scan over steps [T0, T0 + L) of sequences of Ltot steps (PIECE
+// when last_pos is given).
+static int query_scan_launch(const int64_t* x, int64_t x_stride_b, int64_t x_stride_l, int B, int L,
+                             const float* rhos, int N, int64_t vocab_size, const float* c_init,
+                             const int64_t* c_init_keys, int K, const int64_t* doc_ids, float* C_seq,
+                             float* state_out, int32_t* stamp_out, int T0, int Ltot,
+                             const int32_t* last_pos, hipStream_t st) {
+    const bool piece = last_pos != nullptr;
     const int pb = ceil_log2(L);
     const bool wide = vocab_size > 0 && (pb >= 32 || (uint64_t)vocab_size > (1ull << (32 - pb)));
     // token bits the radix sort orders by: those of vocab_size - 1 (ids are < vocab_size)
@@ -885,37 +987,43 @@ extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x
     // Grouping by hash when the token keys are 32-bit and its tables fit beside the index
     // (2^lgTS >= 2L slots); otherwise by the radix sort.
     const int lgTS = pb + 1;
-    const ScanLds lay_hash(L, 1 << pb, 4, kScanThreads, ncut, nH, ceil_log2(slice_w), lgTS);
+    const ScanLds lay_hash(L, 1 << pb, 4, kScanThreads, ncut, nH, ceil_log2(slice_w), lgTS, piece);
     const bool hash = !wide && pb >= 1 && L <= 64 * 64 && lay_hash.total <= kMaxLds;
-    const ScanLds lay = hash ? lay_hash : ScanLds(L, 1 << pb, wide ? 8 : 4, kScanThreads, ncut, nH, ceil_log2(slice_w));
+    const ScanLds lay = hash ? lay_hash
+                             : ScanLds(L, 1 << pb, wide ? 8 : 4, kScanThreads, ncut, nH, ceil_log2(slice_w), 0, piece);
     if (lay.total > kMaxLds)
         return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d with vocab %lld needs %zu B of LDS",
                     L, (long long)vocab_size, lay.total);
     dim3 grid(B, ns);
-    hipStream_t st = (hipStream_t)stream;
-#define MB_LAUNCH_SCAN_H(KT, V, DOCS, HASH)                                                    \
+#define MB_LAUNCH_SCAN_P(KT, V_, DOCS, HASH, PIECE)                                             \
     do {                                                                                       \
         auto kfn = L <= 64 * kScanRoundsSmall * (kScanThreads / 64)                            \
-                       ? ema_query_scan_kernel<KT, V, DOCS, kScanRoundsSmall, HASH>            \
-                       : ema_query_scan_kernel<KT, V, DOCS, kScanRoundsLarge, HASH>;           \
+                       ? ema_query_scan_kernel<KT, V_, DOCS, kScanRoundsSmall, HASH, PIECE>    \
+                       : ema_query_scan_kernel<KT, V_, DOCS, kScanRoundsLarge, HASH, PIECE>;   \
         int rc = set_lds(kfn, lay.total);                                                      \
         if (rc) return rc;                                                                     \
         hipLaunchKernelGGL(kfn, grid, dim3(kScanThreads), lay.total, st, x, x_stride_b,        \
                            x_stride_l, L, rhos, N, c_init, c_init_keys, K, doc_ids, C_seq,     \
-                           state_out, stamp_out, pb, tok_bits, slice_w, lgS, ncut, lgTS);     \
+                           state_out, stamp_out, pb, tok_bits, slice_w, lgS, ncut, lgTS, T0,    \
+                           Ltot, last_pos, vocab_size);                                        \
     } while (0)
-#define MB_LAUNCH_SCAN(KT, V, DOCS)                                                            \
+#define MB_LAUNCH_SCAN_H(KT, V_, DOCS, HASH)                                                    \
     do {                                                                                       \
-        if (hash) MB_LAUNCH_SCAN_H(KT, V, DOCS, true);                                         \
-        else MB_LAUNCH_SCAN_H(KT, V, DOCS, false);                                             \
+        if (piece) MB_LAUNCH_SCAN_P(KT, V_, DOCS, HASH, true);                                  \
+        else MB_LAUNCH_SCAN_P(KT, V_, DOCS, HASH, false);                                       \
     } while (0)
-#define MB_LAUNCH_SCAN_D(KT, V)                                     \
+#define MB_LAUNCH_SCAN(KT, V_, DOCS)                                                            \
+    do {                                                                                       \
+        if (hash) MB_LAUNCH_SCAN_H(KT, V_, DOCS, true);                                        \
+        else MB_LAUNCH_SCAN_H(KT, V_, DOCS, false);                                            \
+    } while (0)
+#define MB_LAUNCH_SCAN_D(KT, V_)                                    \
     do {                                                            \
-        if (doc_ids) MB_LAUNCH_SCAN(KT, V, true);                   \
-        else MB_LAUNCH_SCAN(KT, V, false);                          \
+        if (doc_ids) MB_LAUNCH_SCAN(KT, V_, true);                  \
+        else MB_LAUNCH_SCAN(KT, V_, false);                         \
     } while (0)
     if (wide) {  // (never hashed)
-#define MB_LAUNCH_SCAN_W(V, DOCS) MB_LAUNCH_SCAN_H(uint64_t, V, DOCS, false)
+#define MB_LAUNCH_SCAN_W(V_, DOCS) MB_LAUNCH_SCAN_H(uint64_t, V_, DOCS, false)
         if (vec4) {
             if (doc_ids) MB_LAUNCH_SCAN_W(4, true); else MB_LAUNCH_SCAN_W(4, false);
         } else {
@@ -928,7 +1036,81 @@ extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x
 #undef MB_LAUNCH_SCAN_D
 #undef MB_LAUNCH_SCAN
 #undef MB_LAUNCH_SCAN_H
+#undef MB_LAUNCH_SCAN_P
     return check_launch("mb_ema_query_scan");
+}
+
+}  // namespace mb
+
+extern "C" int64_t mb_ema_query_scan_workspace(int B, int L, int64_t vocab_size) {
+    if (B < 0 || L < 0) {
+        fail(MB_ERR_INVALID_ARGUMENT, "mb_ema_query_scan_workspace: negative B=%d or L=%d", B, L);
+        return -1;
+    }
+    if (L <= kMaxScanL || B == 0) return 0;
+    if (vocab_size < 1) {
+        fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan_workspace: L=%d > %d needs vocab_size >= 1", L, kMaxScanL);
+        return -1;
+    }
+    return (int64_t)B * vocab_size * 4;
+}
+
+extern "C" int mb_ema_query_scan_ws(const int64_t* x, int64_t x_stride_b, int64_t x_stride_l, int B, int L,
+                                    const float* rhos, int N, int64_t vocab_size, const float* c_init,
+                                    const int64_t* c_init_keys, int K, const int64_t* doc_ids, float* C_seq,
+                                    float* state_out, int32_t* stamp_out, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+    MB_REQUIRE(B >= 0 && L >= 0, "mb_ema_query_scan: negative B=%d or L=%d", B, L);
+    MB_REQUIRE(N >= 1, "mb_ema_query_scan: N=%d must be >= 1", N);
+    if (!c_init || !c_init_keys) K = 0;
+    MB_REQUIRE(K >= 0, "mb_ema_query_scan: negative K=%d", K);
+    if (B == 0 || L == 0) return MB_OK;
+    MB_REQUIRE(x && rhos && C_seq, "mb_ema_query_scan: x, rhos and C_seq must be non-null");
+    if ((int64_t)std::min(L, kMaxScanL) * N >= (1ll << 31) || (int64_t)K * N >= (1ll << 31) || K >= (1 << 24))
+        return fail(MB_ERR_UNSUPPORTED, "mb_ema_query_scan: L=%d, K=%d, N=%d: rows of one scan must "
+                    "stay below 2^31 elements (and K below 2^24)", L, K, N);
+    hipStream_t st = (hipStream_t)stream;
+    if (L <= kMaxScanL)
+        return query_scan_launch(x, x_stride_b, x_stride_l, B, L, rhos, N, vocab_size, c_init, c_init_keys, K,
+                                 doc_ids, C_seq, state_out, stamp_out, 0, L, nullptr, st);
+    // Longer sequences: pieces of kScanPiece steps, one launch each, the last positions of
+    // every token so far in the workspace ([B, vocab_size] int32) between them.
+    const int64_t need = mb_ema_query_scan_workspace(B, L, vocab_size);
+    if (need < 0) return MB_ERR_UNSUPPORTED;
+    if (!workspace || workspace_bytes < need)
+        return fail(MB_ERR_WORKSPACE, "mb_ema_query_scan: L=%d > %d runs in pieces and needs %lld B of "
+                    "workspace (mb_ema_query_scan_workspace), got %lld", L, kMaxScanL, (long long)need,
+                    (long long)(workspace ? workspace_bytes : 0));
+    MB_REQUIRE(((uintptr_t)workspace & 3) == 0, "mb_ema_query_scan: workspace must be 4-byte aligned");
+    MB_REQUIRE((int64_t)L + kScanPiece < (1ll << 31), "mb_ema_query_scan: L=%d too long", L);
+    int32_t* last_pos = static_cast<int32_t*>(workspace);
+    const int64_t n = (int64_t)B * vocab_size;
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)), dim3(256), 0, st,
+                       last_pos, n, (int32_t)-1);
+    int rc = check_launch("mb_ema_query_scan (workspace fill)");
+    if (rc) return rc;
+    for (int T0 = 0; T0 < L; T0 += kScanPiece) {
+        const int Lp = std::min(kScanPiece, L - T0);
+        rc = query_scan_launch(x, x_stride_b, x_stride_l, B, Lp, rhos, N, vocab_size, c_init, c_init_keys, K,
+                               doc_ids, C_seq, state_out, stamp_out, T0, L, last_pos, st);
+        if (rc) return rc;
+        if (T0 + Lp < L) {
+            hipLaunchKernelGGL(query_piece_last_kernel, dim3((Lp + 255) / 256, B), dim3(256), 0, st, x,
+                               x_stride_b, x_stride_l, T0, Lp, vocab_size, last_pos);
+            rc = check_launch("mb_ema_query_scan (last positions)");
+            if (rc) return rc;
+        }
+    }
+    return MB_OK;
+}
+
+extern "C" int mb_ema_query_scan(const int64_t* x, int64_t x_stride_b, int64_t x_stride_l, int B,
+                                 int L, const float* rhos, int N, int64_t vocab_size,
+                                 const float* c_init, const int64_t* c_init_keys, int K,
+                                 const int64_t* doc_ids, float* C_seq, float* state_out,
+                                 int32_t* stamp_out, void* stream) {
+    return mb_ema_query_scan_ws(x, x_stride_b, x_stride_l, B, L, rhos, N, vocab_size, c_init, c_init_keys, K,
+                                doc_ids, C_seq, state_out, stamp_out, nullptr, 0, stream);
 }
 
 extern "C" int mb_ema_boundary_states(const int64_t* x, int64_t x_stride_b, int64_t x_stride_l,
@@ -945,11 +1127,10 @@ extern "C" int mb_ema_boundary_states(const int64_t* x, int64_t x_stride_b, int6
     if (B == 0 || K == 0) return MB_OK;
     MB_REQUIRE(unique && rhos && C_bounds, "mb_ema_boundary_states: null pointer");
     MB_REQUIRE(L == 0 || x, "mb_ema_boundary_states: x is null");
-    if (L > kMaxScanL)
-        return fail(MB_ERR_UNSUPPORTED, "mb_ema_boundary_states: L=%d exceeds the on-chip limit %d",
-                    L, kMaxScanL);
+    MB_REQUIRE((int64_t)L + 128 < (1ll << 31), "mb_ema_boundary_states: L=%d too long", L);
     const int nc = L > 0 ? (L + Br - 1) / Br : 1;  // an empty sequence still stores c0 once
-    const size_t lds = (size_t)L * 8 + (size_t)((L >> 6) + 2) * 8;
+    const int WL = std::min(L, kBoundWin);
+    const size_t lds = (size_t)WL * 8 + (size_t)((WL >> 6) + 2) * 8;
     if (lds > kMaxLds)
         return fail(MB_ERR_UNSUPPORTED, "mb_ema_boundary_states: L=%d needs %zu B of LDS", L, lds);
     if (Np > 256)

@@ -38,11 +38,17 @@ def _scan(x, rhos, vocab_size, c_init, c_init_keys, doc_ids, state, stamps):
         K = keys.shape[1]
     docs = None if doc_ids is None else doc_ids.to(torch.int64).contiguous()
     C_seq = torch.empty(B, L, N, dtype=torch.float32, device=dev)
+    # Sequences longer than the one-launch limit run in pieces with a [B, vocab_size] int32
+    # table of each token's last position between them (mb_ema_query_scan_workspace bytes).
+    nws = _lib.lib().mb_ema_query_scan_workspace(B, L, int(vocab_size))
+    if nws < 0:
+        raise _lib.HipKernelError("mb_ema_query_scan_workspace: " + _lib.lib().mb_last_error().decode(errors="replace"))
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws > 0 else None
     with torch.cuda.device(dev):
-        _lib.call("mb_ema_query_scan", _lib.ptr(x), x.stride(0), x.stride(1), B, L,
+        _lib.call("mb_ema_query_scan_ws", _lib.ptr(x), x.stride(0), x.stride(1), B, L,
                   _lib.ptr(rhos_f), N, int(vocab_size), _lib.ptr(ci), _lib.ptr(keys), K,
                   _lib.ptr(docs), _lib.ptr(C_seq), _lib.ptr(state) if K else None,
-                  _lib.ptr(stamps) if K else None, _lib.stream(dev))
+                  _lib.ptr(stamps) if K else None, _lib.ptr(ws), int(nws), _lib.stream(dev))
     return C_seq
 
 
@@ -67,6 +73,8 @@ def compute_query_ema_history(x, rhos, vocab_size, c_init=None, c_init_keys=None
     from 0 (triton_ema_query.py:51-57, 104-110).
 
     x [B, L] int64, rhos [N], c_init [B, K, N], c_init_keys [B, K], doc_ids [B, L].
+    Token ids must lie in [0, vocab_size) (as the reference's [B, V+1] tables need).  Any L:
+    beyond 8192 steps the scan runs in 2048-step pieces.
     Returns C_seq [B, L, N] float32.  With ``return_state=True`` also returns
     (state, stamps): ``state`` [B, K, N] is c_init with each key that occurs in the chunk
     replaced by its lazy state after its last occurrence (C_seq there + 1) and ``stamps``

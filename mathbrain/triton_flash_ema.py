@@ -107,7 +107,11 @@ def _build_unique_index(x, device, width=None):
         ids, _ = unique_rows(x, K_max)
         return ids.to(x.dtype), K_max
     ids, counts = unique_rows(x, max(L, 16))
-    K_max = max(int(counts.max()) if counts.numel() else 0, 16)
+    lo, hi = (int(v) for v in counts.aminmax()) if counts.numel() else (0, 0)
+    if lo < 0:
+        raise _lib.HipKernelError("_build_unique_index: a row of more than 8192 ids spans 2^32 or more "
+                                  "(rows that long are sorted as 32-bit offsets)")
+    K_max = max(hi, 16)
     return ids[:, :K_max].contiguous().to(x.dtype), K_max
 
 

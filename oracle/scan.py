@@ -142,6 +142,48 @@ def boundary_states_closed_form(x, unique, rhos, Br, c_init=None):
     return out
 
 
+def boundary_states_f64(x, unique, rhos, Br, c_init=None, doc_ids=None):
+    """The same states as ``boundary_states`` in float64, chunk by chunk with numpy:
+    S_{j+1} = S_j rho^Br + sum_{s in chunk j, x_s = u_k} rho^((j+1) Br - 1 - s), a document
+    change at step s zeroing the state before that step's occurrence (triton_flash_ema.py:
+    69-75).  For long sequences, where the fp32 step-by-step restatement accumulates its
+    own rounding (one per step) and cannot check a kernel to 1e-5; pinned to the closed
+    form and to the fp32 restatement on short inputs (tests/test_oracle_scan.py)."""
+    x = np.asarray(_as(x, np.int64))
+    unique = np.asarray(_as(unique, np.int64))
+    rhos = np.asarray(_as(rhos, np.float32), dtype=np.float64)
+    B, L = x.shape
+    K = unique.shape[1]
+    N = rhos.shape[0]
+    nc = max(1, -(-L // Br))
+    out = np.zeros((B, nc, K, N))
+    logr = np.log(rhos)
+    for b in range(B):
+        S = np.zeros((K, N)) if c_init is None else np.asarray(_as(c_init, np.float64))[b, :, :N].copy()
+        valid = unique[b] != -1
+        doc = None if doc_ids is None else np.asarray(_as(doc_ids, np.int64))[b]
+        for j in range(nc):
+            out[b, j] = S
+            t0, t1 = j * Br, min((j + 1) * Br, L)
+            if t0 >= t1:
+                continue
+            n = t1 - t0
+            steps = np.arange(t0, t1)
+            keep_from = 0  # the last document change in the chunk drops what came before
+            if doc is not None:
+                chg = [s for s in steps if s > 0 and doc[s] != doc[s - 1]]
+                if chg:
+                    keep_from = chg[-1] - t0
+                    S = np.zeros_like(S)
+            hits = (x[b, t0:t1][None, :] == unique[b][:, None]) & valid[:, None]   # [K, n]
+            hits[:, :keep_from] = False
+            w = np.exp(np.outer(np.arange(n - 1, -1, -1), logr))                  # rho^(n-1-i) [n, N]
+            S = S * np.exp(n * logr)[None, :] + hits.astype(np.float64) @ w
+            if n < Br and j + 1 < nc:
+                raise AssertionError("only the last chunk can be short")
+    return out
+
+
 def query_scan_dense_loop(x, rhos, vocab_size, c_init=None, c_init_keys=None, doc_ids=None):
     """C_seq [B, L, N] float32 by the algorithm of compute_query_ema_history_pt
     (mathbrain/triton_ema_query.py:67-117): per-vocabulary tables of the last position

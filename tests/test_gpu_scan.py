@@ -199,10 +199,12 @@ def test_gpu_scan_more_tokens_than_lds_state(L, V, N, docs):
                 assert sp[b, k] == -1
 
 
-def test_gpu_scan_too_long_raises():
+def test_gpu_scan_long_without_vocab_raises():
+    """Beyond 8192 steps the scan runs in pieces with a [B, vocab_size] table of last
+    positions, so it needs the vocabulary size."""
     from mathbrain._lib import HipKernelError
-    with pytest.raises(HipKernelError, match="unsupported"):
-        _scan(np.zeros((1, 8193), np.int64), np.array([0.5], np.float32), 10)
+    with pytest.raises(HipKernelError, match="vocab_size"):
+        _scan(np.zeros((1, 8193), np.int64), np.array([0.5], np.float32), 0)
 
 
 def test_gpu_scan_cfg3_full_size():

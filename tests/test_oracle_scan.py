@@ -221,3 +221,24 @@ def test_dense_loop_equals_c_restatement(seed):
         a = scan.query_scan_dense_loop(x, rhos, V, c_init, keys, d)
         b = scan.query_scan(x, rhos, V, c_init, keys, d)
         assert np.allclose(a, b, rtol=1e-5, atol=1e-6), float(np.abs(a - b).max())
+
+
+@pytest.mark.parametrize("docs", [False, True])
+def test_boundary_states_f64_matches_closed_form_and_fp32_restatement(docs):
+    """The float64 chunked boundary states (used to check long sequences, where the fp32
+    step-by-step restatement carries one rounding per step) agree with the closed form in
+    float64 and with the fp32 restatement to its rounding."""
+    rng = np.random.default_rng(3 + docs)
+    B, L, V, N, Br = 2, 150, 12, 5, 16
+    x = rng.integers(0, V, (B, L))
+    u = np.stack([np.sort(rng.choice(V, 8, replace=False)) for _ in range(B)])
+    u[0, -1] = -1
+    rh = rng.uniform(0.5, 0.99, N).astype(np.float32)
+    c0 = rng.random((B, 8, N)).astype(np.float32)
+    doc = np.sort(rng.integers(0, 4, (B, L)), axis=1) if docs else None
+    a = scan.boundary_states_f64(x, u, rh, Br, c0, doc)
+    b = scan.boundary_states(x, u, rh, Br, c0, doc)
+    assert np.abs(a - b).max() / np.abs(a).max() < 1e-6
+    if not docs:
+        c = scan.boundary_states_closed_form(x, u, rh.astype(np.float64), Br, c0)
+        assert np.abs(a - c).max() < 1e-12
