@@ -125,15 +125,20 @@ def attention_case(seed=0, config="cfg2"):
 
 
 def attention_step(c, timers=None, precision="bf16"):
-    from mathbrain.triton_flash_ema import (flash_ema_backward, flash_ema_forward, keep_scores,
-                                            precompute_boundaries)
-    # the forward keeps its scores for the backward when FlashEMAFunction would
+    from mathbrain.triton_flash_ema import (_forward_with_scores, _prec, flash_ema_backward,
+                                            flash_ema_forward, keep_scores, precompute_boundaries)
+    # the forward keeps its scores for the backward when FlashEMAFunction would (the same
+    # call FlashEMAFunction makes then)
     keep = keep_scores(c["B"], c["H"], c["K"], c["L"])
     Cb = precompute_boundaries(c["x"], c["unique"], c["rhos"], 64, c["c_base"])
     if timers is not None:
         timers["fwd"][0].record()
-    res = flash_ema_forward(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
-                            c["unique"], c["K"], Cb, precision=precision, return_scores=keep)
+    if keep:
+        res = _forward_with_scores(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
+                                   c["unique"], Cb, True, 64, True, _prec(precision))
+    else:
+        res = flash_ema_forward(c["Q"], c["x"], c["E_k"], c["E_v"], c["W"], c["rhos"], c["V"],
+                                c["unique"], c["K"], Cb, precision=precision)
     O, LSE = res[0], res[1]
     if timers is not None:
         timers["fwd"][1].record()

@@ -362,7 +362,11 @@ int mb_corpus_states(const int64_t *order, const int64_t *chain, int64_t T, cons
  * mb_corpus_states; the scratch is a 32 MiB device array inside the library (one per GPU,
  * held until the process ends), so mb_corpus_states_workspace(T, N) must not exceed
  * 32 MiB (about 44 M tokens at N = 64): larger calls return MB_ERR_WORKSPACE.  The call
- * allocates nothing.  Calls that overlap on one GPU share that scratch and race.
+ * allocates nothing.  Calls on one GPU take the scratch one after the other in the order
+ * the host makes them, whatever their streams: each call's stream waits for an event the
+ * previous call recorded after its last pass (the event is created once per device, with
+ * the scratch address).  Under graph capture that ordering is left to the graph, and
+ * replays that overlap on one GPU race.
  */
 int mb_corpus_states_noalloc(const int64_t *order, const int64_t *chain, int64_t T,
                              const float *rhos, int N, float *states, void *stream);

@@ -104,7 +104,11 @@ constexpr int kTablePrefetch = 4;
 // Hash grouping: a token with at least long_run(L) positions (at most kMaxLongRuns such
 // tokens) is ranked through a position bitmap instead of by counting.
 constexpr int kMaxLongRuns = 128;
-__host__ __device__ inline int long_run(int L) { return L / kMaxLongRuns > 16 ? (L + kMaxLongRuns - 1) / kMaxLongRuns : 16; }
+// (T = ceil(L / kMaxLongRuns), at least 16: then at most L / T <= kMaxLongRuns runs reach T)
+__host__ __device__ inline int long_run(int L) {
+    const int t = (L + kMaxLongRuns - 1) / kMaxLongRuns;
+    return t > 16 ? t : 16;
+}
 
 struct ScanLds {
     size_t keys, chain_start, elem_chain, chain_key, agg, aggr, lowT, highT, scan_scratch, chain_prev;

@@ -355,6 +355,10 @@ namespace {
 constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxScratchDevices];
+// Per device, the event recorded after the last call's final pass: the next call's stream
+// waits for it, so that calls on different streams take the scratch array one after the
+// other instead of overwriting each other's aggregates.
+hipEvent_t g_scratch_done[kMaxScratchDevices];
 
 // The current device's address of `scratch`, looked up once per device (with that device
 // current) and kept.
@@ -371,6 +375,11 @@ int scratch_address(void** out) {
         if (e != hipSuccess || !p)
             return fail((int)(e != hipSuccess ? e : hipErrorInvalidSymbol),
                         "mb_corpus_states_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        hipEvent_t ev = nullptr;
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess)
+            return fail((int)e, "mb_corpus_states_noalloc: hipEventCreateWithFlags: %s", hipGetErrorString(e));
+        g_scratch_done[dev] = ev;
         g_scratch_ptr[dev] = p;
     }
     *out = g_scratch_ptr[dev];
@@ -450,7 +459,27 @@ extern "C" int mb_corpus_states_noalloc(const int64_t* order, const int64_t* cha
     void* work = nullptr;
     int rc = scratch_address(&work);
     if (rc) return rc;
-    return corpus_states_run(order, chain, T, rhos, N, states, work, (hipStream_t)stream);
+    hipStream_t st = (hipStream_t)stream;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail((int)e, "mb_corpus_states_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    // Calls on one device run their passes one call after the other, in the order the host
+    // makes them: each waits for the previous call's event and records its own.  (Under
+    // graph capture the graph's own order applies and replays that overlap race.)
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+        (void)hipGetLastError();
+        cap = hipStreamCaptureStatusNone;
+    }
+    const bool serial = cap == hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (serial && (e = hipStreamWaitEvent(st, g_scratch_done[dev], 0)) != hipSuccess)
+        return fail((int)e, "mb_corpus_states_noalloc: hipStreamWaitEvent: %s", hipGetErrorString(e));
+    rc = corpus_states_run(order, chain, T, rhos, N, states, work, st);
+    if (rc) return rc;
+    if (serial && (e = hipEventRecord(g_scratch_done[dev], st)) != hipSuccess)
+        return fail((int)e, "mb_corpus_states_noalloc: hipEventRecord: %s", hipGetErrorString(e));
+    return MB_OK;
 }
 
 extern "C" int mb_slot_lists(const int32_t* tokens, const int32_t* next_pos, int64_t T, int64_t V,

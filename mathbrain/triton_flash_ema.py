@@ -291,8 +291,9 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
     ``absent_mass`` (the default) the softmax covers all V_total slots as the dense PyTorch
     reference (flash_ema_attention.py:76-77) does; ``absent_mass=False`` gives the Triton
     kernel's softmax over the valid slots only (triton_flash_ema.py:215-229).  With
-    ``return_scores`` a sixth element holds the scores * log2(e) as [B, H, K_max, L]
-    (what ``flash_ema_backward(scores=...)`` consumes instead of recomputing them).
+    ``return_scores`` a sixth element holds the scores * log2(e) as [B, H, K_max, L], -inf in
+    the rows of padding slots (what ``flash_ema_backward(scores=...)`` consumes instead of
+    recomputing them).
     ``precision``: the gate arithmetic (see PRECISIONS): "bf16" (default) splits the gate
     operands into fp16 hi + lo pairs (N <= 64, head_dim <= 64; single fp16 operands
     beyond), "fp16" takes single fp16 operands (faster; for small scores only), "fp32" also
@@ -310,6 +311,20 @@ def flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_
         if Ek.dim() == 2:
             return O, LSE, C_bounds, Ek, Ev
         return O, LSE, C_bounds, Ek.reshape(B, K, H, hd), Ev.reshape(B, K, H, hd)
+    res = _forward_with_scores(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, C_bounds,
+                               use_silu, Br, absent_mass, prec)
+    # the kernel writes the rows of valid slots only: padding slots' rows hold -inf (score
+    # of no slot), as a softmax over them expects
+    res[5].masked_fill_((unique_tensor < 0)[:, None, :, None], float("-inf"))
+    return res
+
+
+def _forward_with_scores(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor, C_bounds,
+                         use_silu, Br, absent_mass, prec):
+    """flash_ema_forward's six outputs with the scores [B, H, K_max, L]; the rows of padding
+    slots are left unwritten (the backward never reads them)."""
+    B, H, L, hd = Q.shape
+    K = unique_tensor.shape[1]
     O, LSE, S2, Ek, Ev, table = _fwd_impl(Q, x, E_k_active, E_v_active, W_pe, rhos, unique_tensor,
                                           C_bounds, V_total, use_silu, Br, absent_mass, True, prec)
     if table:
@@ -481,9 +496,14 @@ class FlashEMAFunction(torch.autograd.Function):
         nbytes = _reserve_scores(Q, unique_tensor.shape[1])
         keep = nbytes > 0
         try:
-            res = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
-                                    K_max, C_bounds, use_silu, Br, absent_mass, return_scores=keep,
-                                    precision=precision)
+            if keep:
+                if unique_tensor.shape[1] != K_max:
+                    raise ValueError(f"unique_tensor has {unique_tensor.shape[1]} slots but K_max={K_max}")
+                res = _forward_with_scores(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
+                                           C_bounds, use_silu, Br, absent_mass, _prec(precision))
+            else:
+                res = flash_ema_forward(Q, x, E_k_active, E_v_active, W_pe, rhos, V_total, unique_tensor,
+                                        K_max, C_bounds, use_silu, Br, absent_mass, precision=precision)
         except BaseException:
             if keep:
                 score_budget.release(Q.device, nbytes)

@@ -285,7 +285,8 @@ def test_bwd_flags(use_silu, absent_mass, stored_scores, precision):
 
 
 def test_fwd_scores_output():
-    """The optional scores output is s * log2(e) = LSE-consistent log-softmax numerators."""
+    """The optional scores output is s * log2(e) = LSE-consistent log-softmax numerators, and
+    -inf in the rows of padding slots."""
     from mathbrain.triton_flash_ema import flash_ema_forward
     c = make_case(2, 50, 120, 4, 32, 16, warmup=40, seed=8, pad_slots=3)
     cu = lambda t: t.cuda()
@@ -295,6 +296,7 @@ def test_fwd_scores_output():
     S2 = S2.cpu().double() * np.log(2.0)               # natural-log scores [B, H, K, L]
     valid = (c["unique"] >= 0)
     kb = valid.sum(1).double()
+    assert torch.isneginf(S2.permute(0, 2, 1, 3)[~valid]).all()   # padding slots' rows
     for b in range(2):
         s = S2[b][:, valid[b]]                         # [H, K_b, L]
         lse = torch.logsumexp(torch.cat([s, torch.log(c["V"] - kb[b]).expand(s.shape[0], 1, s.shape[2])], 1), 1)

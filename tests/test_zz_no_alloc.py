@@ -87,3 +87,31 @@ def test_noalloc_rejects_beyond_scratch():
                                     dummy.data_ptr(), None)
     assert rc == _lib.MB_ERR_WORKSPACE
     assert b"scratch" in L.mb_last_error()
+
+
+def test_noalloc_calls_on_two_streams_do_not_race():
+    """Two calls issued back to back on two streams (no host synchronisation between them)
+    share the one scratch array: the library orders them through its per-device event, so
+    both results equal the workspace entry point's, bit for bit."""
+    _lib, L = _get_lib()
+    from mathbrain.data import chain_order, corpus_states
+    dev = torch.device("cuda:0")
+    cases = []
+    for T, V, nd, N, seed in [(600_000, 50257, 200, 64, 7), (300_000, 20000, 90, 64, 8)]:
+        tokens, doc_ids, rhos = _corpus(T, V, nd, N, seed)
+        tk = torch.from_numpy(tokens).to(dev)
+        dc = torch.from_numpy(doc_ids).to(dev)
+        rh = torch.from_numpy(rhos).to(dev)
+        want = corpus_states(tk, dc, rh)
+        chain, order = chain_order(tk, dc)
+        got = torch.full((T, N), float("nan"), device=dev)
+        cases.append((order, chain, T, rh, N, got, want))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    for (order, chain, T, rh, N, got, _), s in zip(cases, streams):
+        rc = L.mb_corpus_states_noalloc(order.data_ptr(), chain.data_ptr(), T, rh.data_ptr(), N,
+                                        got.data_ptr(), s.cuda_stream)
+        assert rc == 0, L.mb_last_error()
+    torch.cuda.synchronize()
+    for (_, _, _, _, _, got, want) in cases:
+        assert torch.equal(got, want)
