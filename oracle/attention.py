@@ -108,6 +108,12 @@ def _round_gate_counter(c, gate_round):
     return c.float().to(torch.float16 if gate_round != "bf16" else torch.bfloat16).to(c.dtype)
 
 
+def _gate_product(c, W):
+    """The gate GEMM c_dec @ W_pe of both sparse forms (one place, so that a check can
+    substitute another evaluation of it)."""
+    return c @ W
+
+
 def _steps(L, t_eval):
     return list(range(L)) if t_eval is None else sorted({int(t) for t in t_eval})
 
@@ -147,7 +153,7 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
             match = (x[:, t].unsqueeze(1) == unique) & valid
             C = c_dec + match.unsqueeze(-1).to(dt)
             continue
-        pre = (_round_gate_counter(c_dec, gate_round) @ W).reshape(B, K, H, hd)
+        pre = _gate_product(_round_gate_counter(c_dec, gate_round), W).reshape(B, K, H, hd)
         g = F.silu(pre) if use_silu else pre
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
         s = (q_t * Ek * g).sum(-1) / math.sqrt(hd)                   # [B,K,H]
@@ -216,7 +222,7 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
             continue
         i = slot[t]
         cg = _round_gate_counter(c_dec, gate_round)
-        pre = (cg @ W).reshape(B, K, H, hd)
+        pre = _gate_product(cg, W).reshape(B, K, H, hd)
         g = F.silu(pre) if use_silu else pre
         gp = silu_grad(pre) if use_silu else torch.ones_like(pre)
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
