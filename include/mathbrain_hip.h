@@ -193,7 +193,9 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
  * and by default for N > 64 or hd 128 (where the lo tiles do not fit in LDS), the gate
  * takes single fp16 operands.  The fp16 counters are clamped to 65440 at the chunk start;
  * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to ~45,000
- * steps, which the Python entry points check (faster rates are refused there).
+ * steps, which the Python entry points check (rates with longer half-lives are refused
+ * there), so only a caller-supplied initial state (C_bounds from a c_init) above 65440
+ * reaches the clamp.
  *
  * Supported: hd in {32, 64, 128} (32 or 64 with MB_FLASH_FP32), 1 <= H <= 64, N <= 128 (N <= 64
  * with MB_FLASH_FP32), Br <= 32 or Br == 64.  At hd 128 each head takes two waves, one per

@@ -15,10 +15,15 @@
 // Gate operands are fp16 (c_dec and W_pe * log2 e, round to nearest even), not bf16: the
 // gate pre-activation sum_n c_n W_n cancels, and the dW_pe sums over thousands of steps
 // cancel further, so bf16's 8-bit significand moved dW_pe by ~2.5e-2 (norm-wise, against
-// float64) at T = 4096 with long half-lives; fp16's 11 bits bring that to ~4e-3.  The
-// counter stays in fp16 range: the chunk-start state is clamped to kCMax at load, the
-// window adds at most kMaxWin, and rho <= 1.  dpre, whose scale is unbounded, keeps bf16
-// for the dW_pe product, so that product takes the bf16 copy of the tile.
+// float64) at T = 4096 with long half-lives.  Where the lo tiles fit (N <= 64, head_dim <=
+// 64) each operand is split into an fp16 hi part and an fp16 lo part (three products,
+// ~2^-22 relative): with scores near 100 the softmax multiplies a relative gate error by
+// ~100, and one fp16 product per operand (11 bits) then moves the output by ~2e-2.  The
+// counter stays in fp16 range: the host refuses rates whose EMA of one occurrence per step
+// could pass kCMax; a caller-supplied initial state above kCMax (which no such EMA reaches)
+// saturates at kCMax when loaded; the window adds at most kMaxWin; rho <= 1.  dpre, whose
+// scale is unbounded, keeps bf16 for the dW_pe product, so that product takes the bf16 copy
+// of the tile.
 #pragma once
 
 #include <hip/hip_bf16.h>

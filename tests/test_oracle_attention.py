@@ -161,9 +161,37 @@ def test_one_slot_by_hand():
 def test_gate_rounding_modes_stay_close():
     p = _problem(9, dtype=torch.float64)
     exact = _sparse(p)
-    for mode in ("bf16", "f16"):
+    errs = {}
+    for mode in ("bf16", "f16", "f16c", "f16w", "split"):
         r = _sparse(p, gate_round=mode)
-        assert (r - exact).abs().max() / exact.abs().max() < 2e-2
+        errs[mode] = float((r - exact).abs().max() / exact.abs().max())
+    # the split gate's forward is the exact one; each fp16 rounding moves the output, by less
+    # than bf16's (3 more significand bits; measured 3.3x on this small problem), and rounding
+    # both operands by more than rounding either alone
+    assert errs["split"] == 0.0, errs
+    assert 0.0 < errs["f16"] < errs["bf16"] / 2 < 2e-2, errs
+    assert 0.0 < errs["f16c"] < 1.5 * errs["f16"] and 0.0 < errs["f16w"] < 1.5 * errs["f16"], errs
+
+
+def test_gate_rounding_helpers_are_the_formats_roundings():
+    """Each rounded operand is the nearest value of its format (torch's conversions), with W
+    rounded after the kernels' log2 e pre-scaling."""
+    g = torch.Generator().manual_seed(4)
+    W = torch.randn(8, 16, generator=g, dtype=torch.float64) * 0.3
+    c = torch.rand(5, 8, generator=g, dtype=torch.float64) * 900
+    l2e = 1.0 / math.log(2.0)
+    for mode in (None, "split", "f16c"):
+        assert torch.equal(att._round_gate_operands(W, mode), W)
+    for mode in (None, "split", "f16w"):
+        assert torch.equal(att._round_gate_counter(c, mode), c)
+    Wf = att._round_gate_operands(W, "f16") * l2e
+    assert torch.allclose(Wf, Wf.to(torch.float16).double(), rtol=1e-12, atol=0)  # on the fp16 grid
+    assert ((Wf - W * l2e).abs() <= (W * l2e).abs() * 2.0 ** -11 * (1 + 1e-9)).all()
+    assert torch.equal(att._round_gate_operands(W, "bf16"), W.to(torch.bfloat16).double())
+    assert torch.equal(att._round_gate_counter(c, "f16"), c.float().half().double())
+    assert torch.equal(att._round_gate_counter(c, "bf16"), c.float().bfloat16().double())
+    with pytest.raises(ValueError):
+        att._round_gate_operands(W, "fp8")
 
 
 @pytest.mark.parametrize("use_silu", [True, False])
