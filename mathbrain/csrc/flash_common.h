@@ -406,21 +406,36 @@ struct Producer {
                                           fminf(s[ii].z, kCMax), fminf(s[ii].w, kCMax));
             const uint64_t mask = meta[j].mask;
             bf16x4 tb[4], tl4[4];
+            // The quad's first step sums its window directly; the next three follow by
+            // c_dec[t + 1] = rho (c_dec[t] + [x_t == u]).
+            const float4 rho = *reinterpret_cast<const float4*>(powt + NPAD + n0);
+            float c0, c1, c2, c3;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tl = 4 * tq + r;
                 const int tr = t0 - cb + tl;  // 0 .. 63
-                const float4 pw = *reinterpret_cast<const float4*>(powt + (tr + 1) * NPAD + n0);
-                float c0 = sv.x * pw.x, c1 = sv.y * pw.y, c2 = sv.z * pw.z, c3 = sv.w * pw.w;
-                uint64_t m = mask & ((1ull << tr) - 1ull);
-                while (m) {
-                    const int p = __builtin_ctzll(m);
-                    m &= m - 1;
-                    const float4 q = *reinterpret_cast<const float4*>(powt + (tr - p) * NPAD + n0);
-                    c0 += q.x;
-                    c1 += q.y;
-                    c2 += q.z;
-                    c3 += q.w;
+                if (r == 0) {
+                    const float4 pw = *reinterpret_cast<const float4*>(powt + (tr + 1) * NPAD + n0);
+                    c0 = sv.x * pw.x;
+                    c1 = sv.y * pw.y;
+                    c2 = sv.z * pw.z;
+                    c3 = sv.w * pw.w;
+                    uint64_t m = mask & ((1ull << tr) - 1ull);
+                    while (m) {
+                        const int p = __builtin_ctzll(m);
+                        m &= m - 1;
+                        const float4 q = *reinterpret_cast<const float4*>(powt + (tr - p) * NPAD + n0);
+                        c0 += q.x;
+                        c1 += q.y;
+                        c2 += q.z;
+                        c3 += q.w;
+                    }
+                } else {
+                    const float hit = (mask >> (tr - 1)) & 1ull ? 1.f : 0.f;
+                    c0 = (c0 + hit) * rho.x;
+                    c1 = (c1 + hit) * rho.y;
+                    c2 = (c2 + hit) * rho.z;
+                    c3 = (c3 + hit) * rho.w;
                 }
                 if (PG) {
                     // hi and lo come from one materialised float32 counter: a conversion the
