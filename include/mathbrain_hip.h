@@ -232,7 +232,13 @@ int64_t mb_flash_ema_fwd_workspace(int B, int H, int L, int hd, int K, int N, in
  * dQ is written once per element.  dE_k, dE_v and dW_pe are cleared by the call (with a
  * fill kernel, no memset) and then accumulated with fp32 atomics, so their summation
  * order is not fixed, as in the reference's tl.atomic_add.  The gate is recomputed as
- * in the forward (the same arithmetic for the same flags); the dW_pe product takes bf16
+ * in the forward (the same arithmetic for the same flags), except that by default, when
+ * `scores` is given, a slot takes the split gate only in the waves (16 steps of one head)
+ * where the forward's probability reaches 2^-7 at one of the steps, and the single fp16
+ * product elsewhere: every gradient term of a slot carries its probability, so the single
+ * product's rounding enters scaled by it (at a 6-layer model's initialisation 99.9 % of the
+ * slot-steps qualify, and the gradients' distance from the exact model's stays 4.6e-3, as
+ * with the split everywhere).  MB_FLASH_FP32 always splits.  The dW_pe product takes bf16
  * c_dec and bf16 dpre (as the reference's triton_flash_ema.py:463-465 does), or with
  * MB_FLASH_FP32 bf16 hi + lo pairs of both, with fp32 accumulation.  Supported: as
  * mb_flash_ema_fwd.  At hd 128 each head runs as two 64-dim halves on two waves that add

@@ -30,6 +30,9 @@ constexpr int kBwdHeads = 4;  // heads per workgroup
 // Batch slot info ring: a fast wave writes batch i+2's info while slow waves still read
 // batch i's, so at least three entries; four makes the ring index a mask.
 constexpr int kMetaRing = 4;
+// Default mode: a slot takes the backward's split gate in a wave where the forward's
+// probability reaches this at one of the wave's steps (2^-7).
+constexpr float kSplitP = 0.0078125f;
 
 __global__ void zero_fill_kernel(float* p, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -289,28 +292,43 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
                 ek[dt] = E[(j * 2 + 0) * WID + hl * HD + 16 * dt + c16];
                 ev[dt] = E[(j * 2 + 1) * WID + hl * HD + 16 * dt + c16];
             }
-            f16x8 cfl[NS];
-            if (PG) {
+            // The split gate where this slot carries weight: every gradient term of the slot
+            // has a factor p (dE_v, and ds = p (dp - D) in dQ, dE_k and dpre), so where the
+            // forward's probability stays below kSplitP at all of the wave's 16 steps the
+            // single fp16 product's rounding is scaled down by it (the fp32 mode, and the
+            // recomputed scores, whose p comes after the gate, always split).
+            bool split = PG;
+            if constexpr (PG && !PW && HAS_S)
+                split = __any(fmaxf(fmaxf(s2v[0], s2v[1]), fmaxf(s2v[2], s2v[3])) >= kSplitP);
+            f32x4 g2[DT], sg[DT];
+            if (split) {
+                f16x8 cfl[NS];
 #pragma unroll
                 for (int ns = 0; ns < NS; ++ns)
                     cfl[ns] = *reinterpret_cast<const f16x8*>(crow + S::CDEC + c16 * S::CROW + 32 * ns + 8 * g);
-            }
-            f32x4 g2[DT], sg[DT];
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                f32x4 accg = {0.f, 0.f, 0.f, 0.f};
-                if (PG) {  // small terms first
+                for (int dt = 0; dt < DT; ++dt) {
+                    f32x4 accg = {0.f, 0.f, 0.f, 0.f};  // small terms first
 #pragma unroll
                     for (int ns = 0; ns < NS; ++ns)
                         accg = mfma16x16x32(cf[ns], wfl[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
 #pragma unroll
                     for (int ns = 0; ns < NS; ++ns)
                         accg = mfma16x16x32(cfl[ns], wfr[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
-                }
 #pragma unroll
-                for (int ns = 0; ns < NS; ++ns)
-                    accg = mfma16x16x32(cf[ns], wfr[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
-                g2[dt] = accg;
+                    for (int ns = 0; ns < NS; ++ns)
+                        accg = mfma16x16x32(cf[ns], wfr[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
+                    g2[dt] = accg;
+                }
+            } else {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    f32x4 accg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ns = 0; ns < NS; ++ns)
+                        accg = mfma16x16x32(cf[ns], wfr[((hl * DT + dt) * NS + ns) * 64 + lane], accg);
+                    g2[dt] = accg;
+                }
             }
             // Phase 1: gate, score and dO . v partial sums over this lane's dims.
             float s[4] = {0.f, 0.f, 0.f, 0.f}, dp[4] = {0.f, 0.f, 0.f, 0.f};

@@ -169,8 +169,10 @@ def _forget_rates(key):
 # Gate arithmetic of the attention kernels:
 #   "bf16" (default)  the gate GEMM splits c_dec and W_pe * log2 e into fp16 hi + lo pairs
 #                     (three products, ~2^-22 relative) where the kernels take it (N <= 64,
-#                     head_dim <= 64; single fp16 operands otherwise); dW_pe from bf16
-#                     operands, as the reference's kernel takes it;
+#                     head_dim <= 64; single fp16 operands otherwise); the backward, when it
+#                     reads the forward's scores, splits only for the slots whose probability
+#                     reaches 2^-7 at one of a wave's 16 steps (every gradient term of a slot
+#                     carries its p); dW_pe from bf16 operands, as the reference's kernel;
 #   "fp16"            single fp16 gate operands (2^-11): faster, for models whose scores stay
 #                     small (the softmax multiplies a relative gate error by the score scale);
 #   "fp32"            the split gate and a split dW_pe product (bf16 hi + lo), everything else

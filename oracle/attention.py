@@ -77,10 +77,15 @@ def dense(Q, x, E_k_slots, E_v_slots, rhos, pe_weight, n_heads, use_silu=True, c
 # its operands.  None: exact everywhere.  "bf16": both gate operands bf16 (the reference's
 # triton_flash_ema.py:188-190).  "f16": both fp16, W pre-scaled by log2 e (the HIP kernels'
 # single-product gate).  "split": the gate exact (the HIP kernels' fp16 hi + lo split leaves
-# ~2^-22, below what a float64 check resolves at these bars).  "f16c" / "f16w": only the
-# counter / only W_pe rounded to fp16 (for measuring which rounding matters).  Every mode but
-# None takes the dW_pe product from bf16 c_dec and bf16 dpre (triton_flash_ema.py:463-465).
-GATE_ROUNDS = (None, "bf16", "f16", "split", "f16c", "f16w")
+# ~2^-22, below what a float64 check resolves at these bars).  "split_p": "split" in the
+# forward; in the backward, per (sequence, slot, head, 16-step half of a 32-step block), the
+# "f16" gate where the forward's probability stays below SPLIT_P at every step of the half,
+# else "split" (the HIP default mode's backward reading stored scores).  "f16c" / "f16w": only
+# the counter / only W_pe rounded to fp16 (for measuring which rounding matters).  Every mode
+# but None takes the dW_pe product from bf16 c_dec and bf16 dpre (triton_flash_ema.py:463-465).
+GATE_ROUNDS = (None, "bf16", "f16", "split", "split_p", "f16c", "f16w")
+SPLIT_P = 2.0 ** -7
+PHALF = 16  # steps per decision: a wave of the HIP backward takes 16 steps of one head
 
 
 def _round_gate_operands(W, gate_round):
@@ -88,7 +93,7 @@ def _round_gate_operands(W, gate_round):
     ("f16" and "f16w"; "f16c" and "split" leave W exact)."""
     if gate_round not in GATE_ROUNDS:
         raise ValueError(f"gate_round={gate_round!r}")
-    if gate_round in (None, "f16c", "split"):
+    if gate_round in (None, "f16c", "split", "split_p"):
         return W
     if gate_round == "bf16":
         return W.to(torch.bfloat16).to(W.dtype)
@@ -103,7 +108,7 @@ def _round_gate_counter(c, gate_round):
     exact for None, "f16w" and "split", else fp16 ("f16", "f16c") or bf16 ("bf16")."""
     if gate_round not in GATE_ROUNDS:
         raise ValueError(f"gate_round={gate_round!r}")
-    if gate_round in (None, "f16w", "split"):
+    if gate_round in (None, "f16w", "split", "split_p"):
         return c
     return c.float().to(torch.float16 if gate_round != "bf16" else torch.bfloat16).to(c.dtype)
 
@@ -119,13 +124,14 @@ def _steps(L, t_eval):
 
 
 def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=True,
-           absent_mass=True, gate_round=None, return_lse=False, t_eval=None):
+           absent_mass=True, gate_round=None, return_lse=False, t_eval=None, return_probs=False):
     """Unique-slot flash-EMA attention.
 
     Q [B, H, L, hd]; x [B, L]; E_k / E_v [B, K, D]; W_pe [N, D] (= pe_proj.weight.T);
     unique [B, K] int64 with -1 padding; c_init [B, K, N] key-side state at t=0
     (C_bounds[:, 0]).  Returns O [B, H, L, hd] (and LSE [B, H, L]); with ``t_eval``,
-    O [B, H, len(t_eval), hd] and LSE [B, H, len(t_eval)] at those steps, in order.
+    O [B, H, len(t_eval), hd] and LSE [B, H, len(t_eval)] at those steps, in order.  With
+    ``return_probs`` the softmax weights p [B, K, H, steps] of the valid slots come last.
 
     The per-step order is the reference's: c_dec = C * rho (triton_flash_ema.py:185),
     g = SiLU(c_dec @ W_pe[:, head]) (:188-196), s = q.(e_k*g)/sqrt(hd) over valid
@@ -145,7 +151,7 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
     Ek = E_k.reshape(B, K, H, hd).to(dt)
     Ev = E_v.reshape(B, K, H, hd).to(dt)
     log_absent = torch.log((V_total - Kb).clamp(min=0).to(dt))       # -inf if none absent
-    outs, lses = [], []
+    outs, lses, probs = [], [], []
     evaluate = set(_steps(L, t_eval))
     for t in range(L):
         c_dec = C * rho
@@ -167,14 +173,28 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
         o = (p.unsqueeze(-1) * Ev * g).sum(1)                        # [B,H,hd]
         outs.append(o)
         lses.append(lse)
+        if return_probs:
+            probs.append(p)
         match = (x[:, t].unsqueeze(1) == unique) & valid
         C = c_dec + match.unsqueeze(-1).to(dt)
     O = torch.stack(outs, dim=2)                                     # [B,H,L,hd]
     LSE = torch.stack(lses, dim=2)                                   # [B,H,L]
-    return (O, LSE) if return_lse else O
+    res = (O, LSE) if return_lse else (O,)
+    if return_probs:
+        res = res + (torch.stack(probs, dim=-1),)
+    return res if len(res) > 1 else res[0]
 
 
 @torch.no_grad()
+def single_gate_halves(P):
+    """[B, K, H, ceil(L / PHALF)]: True where the probabilities P [B, K, H, L] stay below
+    SPLIT_P at every step of the half-block (steps past L count as 0)."""
+    B, K, H, L = P.shape
+    nh = (L + PHALF - 1) // PHALF
+    P = F.pad(P, (0, nh * PHALF - L))
+    return P.reshape(B, K, H, nh, PHALF).amax(-1) < SPLIT_P
+
+
 def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_init=None,
                              use_silu=True, absent_mass=True, gate_round=None, t_eval=None):
     """The reference's closed-form backward, loop by loop (float64 recommended).
@@ -209,6 +229,11 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     Ek = E_k.reshape(B, K, H, hd).to(dt)
     Ev = E_v.reshape(B, K, H, hd).to(dt)
     bf = (lambda v: v.float().to(torch.bfloat16).to(dt)) if gate_round else (lambda v: v)
+    if gate_round == "split_p":  # per (b, k, h, half-block): may the gate be single fp16?
+        _, _, P = sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init, use_silu, absent_mass,
+                         gate_round="split", return_lse=True, return_probs=True)
+        single = single_gate_halves(P)                                # [B,K,H,nh]
+        W16 = _round_gate_operands(W_pe[:N].to(dt), "f16")
     dQ = torch.zeros_like(Q)
     dEk = torch.zeros(B, K, H, hd, dtype=dt)
     dEv = torch.zeros(B, K, H, hd, dtype=dt)
@@ -223,6 +248,9 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
         i = slot[t]
         cg = _round_gate_counter(c_dec, gate_round)
         pre = _gate_product(cg, W).reshape(B, K, H, hd)
+        if gate_round == "split_p":
+            pre16 = _gate_product(_round_gate_counter(c_dec, "f16"), W16).reshape(B, K, H, hd)
+            pre = torch.where(single[..., t // PHALF].unsqueeze(-1), pre16, pre)
         g = F.silu(pre) if use_silu else pre
         gp = silu_grad(pre) if use_silu else torch.ones_like(pre)
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
@@ -235,7 +263,7 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
         dEk += ds.unsqueeze(-1) * q_t * g * scale
         dEv += p.unsqueeze(-1) * do_t * g
         dpre = (ds.unsqueeze(-1) * q_t * scale * Ek + p.unsqueeze(-1) * do_t * Ev) * gp
-        cw = c_dec.float().to(dt) if gate_round == "split" else cg  # the kernel's float32 counter
+        cw = c_dec.float().to(dt) if gate_round in ("split", "split_p") else cg  # the kernel's float32 counter
         dW += torch.einsum("bkn,bkd->nd", bf(cw), bf(dpre.reshape(B, K, D)))
         match = (x[:, t].unsqueeze(1) == unique) & valid
         C = c_dec + match.unsqueeze(-1).to(dt)

@@ -104,7 +104,9 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
                 Q_full = Q_t.new_zeros(B, L, D).index_copy(1, torch.tensor(steps), Q_t)
             Q_mha = Q_full.reshape(B, L, H, hd).transpose(1, 2)          # :81
             Wt = g("attn.pe_proj.weight").t()
-            if t_eval is None:
+            # "split_p" rounds the backward's gate differently from the forward's, so its
+            # gradients come from the closed-form backward rather than from autograd
+            if t_eval is None and gate_round != "split_p":
                 O = att.sparse(Q_mha, x, Ek, Ev, Wt, rhos.to(dt), vocab_size, unique, cb,
                                use_silu=use_silu, absent_mass=absent_mass, gate_round=gate_round)
             else:

@@ -2,12 +2,12 @@
 float64, the unique-slot device semantics with the absent-slot mass).
 
 Logits and every parameter gradient are compared norm-wise (max|got - want| / max|want|)
-at the task's bf16 bar, 2e-2, against the exact oracle at the model's own initialisation:
-the attention's gate GEMM takes fp16 operands.  Against the oracle with the kernel's own
-gate rounding (fp16 c_dec and fp16 W_pe * log2 e) the logits and every gradient must
-agree to 1e-4 -- except pe_proj.weight, whose attention part the kernel contracts from
-bf16 c_dec and bf16 dpre (as triton_flash_ema.py:463-465 does) while the oracle's
-autograd keeps both exact: 1e-2 there.
+at the task's bf16 bar, 2e-2, against the exact oracle at the model's own initialisation.
+Against the oracle with the kernels' own gate rounding (the split gate; in the backward the
+single fp16 product for slots whose probability stays below 2^-7) the logits must agree to
+1e-4 and the gradients to TOL_ROUNDING_GRAD -- except pe_proj.weight, whose attention part
+the kernel contracts from bf16 c_dec and bf16 dpre (as triton_flash_ema.py:463-465 does):
+1e-2 there.
 """
 import math
 
@@ -20,8 +20,15 @@ pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-2
 # the oracle rounding of the default attention mode at these models' shapes (head_dim <= 64,
-# N <= 64: the split gate; tests.test_gpu_flash.kernel_rounding)
-SPLIT = "split"
+# N <= 64: the split gate, and in the backward, which reads the forward's kept scores, the
+# single product for slots whose probability stays below 2^-7; tests.test_gpu_flash.kernel_rounding)
+SPLIT = "split_p"
+# Gradients against that oracle (pe_proj.weight aside): measured up to 1.3e-4 (LayerNorm and
+# RMSNorm weights and biases, whose gradients sum over every row and cancel; the all-split
+# oracle gives 1.2e-4 on the same run), so the kernels' per-wave choice of gate product is
+# resolved at 3e-4, well under the product of any single-product slot (3.6e-3 with every
+# slot on it).
+TOL_ROUNDING_GRAD = 3e-4
 
 
 def norm_err(got, want):
@@ -70,7 +77,7 @@ def test_model_forward_backward_vs_oracle(with_history):
         print(f"gate_round={gate_round}: logits {err:.2e}; worst grad {worst} {gerr[worst]:.2e}")
         assert err < tol_logits
         for k, e in gerr.items():
-            tol = TOL_BF16 if gate_round is None else (1e-2 if k.endswith("pe_proj.weight") else 1e-4)
+            tol = TOL_BF16 if gate_round is None else (1e-2 if k.endswith("pe_proj.weight") else TOL_ROUNDING_GRAD)
             assert e < tol, (gate_round, k, e)
 
 
@@ -129,7 +136,7 @@ def test_model_vocab_table_path_vs_oracle(kv_table):
     assert norm_err(logits, want) < 1e-4
     grads = dict(m.named_parameters())
     for k, v in p.items():
-        tol = 1e-2 if k.endswith("pe_proj.weight") else 1e-4
+        tol = 1e-2 if k.endswith("pe_proj.weight") else TOL_ROUNDING_GRAD
         assert norm_err(grads[k].grad, v.grad) < tol, (kv_table, k)
 
 
@@ -160,7 +167,7 @@ def test_model_absent_mass_switch_vs_oracle(absent_mass):
     assert norm_err(logits, want) < 1e-4
     grads = dict(m.named_parameters())
     for k, v in p.items():
-        tol = 1e-2 if k.endswith("pe_proj.weight") else 1e-4
+        tol = 1e-2 if k.endswith("pe_proj.weight") else TOL_ROUNDING_GRAD
         assert norm_err(grads[k].grad, v.grad) < tol, (absent_mass, k)
     other = omodel.lm_forward({k: v.detach() for k, v in p.items()}, x, n_layers, H,
                               m.ema_rhos.cpu(), V, gate_round=SPLIT, absent_mass=not absent_mass, **kw)
@@ -238,5 +245,7 @@ def test_model_traces_without_graph_breaks():
     out = cm(*args)
     (out.float() ** 2).mean().backward()
     assert norm_err(out, ref) < 1e-6
+    # the traced graph recomputes the scores in the backward, which then takes the split gate
+    # for every slot; eager keeps them and takes the single product where p < 2^-7
     for k, p in m.named_parameters():
-        assert norm_err(p.grad, gref[k]) < 1e-5, k
+        assert norm_err(p.grad, gref[k]) < 1e-4, k

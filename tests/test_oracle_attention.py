@@ -254,3 +254,58 @@ def test_sampled_steps_equal_full_evaluation(seed):
     sampled = att.sparse_backward_formulas(*args, dO, p["c_init"], t_eval=steps)
     for got, want in zip(sampled, full):
         assert torch.allclose(got, want, rtol=1e-12, atol=1e-15)
+
+
+def _bwd(p, gate_round, seed=11):
+    B, L, D = p["Q"].shape
+    Qh = p["Q"].reshape(B, L, p["H"], p["hd"]).transpose(1, 2)
+    g = torch.Generator().manual_seed(seed)
+    dO = torch.randn(Qh.shape, generator=g, dtype=Qh.dtype)
+    return att.sparse_backward_formulas(Qh, p["x"], p["E_k"], p["E_v"], p["pe_weight"].t(), p["rhos"],
+                                        p["V"], p["unique"], dO, p["c_init"], gate_round=gate_round)
+
+
+def test_split_p_takes_the_split_or_the_single_product_by_probability(monkeypatch):
+    """"split_p" (the default kernels' backward with stored scores): its forward is the exact
+    one; with a threshold of 0 its backward is "split"'s exactly; with every probability below
+    the threshold the backward's gate takes the single fp16 product, which moves the gradients
+    by about what "f16" moves them (not at all in dW_pe's counter operand); a threshold
+    between the two gives a result between them."""
+    p = _problem(12, L=40)
+    assert torch.equal(_sparse(p, gate_round="split_p"), _sparse(p))
+    split, f16 = _bwd(p, "split"), _bwd(p, "f16")
+    dist = lambda a, b: float((a - b).abs().max() / b.abs().max())
+    monkeypatch.setattr(att, "SPLIT_P", 0.0)
+    for a, b in zip(_bwd(p, "split_p"), split):
+        assert torch.equal(a, b)
+    monkeypatch.setattr(att, "SPLIT_P", 2.0)
+    lo = _bwd(p, "split_p")
+    for k in range(3):
+        d_lo, d_f16 = dist(lo[k], split[k]), dist(f16[k], split[k])
+        assert 0.0 < d_lo < 3 * d_f16 and d_lo > d_f16 / 30, (k, d_lo, d_f16)
+    _, _, P = _sparse(p, return_lse=True, return_probs=True)
+    monkeypatch.setattr(att, "SPLIT_P", float(P[p["unique"] >= 0].median()))
+    mid = _bwd(p, "split_p")
+    assert 0.0 < dist(mid[0], split[0]) and 0.0 < dist(mid[0], lo[0])
+
+
+def test_single_gate_halves_groups_16_steps():
+    P = torch.zeros(1, 2, 1, 40, dtype=torch.float64)
+    P[0, 0, 0, 17] = att.SPLIT_P          # at the threshold: the half [16, 32) splits
+    P[0, 1, 0, 39] = att.SPLIT_P * 0.999  # below it everywhere: all single
+    single = att.single_gate_halves(P)
+    assert single.shape == (1, 2, 1, 3)
+    assert single[0, 0, 0].tolist() == [True, False, True]
+    assert single[0, 1, 0].tolist() == [True, True, True]
+
+
+def test_return_probs_are_the_softmax_weights():
+    p = _problem(13, L=12)
+    O, LSE, P = _sparse(p, return_lse=True, return_probs=True)
+    valid = (p["unique"] >= 0)
+    # weights of the valid slots plus the absent mass sum to one at every (b, h, t)
+    V, Kb = p["V"], valid.sum(1).to(torch.float64)
+    absent = ((V - Kb).clamp(min=0).reshape(-1, 1, 1) * torch.exp(-LSE))  # score 0 each
+    total = P.sum(1) + absent
+    assert torch.allclose(total, torch.ones_like(total), rtol=1e-12)
+    assert torch.count_nonzero(P[~valid]) == 0
