@@ -67,7 +67,7 @@ GATE_DTYPES = {
 }
 
 TRAFFIC_BYTES = {
-    "cfg2": 14733.4e6,     # flash_ema_bwd_kernel, default mode (profiles/flash_ema_cfg2.md)
+    "cfg2": 14703.6e6,     # flash_ema_bwd_kernel, default mode (profiles/flash_ema_cfg2.md)
     "cfg4": 50700.7e6,
     "corpus": 19654.0e6,   # the three mb_corpus_states launches (profiles/corpus_states_64M_tokens.md)
     "scan": 109.3e6,       # ema_query_scan_kernel at configuration 3 (profiles/ema_query_scan_cfg3.md)
