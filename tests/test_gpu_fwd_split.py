@@ -3,8 +3,9 @@ run as ks parts whose partial softmax states flash_fwd_merge_kernel combines.  C
 the C ABI against the same launch without a workspace (unsplit) on the same inputs: O and LSE
 agree to fp32 rounding of the reordered sums (1e-5 norm-wise; the unsplit path is pinned
 against the oracle by test_gpu_flash.py), including rows whose parts hold no slot, padding
-slots, both softmax modes, vocabulary rows and the fp32 mode.  Also the planner: the
-configuration-2 shape splits in two on a 256-CU device, configuration 4's does not."""
+slots, both softmax modes, vocabulary rows, in all three precision modes.  Also the
+planner: the configuration-2 shape splits in two on a 256-CU device, configuration 4's does
+not."""
 import pytest
 import torch
 
@@ -15,11 +16,11 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-5
 
 
-def run(c, ws_mode, use_silu=True, absent_mass=True, table=False, fp32=False, scores=False):
+def run(c, ws_mode, use_silu=True, absent_mass=True, table=False, prec="fp16", scores=False):
     """mb_flash_ema_fwd on the case; ws_mode None (no workspace), "exact" (the planned bytes)
     or "short" (one byte less: the launch must then run unsplit)."""
     from mathbrain import _lib
-    from mathbrain.triton_flash_ema import _flash_flags
+    from mathbrain.triton_flash_ema import _flash_flags, _prec
     dev = torch.device("cuda", 0)
     B, H, L, hd = c["Q"].shape
     K, N = c["K"], c["rhos"].shape[0]
@@ -41,7 +42,7 @@ def run(c, ws_mode, use_silu=True, absent_mass=True, table=False, fp32=False, sc
     rh = c["rhos"].to(dev).float().contiguous()
     uniq = c["unique"].to(dev)
     Cb = c["Cb"].to(dev).float().contiguous()
-    flags = _flash_flags(use_silu, absent_mass, table, fp32)
+    flags = _flash_flags(use_silu, absent_mass, table, _prec(prec))
     need = _lib.lib().mb_flash_ema_fwd_workspace(B, H, L, hd, K, N, flags)
     assert need >= 0
     ws, nws = None, 0
@@ -59,14 +60,14 @@ def run(c, ws_mode, use_silu=True, absent_mass=True, table=False, fp32=False, sc
     return need, O.cpu(), LSE.cpu(), (S2.cpu() if scores else None)
 
 
-def compare(c, **kw):
+def compare(c, tol=TOL, **kw):
     need, Os, Ls, Ss = run(c, "exact", **kw)
     assert need > 0, "the planner should split this small grid"
     _, Ou, Lu, Su = run(c, None, **kw)
     assert torch.isfinite(Os).all() and torch.isfinite(Ou).all()
     eo, el = norm_err(Os, Ou), norm_err(Ls, Lu)
     print(f"workspace {need} B: O {eo:.2e}, LSE {el:.2e}")
-    assert eo < TOL and el < TOL
+    assert eo < tol and el < tol
     if Ss is not None:   # the scores do not depend on the split: bit-identical
         valid = (c["unique"] >= 0)[:, None, :, None].expand_as(Ss)
         assert torch.equal(Ss[valid], Su[valid])
@@ -75,6 +76,14 @@ def compare(c, **kw):
 def test_split_matches_unsplit_cfg_like():
     c = make_case(2, 96, 300, 8, 64, 64, warmup=100, seed=1, qs=0.5, es=0.3, ws=0.2)
     compare(c)
+
+
+def test_split_default_mode():
+    """The default mode (the split gate in the forward) and its scores."""
+    c = make_case(2, 70, 200, 4, 32, 16, warmup=60, seed=7, qs=0.5, es=0.3, ws=0.2)
+    compare(c, prec="bf16", scores=True)
+    c = make_case(2, 96, 300, 8, 64, 64, warmup=100, seed=1, qs=0.5, es=0.3, ws=0.2)
+    compare(c, prec="bf16", scores=True)
 
 
 @pytest.mark.parametrize("use_silu", [True, False])
@@ -96,7 +105,7 @@ def test_split_vocab_rows():
 
 def test_split_fp32_mode():
     c = make_case(2, 64, 160, 8, 64, 64, warmup=80, seed=17, qs=0.5, es=0.3, ws=0.2)
-    compare(c, fp32=True)
+    compare(c, prec="fp32", scores=True)
 
 
 def test_split_empty_parts():
@@ -109,8 +118,8 @@ def test_split_empty_parts():
 
 def test_short_workspace_runs_unsplit():
     c = make_case(2, 64, 150, 8, 64, 64, warmup=40, seed=23, qs=0.5, es=0.3, ws=0.2)
-    need, Os, Ls, _ = run(c, "short")
-    _, Ou, Lu, _ = run(c, None)
+    need, Os, Ls, _ = run(c, "short", prec="bf16")
+    _, Ou, Lu, _ = run(c, None, prec="bf16")
     assert need > 0
     assert torch.equal(Os, Ou) and torch.equal(Ls, Lu)
 
