@@ -35,6 +35,8 @@ namespace mb {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -442,11 +444,10 @@ struct Producer {
                     // compiler fused with the last add would round hi from a different value
                     asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
                 }
-                f16x4 w;
-                w[0] = (_Float16)c0;
-                w[1] = (_Float16)c1;
-                w[2] = (_Float16)c2;
-                w[3] = (_Float16)c3;
+                // two values per conversion (round to nearest even, as one at a time)
+                const f16x2 w01 = __builtin_convertvector(f32x2{c0, c1}, f16x2);
+                const f16x2 w23 = __builtin_convertvector(f32x2{c2, c3}, f16x2);
+                const f16x4 w = {w01[0], w01[1], w23[0], w23[1]};
                 *reinterpret_cast<f16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
                 if (PG) {  // the fp16 rounding remainder
                     f16x4 wl;
