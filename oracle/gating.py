@@ -21,12 +21,14 @@ def gate_ln(x_q, p_pre, bias, ln_w, ln_b, use_silu=True, eps=1e-5):
     return F.layer_norm(x_emb, (x_q.shape[-1],), ln_w, ln_b, eps)
 
 
-def forward(x_q, C_seq, pe_weight, ln_w, ln_b, q_weight, use_silu=True):
-    """fused_apply_symmetric_query_gating (triton_fused_gating.py:179-197)."""
+def forward(x_q, C_seq, pe_weight, ln_w, ln_b, q_weight, use_silu=True, linear=None, pe_linear=None):
+    """fused_apply_symmetric_query_gating (triton_fused_gating.py:179-197).  ``linear`` /
+    ``pe_linear`` (u, w) -> u @ w.T evaluate the q_proj / pe_proj Linears (default: exact)."""
+    mm = lambda u, w: u @ w.t()
     bias = pe_weight.sum(dim=1)                      # :180
-    p_pre = C_seq @ pe_weight.t()                    # :183
+    p_pre = (pe_linear or mm)(C_seq, pe_weight)      # :183
     q_ln = gate_ln(x_q, p_pre, bias, ln_w, ln_b, use_silu)
-    return q_ln @ q_weight.t()                       # :197
+    return (linear or mm)(q_ln, q_weight)            # :197
 
 
 @torch.no_grad()

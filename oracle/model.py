@@ -24,14 +24,63 @@ from . import gating
 from . import scan
 
 
+class _Rounded(torch.autograd.Function):
+    """Rounds the value to ``dtype`` and back, and its gradient the same way: a tensor that
+    torch.autocast keeps in bf16, forward and backward."""
+
+    @staticmethod
+    def forward(ctx, t, dtype):
+        ctx.dt = dtype
+        return t.to(dtype).to(t.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(ctx.dt).to(g.dtype), None
+
+
+class _RoundedLinear(torch.autograd.Function):
+    """a @ w.T as a Linear under torch.autocast computes it: both operands rounded to
+    ``dtype``, the product accumulated wide and rounded to ``dtype``; in the backward the
+    incoming gradient is rounded and both products rounded the same way."""
+
+    @staticmethod
+    def forward(ctx, a, w, dtype):
+        r = lambda t: t.to(dtype).to(t.dtype)
+        ar, wr = r(a), r(w)
+        ctx.save_for_backward(ar, wr)
+        ctx.dt = dtype
+        return r(ar @ wr.t())
+
+    @staticmethod
+    def backward(ctx, g):
+        ar, wr = ctx.saved_tensors
+        r = lambda t: t.to(ctx.dt).to(t.dtype)
+        gr = r(g)
+        da = r(gr @ wr)
+        dw = r(gr.reshape(-1, gr.shape[-1]).t() @ ar.reshape(-1, ar.shape[-1]))
+        return da, dw, None
+
+
+def linear(a, w, dtype=None):
+    """nn.Linear without bias (w [out, in]); ``dtype`` (e.g. torch.bfloat16) evaluates it as
+    torch.autocast does."""
+    return a @ w.t() if dtype is None else _RoundedLinear.apply(a, w, dtype)
+
+
+def rounded(t, dtype=None):
+    return t if dtype is None else _Rounded.apply(t, dtype)
+
+
 def rmsnorm(x, w, eps=1e-6):
     """model.py:17-19."""
     return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
 
 
-def swiglu(x, w1, w2, w3):
-    """model.py:28-29 (nn.Linear weights are [out, in])."""
-    return (F.silu(x @ w1.t()) * (x @ w3.t())) @ w2.t()
+def swiglu(x, w1, w2, w3, amp=None):
+    """model.py:28-29 (nn.Linear weights are [out, in]); ``amp``: the autocast dtype, whose
+    roundings the silu and the product of the bf16 projections then take too."""
+    h = rounded(rounded(F.silu(linear(x, w1, amp)), amp) * linear(x, w3, amp), amp)
+    return linear(h, w2, amp)
 
 
 def unique_index(x):
@@ -47,7 +96,7 @@ def unique_index(x):
 
 def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_base=None,
                pad_mask=None, use_silu=True, attention="sparse", gate_round=None,
-               absent_mass=True, mask_query_keys=True, t_eval=None):
+               absent_mass=True, mask_query_keys=True, t_eval=None, amp=None, amp_pe_proj=False):
     """Logits [B, L, V] of SlotTransformerLM.forward (model.py:144-186).
 
     ``absent_mass`` picks the attention's softmax (all V slots, or the valid slots only as
@@ -55,7 +104,15 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
     reference's query scan on the 0-padded slot list (model.py:157).  With ``t_eval`` the
     logits are [B, len(t_eval), V] at those positions only: K/V come from the embedding
     table and the counter states, not from other positions' hidden states, so every
-    position's logits depend on its own row and the states alone (exact)."""
+    position's logits depend on its own row and the states alone (exact).
+
+    ``amp`` (torch.bfloat16) evaluates the model as it runs under torch.autocast: every
+    Linear's operands, product and gradients rounded to bf16 (``linear``), the SwiGLU silu and
+    product too; norms, the gating and the attention (custom_fwd(cast_inputs=float32) in
+    the reference, triton_flash_ema.py:573, triton_fused_gating.py) stay wide.  The query
+    gate's pe_proj is a Linear in the reference's wrapper (triton_fused_gating.py:183), so
+    under autocast its output is bf16 there; ``amp_pe_proj`` rounds it that way, where this
+    implementation computes it inside the fp32 gating kernel."""
     B, L = x.shape
     E = p["embed.weight"]
     dt = E.dtype
@@ -93,12 +150,14 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
         g = lambda name: p[pre + name]
         a = rmsnorm(x_q, g("attn_norm.weight"))                         # :114
         Q_t = gating.forward(a, C_seq, g("attn.pe_proj.weight"), g("attn.ln_q.weight"),
-                             g("attn.ln_q.bias"), g("attn.q_proj.weight"), use_silu)   # :75
+                             g("attn.ln_q.bias"), g("attn.q_proj.weight"), use_silu,
+                             linear=lambda u, w: linear(u, w, amp),
+                             pe_linear=lambda u, w: linear(u, w, amp if amp_pe_proj else None))   # :75
         if attention == "sparse":
             E_active = E[unique.clamp(min=0)]                           # :64-65
             mem = F.layer_norm(E_active, (D,), g("attn.ln_kv.weight"), g("attn.ln_kv.bias"))
-            Ek = mem @ g("attn.k_proj.weight").t()                      # :67
-            Ev = mem @ g("attn.v_proj.weight").t()                      # :68
+            Ek = linear(mem, g("attn.k_proj.weight"), amp)              # :67
+            Ev = linear(mem, g("attn.v_proj.weight"), amp)              # :68
             Q_full = Q_t
             if t_eval is not None:   # rows of the other steps are never read
                 Q_full = Q_t.new_zeros(B, L, D).index_copy(1, torch.tensor(steps), Q_t)
@@ -120,13 +179,13 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
             out = att.dense(Q_t, x, Eks, Evs, rhos.to(dt), g("attn.pe_proj.weight"), H, use_silu)
         else:
             raise ValueError(attention)
-        out = out @ g("attn.o_proj.weight").t()                         # :101
+        out = linear(out, g("attn.o_proj.weight"), amp)                 # :101
         h = x_q + out                                                   # :114
         h = h + swiglu(rmsnorm(h, g("ffn_norm.weight")), g("ffn.w1.weight"), g("ffn.w2.weight"),
-                       g("ffn.w3.weight"))                              # :115
+                       g("ffn.w3.weight"), amp)                         # :115
         x_q = h
     x_q = rmsnorm(x_q, p["final_norm.weight"])                          # :185
-    return x_q @ E.t()                                                  # :186, tied lm_head
+    return linear(x_q, E, amp)                                          # :186, tied lm_head
 
 
 class _SampledAttention(torch.autograd.Function):

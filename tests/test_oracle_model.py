@@ -46,3 +46,36 @@ def test_product_model_has_no_cpu_path():
     m = SlotTransformerLM(50, 64, 1, 2, N=4, dropout=0.0)
     with pytest.raises(NotImplementedError):
         m(torch.randint(0, 50, (1, 8)))
+
+
+def test_autocast_linear_matches_torch_bf16_matmul():
+    """oracle.model.linear with dtype bf16 (the model oracle's autocast roundings) against
+    torch's own bf16 matmul and its autograd on the CPU (float32 accumulation, one bf16
+    rounding of the output and of each gradient product): equal up to the accumulation order,
+    i.e. at most one bf16 step apart, and equal on nearly every element."""
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(3, 40, 96, generator=g, dtype=torch.float64)
+    w = torch.randn(72, 96, generator=g, dtype=torch.float64)
+    dy = torch.randn(3, 40, 72, generator=g, dtype=torch.float64)
+    ao, wo = a.clone().requires_grad_(), w.clone().requires_grad_()
+    y = omodel.linear(ao, wo, torch.bfloat16)
+    y.backward(dy)
+    ab, wb = a.to(torch.bfloat16).requires_grad_(), w.to(torch.bfloat16).requires_grad_()
+    yb = ab @ wb.t()
+    yb.backward(dy.to(torch.bfloat16))
+    r = lambda t: t.to(torch.bfloat16).double().abs()
+    mag = (r(a) @ r(w).t(), r(dy) @ r(w), r(dy).reshape(-1, 72).t() @ r(a).reshape(-1, 96))
+    for (got, want), m in zip(((y, yb), (ao.grad, ab.grad), (wo.grad, wb.grad)), mag):
+        want = want.double()
+        assert got.dtype == torch.float64
+        # values are bf16 numbers
+        assert torch.equal(got, got.to(torch.bfloat16).double())
+        # one bf16 step (8 significant bits) plus float32 accumulation over <= 120 terms
+        bound = want.abs() * 2.0**-7 + m * 120 * 2.0**-24
+        assert ((got - want).abs() <= bound).all()
+        assert (got == want).double().mean() > 0.97
+    # no rounding without a dtype, and the rounding helper rounds both ways
+    assert torch.equal(omodel.linear(a, w), a @ w.t())
+    t = a.clone().requires_grad_()
+    omodel.rounded(t, torch.bfloat16).backward(torch.ones_like(a) / 3)
+    assert torch.equal(t.grad, (torch.ones_like(a) / 3).to(torch.bfloat16).double())
