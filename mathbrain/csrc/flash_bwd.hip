@@ -147,6 +147,13 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         }
     };
 
+    // The default mode's split gate is the forward's, whose lo products cover only the rate
+    // tiles split_tiles picks: the other tiles' W_lo fragments and c_lo entries are zeros here,
+    // so that a split slot's gate (and with recomputed scores, its scores) are the forward's.
+    // The fp32 mode splits every tile.
+    int ctile = 3;
+    if constexpr (PG && !PW && NS == 2) ctile = split_tiles(a, lane);
+
     // Gate weights as the B operand: W[n = 32 ns + 8 g + e][d = 16 dt + c16] * log2 e,
     // one fragment per (head, dt, ns, lane) in LDS.
     // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
@@ -171,7 +178,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             vl[e] = (_Float16)(ws - (float)v[e]);
         }
         wfr[f] = v;
-        if (PG) wfl[f] = vl;
+        if (PG) wfl[f] = (ctile >> ns) & 1 ? vl : f16x8{};
     }
     flash_setup<NPAD>(a, b, t0, cb, win, powt, kinfo);
     const int kend = kinfo[1];
@@ -250,7 +257,8 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         load_scores(0);
         __syncthreads();
         store_scores(S2_of(0));
-        prod.template store<TT, S::CROW, S::TROW, PG, PW, S::CDEC, S::CT>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0), E_of(0), WID);
+        prod.template store<TT, S::CROW, S::TROW, PG, PW, S::CDEC, S::CT>(t0, cb, powt, meta_of(0), cdec_of(0), cdecT_of(0), E_of(0), WID,
+                                                                     ctile);
         if (nb > 1) flash_batch_meta<SB>(a, b, 1, kend, win, meta_of(1));
         wait_e_lds();
         __syncthreads();
@@ -296,7 +304,8 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
             // has a factor p (dE_v, and ds = p (dp - D) in dQ, dE_k and dpre), so where the
             // forward's probability stays below kSplitP at all of the wave's 16 steps the
             // single fp16 product's rounding is scaled down by it (the fp32 mode, and the
-            // recomputed scores, whose p comes after the gate, always split).
+            // recomputed scores, whose p comes after the gate, always split).  The split is
+            // the forward's (ctile).
             bool split = PG;
             if constexpr (PG && !PW && HAS_S)
                 split = __any(fmaxf(fmaxf(s2v[0], s2v[1]), fmaxf(s2v[2], s2v[3])) >= kSplitP);
@@ -494,7 +503,7 @@ flash_ema_bwd_kernel(typename FlashArgsOf<VR>::type a) {
         }
         if (bi + 1 < nb) {
             prod.template store<TT, S::CROW, S::TROW, PG, PW, S::CDEC, S::CT>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), cdecT_of(cur ^ 1),
-                                                E_of(cur ^ 1), WID);
+                                                E_of(cur ^ 1), WID, ctile);
             store_scores(S2_of(cur ^ 1));
             if (bi + 2 < nb) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }

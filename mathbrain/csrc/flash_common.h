@@ -281,6 +281,22 @@ __device__ void flash_setup(const FlashArgs& a, int b, int t0, int cb, int64_t* 
     __syncthreads();
 }
 
+// Rate tiles of the default mode's split gate that take the lo products (bit ns: tile ns),
+// for two 32-rate tiles: a counter is an EMA of at most one occurrence per step, so it stays
+// near or below B = 1 / (1 - rho), and a single fp16 product's rounding on a rate's term
+// scales with its counter; the first tile is left to the single product (2) when its largest
+// B is below 1/32 of the second's, else both are corrected (3).  Lane n reads rate n; every
+// wave computes the same value, so it is uniform over the workgroup.
+__device__ inline int split_tiles(const FlashArgs& a, int lane) {
+    float bh = lane < a.N ? 1.0f / fmaxf(1.0f - a.rhos[lane], 1e-30f) : 0.f;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) bh = fmaxf(bh, __shfl_xor(bh, off));
+    const float bo = __shfl_xor(bh, 32);
+    const float b0 = lane < 32 ? bh : bo;
+    const float b1 = lane < 32 ? bo : bh;
+    return 32.0f * b0 < fmaxf(b0, b1) ? 2 : 3;
+}
+
 // Slot ids and 64-bit occurrence masks of batch `bi`: wave j < SB handles slot j.
 template <int SB>
 __device__ void flash_batch_meta(const FlashArgs& a, int b, int bi, int kend, const int64_t* win,
@@ -390,10 +406,11 @@ struct Producer {
     // ([SB][2][width]) of the batch into the staging buffer.  With PG also cdec's lo tile, CLO
     // entries after cdec, and with PW cdecT's, CTLO entries after cdecT (see Stage).  With PG
     // the bf16 copy rounds the float32 counter; without, the gate's fp16 counter (the gate and
-    // the dW_pe product then see one c_dec).
+    // the dW_pe product then see one c_dec).  lo_tiles (PG): the 32-rate tiles whose lo entries
+    // are the rounding remainders (bit ns); the others' are written as zeros (split_tiles).
     template <bool BF, int CROW, int TROW, bool PG = false, bool PW = false, int CLO = 0, int CTLO = 0>
     __device__ void store(int t0, int cb, const float* powt, const BatchMeta* meta,
-                          _Float16* cdec, __bf16* cdecT, float* E, int width) {
+                          _Float16* cdec, __bf16* cdecT, float* E, int width, int lo_tiles = 3) {
         const int tid = threadIdx.x;
         const int nthr = blockDim.x;
 #pragma unroll
@@ -450,11 +467,13 @@ struct Producer {
                 const f16x4 w = {w01[0], w01[1], w23[0], w23[1]};
                 *reinterpret_cast<f16x4*>(cdec + (j * kTB + tl) * CROW + n0) = w;
                 if (PG) {  // the fp16 rounding remainder
-                    f16x4 wl;
-                    wl[0] = (_Float16)(c0 - (float)w[0]);
-                    wl[1] = (_Float16)(c1 - (float)w[1]);
-                    wl[2] = (_Float16)(c2 - (float)w[2]);
-                    wl[3] = (_Float16)(c3 - (float)w[3]);
+                    f16x4 wl = {0, 0, 0, 0};
+                    if ((lo_tiles >> (n0 >> 5)) & 1) {
+                        wl[0] = (_Float16)(c0 - (float)w[0]);
+                        wl[1] = (_Float16)(c1 - (float)w[1]);
+                        wl[2] = (_Float16)(c2 - (float)w[2]);
+                        wl[3] = (_Float16)(c3 - (float)w[3]);
+                    }
                     *reinterpret_cast<f16x4*>(cdec + CLO + (j * kTB + tl) * CROW + n0) = wl;
                 }
                 if (BF && PG) {  // bf16 (with PW hi + lo) of the float32 counter

@@ -35,12 +35,14 @@ static int fwd_dispatch(const FlashArgsV& a, int hd, int N, int flags, bool vr, 
     if (gm < 0) return gm;
     if (gm > 0) {
         // the split gate (both modes take it in the forward): hi + lo counter tiles and each
-        // wave's W_lo fragments in LDS; three slots per batch fill LDS at N = 64, head_dim 64
+        // wave's W_lo fragments in LDS; three slots per batch fill LDS at N = 64, head_dim 64.
+        // The fp32 mode corrects every rate tile, the default the large-counter ones.
+        const bool full = gm == 2;
         if (hd == 64)
-            return NS == 1 ? launch_fwd<64, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
-                           : launch_fwd<64, 2, 3, true>(a, vr, st, part, ws_bytes, ws_need);
-        return NS == 1 ? launch_fwd<32, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need)
-                       : launch_fwd<32, 2, 4, true>(a, vr, st, part, ws_bytes, ws_need);
+            return NS == 1 ? launch_fwd<64, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need, full)
+                           : launch_fwd<64, 2, 3, true>(a, vr, st, part, ws_bytes, ws_need, full);
+        return NS == 1 ? launch_fwd<32, 1, 4, true>(a, vr, st, part, ws_bytes, ws_need, full)
+                       : launch_fwd<32, 2, 4, true>(a, vr, st, part, ws_bytes, ws_need, full);
     }
     if (hd == 128) {  // two waves per head, one 16-step tile each
         if (NS == 1) return launch_fwd<128, 1, 4>(a, vr, st, part, ws_bytes, ws_need);

@@ -32,7 +32,11 @@ constexpr float kTau = 8.0f;
 // PREC (MB_FLASH_FP32): the gate GEMM carries both operands as fp16 hi + lo pairs,
 //   pre = W_lo c_hi + W_hi c_lo + W_hi c_hi  (three MFMAs, fp32 accumulation),
 // which leaves ~2^-22 relative error per product instead of fp16's 2^-11; W_lo waits in
-// LDS (W_hi stays in registers) and the producer writes a c_lo tile beside c_hi.
+// LDS (W_hi stays in registers) and the producer writes a c_lo tile beside c_hi.  The default
+// mode (PREC without FwdSplit::full) takes the two lo products only for the 32-rate tiles
+// whose counters can be large (split_tiles: with rates spread from half-life 1 to 4096, the
+// first tile's counters stay below ~87 against the second's ~5900, and the first takes the
+// single product).  MB_FLASH_FP32 corrects every tile.
 // GQ: the workgroup computes its queries from the gating inputs (flash_gq.h) instead of
 // reading Q.
 // Slot parts of the forward: each (b, block, head group) runs as ksplit workgroups over
@@ -43,12 +47,18 @@ constexpr float kTau = 8.0f;
 struct FwdSplit {
     float* part;
     int ksplit;
+    int full;  // PREC: every rate tile takes the lo products (MB_FLASH_FP32)
 };
 
 // TW: 16-step tiles per wave.  2 (head_dim <= 64): wave w < hpg takes head w and both tiles
 // of the block; 1 (head_dim 128): wave w < 2 hpg takes head w % hpg and tile w / hpg, so that
 // a lane's queries, outputs and gate tiles stay within the register budget.
-template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR, bool PREC = false, bool GQ = false>
+// CM (PREC): the rate tiles whose gate takes the lo products (bit ns: tile ns).  With two
+// tiles a default-mode launch runs the CM = 3 and the CM = 2 instantiation over the same grid,
+// and each workgroup returns at entry unless split_tiles picks its CM (one global read and a
+// few shuffles); a mask fixed at compile time keeps each slot loop's MFMA chain unbroken.
+template <int HD, int NS, int SB, int MAXI, int MAXE, bool SILU, bool VR, bool PREC = false, bool GQ = false,
+          int CM = (1 << NS) - 1>
 __global__ void __launch_bounds__(512, 1)
 flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     constexpr int NPAD = 32 * NS;
@@ -96,6 +106,9 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     const int tile0 = TW == 2 ? 0 : wave / hpg;  // the wave's first 16-step tile
     const int hw = TW == 2 ? wave : wave % hpg;  // the wave's head within the group
     const int h = active ? hg * hpg + hw : 0;    // idle waves read head 0 and write nothing
+    if constexpr (PREC && NS == 2 && TW == 2) {
+        if (!sp.full && split_tiles(a, lane) != CM) return;  // the other instantiation's (uniform)
+    }
 
     // Queries of this lane's steps (lane c16 of step tile tile0 + tt, dims 16 dt + 4 g + i).
     f32x4 qs[TW][DT];
@@ -115,6 +128,7 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     const int bi0 = part * nball / sp.ksplit;
     const int bi1 = (part + 1) * nball / sp.ksplit;
     const int x32 = (lane ^ 32) << 2;  // ds_bpermute byte address of lane l ^ 32
+
 
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
     // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
@@ -201,7 +215,7 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
         prod.template load<VR>(a, b, cbi, bi0, kend, D, col0, WIDF, meta_of(bi0));
         if constexpr (MAXE == 0) prod.template load_e_lds<VR>(a, b, bi0, kend, D, col0, WIDF, meta_of(bi0), E_of(0));
         __syncthreads();
-        prod.template store<false, S::CROW, S::TROW, PREC, false, S::CDEC>(t0, cb, powt, meta_of(bi0), cdec_of(0), nullptr, E_of(0), WIDF);
+        prod.template store<false, S::CROW, S::TROW, PREC, false, S::CDEC>(t0, cb, powt, meta_of(bi0), cdec_of(0), nullptr, E_of(0), WIDF, CM);
         if (bi0 + 1 < bi1) flash_batch_meta<SB>(a, b, bi0 + 1, kend, win, meta_of(bi0 + 1));
         wait_e_lds();
         __syncthreads();
@@ -246,8 +260,9 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
                 if (PREC) {
 #pragma unroll
                     for (int ns = 0; ns < NS; ++ns)
-                        cl[ns] = *reinterpret_cast<const f16x8*>(
-                            cdec + S::CDEC + (j * kTB + 16 * (tile0 + tt) + c16) * S::CROW + 32 * ns + 8 * g);
+                        if ((CM >> ns) & 1)
+                            cl[ns] = *reinterpret_cast<const f16x8*>(
+                                cdec + S::CDEC + (j * kTB + 16 * (tile0 + tt) + c16) * S::CROW + 32 * ns + 8 * g);
                 }
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
@@ -255,9 +270,11 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
                     if (PREC) {  // small terms first
 #pragma unroll
                         for (int ns = 0; ns < NS; ++ns)
-                            acc = mfma16x16x32(wlo[((wave * DT + dt) * NS + ns) * 64 + lane], cf[tt][ns], acc);
+                            if ((CM >> ns) & 1)
+                                acc = mfma16x16x32(wlo[((wave * DT + dt) * NS + ns) * 64 + lane], cf[tt][ns], acc);
 #pragma unroll
-                        for (int ns = 0; ns < NS; ++ns) acc = mfma16x16x32(wf[dt][ns], cl[ns], acc);
+                        for (int ns = 0; ns < NS; ++ns)
+                            if ((CM >> ns) & 1) acc = mfma16x16x32(wf[dt][ns], cl[ns], acc);
                     }
 #pragma unroll
                     for (int ns = 0; ns < NS; ++ns) {
@@ -330,7 +347,7 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
         }
         if (bi + 1 < bi1) {
             prod.template store<false, S::CROW, S::TROW, PREC, false, S::CDEC>(t0, cb, powt, meta_of(bi + 1), cdec_of(cur ^ 1), nullptr,
-                                              E_of(cur ^ 1), WIDF);
+                                              E_of(cur ^ 1), WIDF, CM);
             if (bi + 2 < bi1) flash_batch_meta<SB>(a, b, bi + 2, kend, win, meta_of(bi + 2));
         }
         wait_e_lds();
@@ -451,6 +468,14 @@ static int64_t fwd_part_bytes(int ks, int B, int H, int L, int hd) {
     return ks > 1 ? (int64_t)ks * B * H * L * (hd + 2) * 4 : 0;
 }
 
+// The CM = 2 instantiation a default-mode launch adds (two rate tiles), or nullptr.
+template <int HD, int NS, int SB, int MI, int ME, bool SILU, bool VR, bool PREC, bool GQ>
+constexpr auto fwd_kernel_cm2() {
+    using K = decltype(&flash_ema_fwd_kernel<HD, NS, SB, MI, ME, SILU, VR, PREC, GQ>);
+    if constexpr (PREC && NS == 2 && HD <= 64) return (K)&flash_ema_fwd_kernel<HD, NS, SB, MI, ME, SILU, VR, PREC, GQ, 2>;
+    else return (K) nullptr;
+}
+
 // nfrag: W fragment sets in LDS (PREC: one W_lo set per wave; head_dim 128: one W set per head)
 template <int HD, int NS, int SB, bool PREC>
 static size_t fwd_lds_bytes(int width, int nfrag) {
@@ -472,7 +497,7 @@ static int fwd_heads_per_group(int H, int hmax) {
 // splits only when `part` holds that many bytes (ws_bytes); otherwise it runs unsplit.
 template <int HD, int NS, int SB, bool PREC = false, bool GQ = false, class A = FlashArgsV>
 static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullptr, int64_t ws_bytes = 0,
-                      int64_t* ws_need = nullptr) {
+                      int64_t* ws_need = nullptr, bool full = false) {
     A a = a0;
     constexpr int TW = HD > 64 ? 1 : 2;  // 16-step tiles per wave, as the kernel takes them
     // head_dim 128: up to four heads (eight waves), fewer where their W fragments and
@@ -496,7 +521,8 @@ static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullpt
     const int64_t G = (int64_t)a.B * ntb * a.head_groups;
     const int64_t rows = (int64_t)a.B * a.H * a.L;
     // the kernels without VR take the base argument block, the GQ ones always FlashArgsG
-    auto run = [&](auto kern, const auto& args) -> int {
+    // kern2 (or nullptr): the CM = 2 instantiation, launched over the same grid before kern
+    auto run = [&](auto kern, const auto& args, decltype(kern) kern2 = nullptr) -> int {
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nthr, lds) != hipSuccess || per_cu < 1) {
             (void)hipGetLastError();
@@ -508,7 +534,11 @@ static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullpt
             *ws_need = need;
             return MB_OK;
         }
-        const FwdSplit sp{part, (ks > 1 && part && ws_bytes >= need) ? ks : 1};
+        const FwdSplit sp{part, (ks > 1 && part && ws_bytes >= need) ? ks : 1, full ? 1 : 0};
+        if (kern2 && !full) {
+            const int rc2 = launch_with_lds(kern2, dim3(G * sp.ksplit), nthr, lds, st, "mb_flash_ema_fwd", args, sp);
+            if (rc2) return rc2;
+        }
         const int rc = launch_with_lds(kern, dim3(G * sp.ksplit), nthr, lds, st, "mb_flash_ema_fwd", args, sp);
         if (rc || sp.ksplit == 1) return rc;
         const int64_t threads = rows * (HD / 4);
@@ -519,10 +549,14 @@ static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullpt
     const typename FlashArgsK<false, GQ>::type& base = a;
 #define MB_FWD(MI, ME)                                                                                       \
     do {                                                                                                     \
-        const int rc_ = vr ? (a.silu ? run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true, PREC, GQ>, a)         \
-                                     : run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true, PREC, GQ>, a))       \
-                           : (a.silu ? run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false, PREC, GQ>, base)     \
-                                     : run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false, PREC, GQ>, base));  \
+        const int rc_ = vr ? (a.silu ? run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, true, PREC, GQ>, a,                 \
+                                           fwd_kernel_cm2<HD, NS, SB, MI, ME, true, true, PREC, GQ>())                      \
+                                     : run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, true, PREC, GQ>, a,                \
+                                           fwd_kernel_cm2<HD, NS, SB, MI, ME, false, true, PREC, GQ>()))                    \
+                           : (a.silu ? run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, true, false, PREC, GQ>, base,             \
+                                           fwd_kernel_cm2<HD, NS, SB, MI, ME, true, false, PREC, GQ>())                     \
+                                     : run(flash_ema_fwd_kernel<HD, NS, SB, MI, ME, false, false, PREC, GQ>, base,            \
+                                           fwd_kernel_cm2<HD, NS, SB, MI, ME, false, false, PREC, GQ>()));                  \
         if (rc_ || ws_need) return rc_;                                                                      \
     } while (0)
     // With the split gate the embedding rows are staged by LDS DMA (ME = 0), which keeps the

@@ -65,9 +65,12 @@ extern "C" int mb_flash_ema_fwd_gq(const float* x_q, int64_t xq_sb, int64_t xq_s
     const int gm = flash_gate_mode("mb_flash_ema_fwd_gq", flags, N, hd);
     if (gm < 0) return gm;
     if (gm > 0) {
+        const bool full = gm == 2;  // the fp32 mode corrects every rate tile
         if (hd == 64)
-            return NS == 1 ? launch_fwd<64, 1, 4, true, true>(a, vr, st) : launch_fwd<64, 2, 2, true, true>(a, vr, st);
-        return NS == 1 ? launch_fwd<32, 1, 4, true, true>(a, vr, st) : launch_fwd<32, 2, 2, true, true>(a, vr, st);
+            return NS == 1 ? launch_fwd<64, 1, 4, true, true>(a, vr, st, nullptr, 0, nullptr, full)
+                           : launch_fwd<64, 2, 2, true, true>(a, vr, st, nullptr, 0, nullptr, full);
+        return NS == 1 ? launch_fwd<32, 1, 4, true, true>(a, vr, st, nullptr, 0, nullptr, full)
+                       : launch_fwd<32, 2, 2, true, true>(a, vr, st, nullptr, 0, nullptr, full);
     }
     if (hd == 64) {
         if (NS == 1) return launch_fwd<64, 1, 4, false, true>(a, vr, st);

@@ -77,13 +77,17 @@ def dense(Q, x, E_k_slots, E_v_slots, rhos, pe_weight, n_heads, use_silu=True, c
 # its operands.  None: exact everywhere.  "bf16": both gate operands bf16 (the reference's
 # triton_flash_ema.py:188-190).  "f16": both fp16, W pre-scaled by log2 e (the HIP kernels'
 # single-product gate).  "split": the gate exact (the HIP kernels' fp16 hi + lo split leaves
-# ~2^-22, below what a float64 check resolves at these bars).  "split_p": "split" in the
-# forward; in the backward, per (sequence, slot, head, 16-step half of a 32-step block), the
-# "f16" gate where the forward's probability stays below SPLIT_P at every step of the half,
-# else "split" (the HIP default mode's backward reading stored scores).  "f16c" / "f16w": only
+# ~2^-22, below what a float64 check resolves at these bars; the fp32 mode).  "split_t": the
+# split only on the 32-rate tiles ``corrected_rates`` selects and the "f16" product on the
+# others, in the forward and the backward (the default mode when the backward recomputes the
+# scores).  "split_p": "split_t"'s forward; in the backward p from the forward's scores (as
+# stored) and, per (sequence, slot, head, 16-step half of a 32-step block), the "f16" gate
+# where the forward's probability stays below SPLIT_P at every step of the half, else
+# "split_t"'s (the HIP default mode's backward reading stored scores).  "f16c" / "f16w": only
 # the counter / only W_pe rounded to fp16 (for measuring which rounding matters).  Every mode
 # but None takes the dW_pe product from bf16 c_dec and bf16 dpre (triton_flash_ema.py:463-465).
-GATE_ROUNDS = (None, "bf16", "f16", "split", "split_p", "f16c", "f16w")
+GATE_ROUNDS = (None, "bf16", "f16", "split", "split_t", "split_p", "f16c", "f16w")
+TILE_ROUNDS = ("split_t", "split_p")  # forwards that correct only some rate tiles
 SPLIT_P = 2.0 ** -7
 PHALF = 16  # steps per decision: a wave of the HIP backward takes 16 steps of one head
 
@@ -93,7 +97,7 @@ def _round_gate_operands(W, gate_round):
     ("f16" and "f16w"; "f16c" and "split" leave W exact)."""
     if gate_round not in GATE_ROUNDS:
         raise ValueError(f"gate_round={gate_round!r}")
-    if gate_round in (None, "f16c", "split", "split_p"):
+    if gate_round in (None, "f16c", "split", "split_t", "split_p"):
         return W
     if gate_round == "bf16":
         return W.to(torch.bfloat16).to(W.dtype)
@@ -108,9 +112,44 @@ def _round_gate_counter(c, gate_round):
     exact for None, "f16w" and "split", else fp16 ("f16", "f16c") or bf16 ("bf16")."""
     if gate_round not in GATE_ROUNDS:
         raise ValueError(f"gate_round={gate_round!r}")
-    if gate_round in (None, "f16w", "split", "split_p"):
+    if gate_round in (None, "f16w", "split", "split_t", "split_p"):
         return c
     return c.float().to(torch.float16 if gate_round != "bf16" else torch.bfloat16).to(c.dtype)
+
+
+def corrected_rates(rhos):
+    """Bool [N]: the rates whose 32-rate tile the default mode's forward gate splits into
+    hi + lo products (flash_fwd_kernel.h).  A counter stays near or below B = 1 / (1 - rho)
+    (float32, as the kernel computes it), and a single fp16 product's rounding on a rate's
+    term scales with its counter; with two tiles (32 < N <= 64) the first is left to the
+    single product when its largest B is below 1/32 of the second's.  Every other case is
+    corrected in full."""
+    N = rhos.shape[0]
+    mask = torch.ones(N, dtype=torch.bool)
+    if not 32 < N <= 64:
+        return mask
+    r = rhos.detach().to(torch.float32)
+    B = 1.0 / torch.clamp(1.0 - r, min=1e-30)
+    b0, b1 = B[:32].max(), B[32:].max()
+    if 32.0 * b0 < torch.maximum(b0, b1):
+        mask[:32] = False
+    return mask
+
+
+def _tile_gate_operands(W, rhos, gate_round):
+    """(rate mask, W operand) of the "split_t" / "split_p" forward gate: the corrected rates
+    take W exact, the others W rounded as "f16" takes it; (None, W) for other modes."""
+    if gate_round not in TILE_ROUNDS:
+        return None, W
+    mask = corrected_rates(rhos)
+    return mask, torch.where(mask.unsqueeze(1), W, _round_gate_operands(W, "f16"))
+
+
+def _tile_gate_counter(c, mask):
+    """c_dec operand of the tile-corrected forward gate (mask None: c unchanged)."""
+    if mask is None:
+        return c
+    return torch.where(mask, c, _round_gate_counter(c, "f16"))
 
 
 def _gate_product(c, W):
@@ -148,6 +187,7 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
     C = C * valid.unsqueeze(-1).to(dt)
     rho = rhos.to(dt).reshape(1, 1, N)
     W = _round_gate_operands(W_pe[:N].to(dt), gate_round)
+    tmask, W = _tile_gate_operands(W, rhos[:N], gate_round)
     Ek = E_k.reshape(B, K, H, hd).to(dt)
     Ev = E_v.reshape(B, K, H, hd).to(dt)
     log_absent = torch.log((V_total - Kb).clamp(min=0).to(dt))       # -inf if none absent
@@ -159,7 +199,8 @@ def sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init=None, use_silu=Tr
             match = (x[:, t].unsqueeze(1) == unique) & valid
             C = c_dec + match.unsqueeze(-1).to(dt)
             continue
-        pre = _gate_product(_round_gate_counter(c_dec, gate_round), W).reshape(B, K, H, hd)
+        cg = _tile_gate_counter(_round_gate_counter(c_dec, gate_round), tmask)
+        pre = _gate_product(cg, W).reshape(B, K, H, hd)
         g = F.silu(pre) if use_silu else pre
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
         s = (q_t * Ek * g).sum(-1) / math.sqrt(hd)                   # [B,K,H]
@@ -205,9 +246,10 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     dpre = (ds q/sqrt(hd)*e_k + p dO*e_v) * SiLU'(pre) (:453-461);
     dW_pe[:, head] = sum c_dec^T dpre (:465).
     Returns dQ [B,H,L,hd], dE_k [B,K,D], dE_v [B,K,D], dW_pe [N,D].
-    With ``gate_round`` the gate operands are rounded as in ``sparse`` and the dW_pe
-    product takes bf16 c_dec (of the gate's rounded c_dec; of the float32 counter with
-    "split") and bf16 dpre, as triton_flash_ema.py:463-465 does.
+    With ``gate_round`` the gate operands are rounded as in ``sparse`` (for "split_p" the
+    backward's gate and p differ, see GATE_ROUNDS) and the dW_pe product takes bf16 c_dec (of
+    the gate's rounded c_dec; of the float32 counter with the split modes) and bf16 dpre, as
+    triton_flash_ema.py:463-465 does.
     With ``t_eval`` only those steps contribute (exact when dO is zero elsewhere); dQ
     is zero at the other steps.
     """
@@ -226,12 +268,14 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
     C = C * valid.unsqueeze(-1).to(dt)
     rho = rhos.to(dt).reshape(1, 1, N)
     W = _round_gate_operands(W_pe[:N].to(dt), gate_round)
+    tmask, W = _tile_gate_operands(W, rhos[:N], gate_round)
     Ek = E_k.reshape(B, K, H, hd).to(dt)
     Ev = E_v.reshape(B, K, H, hd).to(dt)
     bf = (lambda v: v.float().to(torch.bfloat16).to(dt)) if gate_round else (lambda v: v)
-    if gate_round == "split_p":  # per (b, k, h, half-block): may the gate be single fp16?
+    if gate_round == "split_p":  # the forward's probabilities; per (b, k, h, half-block):
+        # may the backward's gate be single fp16?
         _, _, P = sparse(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, c_init, use_silu, absent_mass,
-                         gate_round="split", return_lse=True, return_probs=True)
+                         gate_round="split_t", return_lse=True, return_probs=True)
         single = single_gate_halves(P)                                # [B,K,H,nh]
         W16 = _round_gate_operands(W_pe[:N].to(dt), "f16")
     dQ = torch.zeros_like(Q)
@@ -246,7 +290,7 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
             C = c_dec + match.unsqueeze(-1).to(dt)
             continue
         i = slot[t]
-        cg = _round_gate_counter(c_dec, gate_round)
+        cg = _tile_gate_counter(_round_gate_counter(c_dec, gate_round), tmask)
         pre = _gate_product(cg, W).reshape(B, K, H, hd)
         if gate_round == "split_p":
             pre16 = _gate_product(_round_gate_counter(c_dec, "f16"), W16).reshape(B, K, H, hd)
@@ -255,15 +299,18 @@ def sparse_backward_formulas(Q, x, E_k, E_v, W_pe, rhos, V_total, unique, dO, c_
         gp = silu_grad(pre) if use_silu else torch.ones_like(pre)
         q_t = Q[:, :, t].unsqueeze(1)                                # [B,1,H,hd]
         do_t = dO[:, :, t].unsqueeze(1)
-        s = (q_t * Ek * g).sum(-1) * scale
-        p = torch.exp(s - LSE[:, :, i].unsqueeze(1)) * valid.unsqueeze(-1).to(dt)
+        if gate_round == "split_p":  # the forward's stored scores give p (its own gate)
+            p = P[..., t] * valid.unsqueeze(-1).to(dt)
+        else:
+            s = (q_t * Ek * g).sum(-1) * scale
+            p = torch.exp(s - LSE[:, :, i].unsqueeze(1)) * valid.unsqueeze(-1).to(dt)
         dp = (do_t * Ev * g).sum(-1)
         ds = p * (dp - Dv[:, :, i].unsqueeze(1))                     # [B,K,H]
         dQ[:, :, t] = (ds.unsqueeze(-1) * Ek * g).sum(1) * scale
         dEk += ds.unsqueeze(-1) * q_t * g * scale
         dEv += p.unsqueeze(-1) * do_t * g
         dpre = (ds.unsqueeze(-1) * q_t * scale * Ek + p.unsqueeze(-1) * do_t * Ev) * gp
-        cw = c_dec.float().to(dt) if gate_round in ("split", "split_p") else cg  # the kernel's float32 counter
+        cw = c_dec.float().to(dt) if gate_round in ("split", "split_t", "split_p") else cg  # the kernel's float32 counter
         dW += torch.einsum("bkn,bkd->nd", bf(cw), bf(dpre.reshape(B, K, D)))
         match = (x[:, t].unsqueeze(1) == unique) & valid
         C = c_dec + match.unsqueeze(-1).to(dt)

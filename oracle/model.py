@@ -76,10 +76,12 @@ def rmsnorm(x, w, eps=1e-6):
     return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
 
 
-def swiglu(x, w1, w2, w3, amp=None):
+def swiglu(x, w1, w2, w3, amp=None, fused=False):
     """model.py:28-29 (nn.Linear weights are [out, in]); ``amp``: the autocast dtype, whose
-    roundings the silu and the product of the bf16 projections then take too."""
-    h = rounded(rounded(F.silu(linear(x, w1, amp)), amp) * linear(x, w3, amp), amp)
+    roundings the silu and the product of the bf16 projections then take too, each (torch's
+    separate ops, the reference) or only the product (``fused``: a fused silu-product kernel)."""
+    a = linear(x, w1, amp)
+    h = rounded((F.silu(a) if fused else rounded(F.silu(a), amp)) * linear(x, w3, amp), amp)
     return linear(h, w2, amp)
 
 
@@ -96,7 +98,8 @@ def unique_index(x):
 
 def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_base=None,
                pad_mask=None, use_silu=True, attention="sparse", gate_round=None,
-               absent_mass=True, mask_query_keys=True, t_eval=None, amp=None, amp_pe_proj=False):
+               absent_mass=True, mask_query_keys=True, t_eval=None, amp=None, amp_pe_proj=False,
+               amp_fused_swiglu=False):
     """Logits [B, L, V] of SlotTransformerLM.forward (model.py:144-186).
 
     ``absent_mass`` picks the attention's softmax (all V slots, or the valid slots only as
@@ -112,7 +115,9 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
     the reference, triton_flash_ema.py:573, triton_fused_gating.py) stay wide.  The query
     gate's pe_proj is a Linear in the reference's wrapper (triton_fused_gating.py:183), so
     under autocast its output is bf16 there; ``amp_pe_proj`` rounds it that way, where this
-    implementation computes it inside the fp32 gating kernel."""
+    implementation computes it inside the fp32 gating kernel.  ``amp_fused_swiglu`` rounds
+    SwiGLU's silu-product once, as this implementation's fused kernel does (twice in torch's
+    separate ops)."""
     B, L = x.shape
     E = p["embed.weight"]
     dt = E.dtype
@@ -163,9 +168,9 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
                 Q_full = Q_t.new_zeros(B, L, D).index_copy(1, torch.tensor(steps), Q_t)
             Q_mha = Q_full.reshape(B, L, H, hd).transpose(1, 2)          # :81
             Wt = g("attn.pe_proj.weight").t()
-            # "split_p" rounds the backward's gate differently from the forward's, so its
-            # gradients come from the closed-form backward rather than from autograd
-            if t_eval is None and gate_round != "split_p":
+            # "split_t" and "split_p" round the backward's gate differently from the forward's,
+            # so their gradients come from the closed-form backward rather than from autograd
+            if t_eval is None and gate_round not in att.TILE_ROUNDS:
                 O = att.sparse(Q_mha, x, Ek, Ev, Wt, rhos.to(dt), vocab_size, unique, cb,
                                use_silu=use_silu, absent_mass=absent_mass, gate_round=gate_round)
             else:
@@ -182,7 +187,7 @@ def lm_forward(p, x, n_layers, n_heads, rhos, vocab_size, unique_slots=None, c_b
         out = linear(out, g("attn.o_proj.weight"), amp)                 # :101
         h = x_q + out                                                   # :114
         h = h + swiglu(rmsnorm(h, g("ffn_norm.weight")), g("ffn.w1.weight"), g("ffn.w2.weight"),
-                       g("ffn.w3.weight"), amp)                         # :115
+                       g("ffn.w3.weight"), amp, amp_fused_swiglu)       # :115
         x_q = h
     x_q = rmsnorm(x_q, p["final_norm.weight"])                          # :185
     return linear(x_q, E, amp)                                          # :186, tied lm_head

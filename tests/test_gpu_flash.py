@@ -66,13 +66,17 @@ def make_case(B, L, V, H, hd, N, warmup=0, seed=0, uniform=False, min_hl=1.0, ma
 
 def kernel_rounding(N, hd, precision="bf16", stored_scores=True):
     """The oracle's gate_round that the kernels' gate arithmetic matches: the default mode
-    splits the gate operands where N <= 64 and head_dim <= 64, in the backward only for the
-    slots whose stored probability reaches 2^-7 in a wave's 16 steps ("split_p"; "split" when
-    the backward recomputes the scores); the fast mode and the default beyond those shapes
-    take single fp16 operands ("f16")."""
+    splits the gate operands where N <= 64 and head_dim <= 64, in the forward on the rate
+    tiles whose counters can be large, in the backward only for the slots whose stored
+    probability reaches 2^-7 in a wave's 16 steps ("split_p"; "split_t" when the backward
+    recomputes the scores, which splits every slot); the fp32 mode splits everywhere
+    ("split"); the fast mode and the default beyond those shapes take single fp16 operands
+    ("f16")."""
     if precision == "fp16" or N > 64 or hd > 64:
         return "f16"
-    return "split_p" if stored_scores else "split"
+    if precision == "fp32":
+        return "split"
+    return "split_p" if stored_scores else "split_t"
 
 
 def case_rounding(c, precision="bf16", stored_scores=True):

@@ -309,3 +309,85 @@ def test_return_probs_are_the_softmax_weights():
     total = P.sum(1) + absent
     assert torch.allclose(total, torch.ones_like(total), rtol=1e-12)
     assert torch.count_nonzero(P[~valid]) == 0
+
+
+def _cfg_rates(N=64, lo=1.0, hi=4096.0):
+    """Rates of half-lives log-spaced from lo to hi, as SlotTransformerLM sets them."""
+    hl = torch.logspace(math.log10(lo), math.log10(hi), N, dtype=torch.float64)
+    return torch.exp(math.log(0.5) / hl).to(torch.float32)
+
+
+def test_corrected_rates_rule():
+    """The default forward's tile rule: with the model's rates (half-lives 1..4096) the first
+    32-rate tile's largest bound B = 1/(1 - rho) is ~87 against ~5900 and is left to the
+    single product; the comparison is 32 B_0 >= max B (at equality the tile is corrected);
+    one tile, more than two, or the large rates first: every rate corrected."""
+    r = _cfg_rates()
+    B = 1.0 / (1.0 - r.double())
+    assert 80 < float(B[:32].max()) < 95 and 5800 < float(B[32:].max()) < 6000
+    m = att.corrected_rates(r)
+    assert m.tolist() == [False] * 32 + [True] * 32
+    assert att.corrected_rates(r.flip(0)).all()                  # large rates in tile 0
+    assert att.corrected_rates(_cfg_rates(32)).all()              # one tile
+    assert att.corrected_rates(_cfg_rates(96)).all()              # beyond the split's N
+    assert att.corrected_rates(torch.full((64,), 0.9)).all()
+    # B = 2^k exactly: 32 * 8 = 256 corrects tile 0, 512 does not
+    eq = torch.tensor([1 - 2.0**-3] * 32 + [1 - 2.0**-8] * 32, dtype=torch.float32)
+    assert att.corrected_rates(eq).all()
+    gt = torch.tensor([1 - 2.0**-3] * 32 + [1 - 2.0**-9] * 32, dtype=torch.float32)
+    assert att.corrected_rates(gt).tolist() == [False] * 32 + [True] * 32
+
+
+def _problem64(seed, zero_tile=None, L=12):
+    """_problem with N = 64 model rates; zero_tile t zeroes W_pe's rows of rate tile t."""
+    p = _problem(seed, L=L)
+    g = torch.Generator().manual_seed(seed + 100)
+    D = p["pe_weight"].shape[0]
+    p["rhos"] = _cfg_rates().double()
+    p["pe_weight"] = torch.randn(D, 64, generator=g, dtype=torch.float64) * 0.05
+    if zero_tile is not None:
+        p["pe_weight"][:, 32 * zero_tile: 32 * zero_tile + 32] = 0.0
+    K = p["unique"].shape[1]
+    p["c_init"] = torch.rand(p["unique"].shape[0], K, 64, generator=g, dtype=torch.float64) / (1 - p["rhos"])
+    p["c_init"] *= (p["unique"] >= 0).unsqueeze(-1)
+    return p
+
+
+def test_split_t_forward_rounds_only_the_uncorrected_tile():
+    """"split_t" / "split_p" forward: the corrected tile's products exact, the other tile's
+    the single fp16 product: with the uncorrected tile's W rows zero it is the exact forward,
+    with the corrected tile's zero it is "f16"'s, and in general it sits between them."""
+    p = _problem64(20, zero_tile=0)
+    assert torch.equal(_sparse(p, gate_round="split_t"), _sparse(p))
+    assert torch.equal(_sparse(p, gate_round="split_p"), _sparse(p))
+    p = _problem64(20, zero_tile=1)
+    assert torch.equal(_sparse(p, gate_round="split_t"), _sparse(p, gate_round="f16"))
+    p = _problem64(21)
+    exact = _sparse(p)
+    d = lambda a: float((a - exact).abs().max() / exact.abs().max())
+    dt, d16 = d(_sparse(p, gate_round="split_t")), d(_sparse(p, gate_round="f16"))
+    assert 0.0 < dt < d16, (dt, d16)
+    assert d(_sparse(p, gate_round="split")) == 0.0
+
+
+def test_split_t_backward_takes_the_forwards_gate():
+    """"split_t"'s backward gate is its forward's (the tile rule): with the uncorrected tile's
+    W rows zero it is "split" exactly, otherwise close to it.  "split_p" takes p from the
+    forward's scores (the stored ones) and the same gate where it splits: with a threshold of
+    0 (every slot split) it is "split_t" up to the order of the score arithmetic."""
+    p = _problem64(22, zero_tile=0)
+    for a, b in zip(_bwd(p, "split_t"), _bwd(p, "split")):
+        assert torch.equal(a, b)
+    p = _problem64(23)
+    st, sp = _bwd(p, "split_t"), _bwd(p, "split")
+    assert any(not torch.equal(a, b) for a, b in zip(st, sp))
+    for a, b in zip(st, sp):
+        assert float((a - b).abs().max() / b.abs().max()) < 1e-2
+    import oracle.attention as mod
+    old = mod.SPLIT_P
+    try:
+        mod.SPLIT_P = 0.0
+        for a, b in zip(_bwd(p, "split_p"), st):
+            assert torch.allclose(a, b, rtol=1e-9, atol=1e-300)
+    finally:
+        mod.SPLIT_P = old
