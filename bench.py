@@ -61,8 +61,9 @@ PEAK_HBM_GBS = 8000.0
 # the attention's arithmetic per --precision (the default splits the gate operands where
 # N <= 64 and head_dim <= 64, and takes single fp16 operands beyond)
 GATE_DTYPES = {
-    "bf16": ("fp16 hi+lo split gate MFMA (3 products; in the backward only for slots whose stored p "
-             "reaches 2^-7, else 1 product), bf16 dW_pe MFMA, fp32 state/softmax/accumulate"),
+    "bf16": ("fp16 hi+lo split gate MFMA (3 products on the large-counter rate tile, 1 on the other; "
+             "in the backward only for slots whose stored p reaches 2^-7, else 1 product), bf16 dW_pe "
+             "MFMA, fp32 state/softmax/accumulate"),
     "fp16": "fp16 gate MFMA (1 product), bf16 dW_pe MFMA, fp32 state/softmax/accumulate",
     "fp32": "fp32 mode: fp16 hi+lo gate MFMA (bf16 hi+lo dW_pe MFMA), fp32 state/softmax/accumulate",
 }

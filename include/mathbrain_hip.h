@@ -189,7 +189,13 @@ int mb_unique_rows(const int64_t *x, int64_t x_stride_b, int64_t x_stride_l, int
  * W_hi c_lo + W_hi c_hi) with fp32 accumulation, ~2^-22 relative: where scores reach
  * ~100 (a model's own initialisation can do that) the softmax turns a relative gate error
  * e into ~100 e of the weights, and single fp16 operands (2^-11) moved a 6-layer model's
- * logits by 2e-2 and its gradients by 0.1 from the exact model.  With MB_FLASH_FAST_GATE,
+ * logits by 2e-2 and its gradients by 0.1 from the exact model.  The two lo products are
+ * taken only on the 32-rate tiles whose counters can be large: an EMA of counts stays near
+ * or below B = 1/(1 - rho), and with two tiles the first takes the single product when its
+ * largest B is below 1/32 of the second's (rates from half-life 1 to 4096: 87 against 5900;
+ * the 6-layer model then sits 6e-4 / 5e-3 from the exact one).  Each workgroup decides from
+ * `rhos`, and the launch runs one kernel instantiation per choice.  MB_FLASH_FP32 splits
+ * every tile.  With MB_FLASH_FAST_GATE,
  * and by default for N > 64 or hd 128 (where the lo tiles do not fit in LDS), the gate
  * takes single fp16 operands.  The fp16 counters are clamped to 65440 at the chunk start;
  * an EMA of counts stays below 1/(1 - rho), under that bound for half-lives up to ~45,000
@@ -238,7 +244,9 @@ int64_t mb_flash_ema_fwd_workspace(int B, int H, int L, int hd, int K, int N, in
  * product elsewhere: every gradient term of a slot carries its probability, so the single
  * product's rounding enters scaled by it (at a 6-layer model's initialisation 99.9 % of the
  * slot-steps qualify, and the gradients' distance from the exact model's stays 4.6e-3, as
- * with the split everywhere).  MB_FLASH_FP32 always splits.  The dW_pe product takes bf16
+ * with the split everywhere).  The backward's split is the forward's gate (lo products on the
+ * same rate tiles), so recomputed scores are the forward's.  MB_FLASH_FP32 always splits,
+ * every tile.  The dW_pe product takes bf16
  * c_dec and bf16 dpre (as the reference's triton_flash_ema.py:463-465 does), or with
  * MB_FLASH_FP32 bf16 hi + lo pairs of both, with fp32 accumulation.  Supported: as
  * mb_flash_ema_fwd.  At hd 128 each head runs as two 64-dim halves on two waves that add

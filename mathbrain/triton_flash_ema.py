@@ -169,7 +169,9 @@ def _forget_rates(key):
 # Gate arithmetic of the attention kernels:
 #   "bf16" (default)  the gate GEMM splits c_dec and W_pe * log2 e into fp16 hi + lo pairs
 #                     (three products, ~2^-22 relative) where the kernels take it (N <= 64,
-#                     head_dim <= 64; single fp16 operands otherwise); the backward, when it
+#                     head_dim <= 64; single fp16 operands otherwise), on the 32-rate tiles
+#                     whose counters can be large (a tile whose largest 1/(1 - rho) is below
+#                     1/32 of the largest takes the single product); the backward, when it
 #                     reads the forward's scores, splits only for the slots whose probability
 #                     reaches 2^-7 at one of a wave's 16 steps (every gradient term of a slot
 #                     carries its p); dW_pe from bf16 operands, as the reference's kernel;
