@@ -129,7 +129,6 @@ flash_ema_fwd_kernel(typename FlashArgsK<VR, GQ>::type a, FwdSplit sp) {
     const int bi1 = (part + 1) * nball / sp.ksplit;
     const int x32 = (lane ^ 32) << 2;  // ds_bpermute byte address of lane l ^ 32
 
-
     // Gate weights as the A operand: W^T[d = 16 dt + c16][n = 32 ns + 8 g + e] * log2 e.
     // Rows n >= N are zero; their loads read row N - 1 so that all loads issue at once.
     f16x8 wf[TW == 2 ? DT : 1][TW == 2 ? NS : 1];
