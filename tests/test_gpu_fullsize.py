@@ -223,9 +223,11 @@ def test_cfg5_full_model_fp32_mode_exact():
 # the most sensitive one to where bf16 rounds: the GPU's sits 0.25 from the oracle at the
 # reference's rounding points and 0.21 from the exact model, and before the forward's gate
 # corrected only the large-counter rate tile (a change at the 1e-4 level) 0.13 from this one.
+# Its bar is twice the spread measured between valid evaluations (the atomics' summation
+# order varies from run to run too).
 TOL_AMP_LOGITS = 2e-2
 TOL_AMP_GRAD = 5e-2
-TOL_AMP_GRAD_LNQ_BIAS = 3e-1
+TOL_AMP_GRAD_LNQ_BIAS = 5e-1
 
 
 def test_cfg5_full_model_bf16_autocast():
