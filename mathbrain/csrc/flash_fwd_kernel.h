@@ -467,11 +467,15 @@ static int64_t fwd_part_bytes(int ks, int B, int H, int L, int hd) {
     return ks > 1 ? (int64_t)ks * B * H * L * (hd + 2) * 4 : 0;
 }
 
-// The CM = 2 instantiation a default-mode launch adds (two rate tiles), or nullptr.
+// The CM = 2 instantiation a default-mode launch adds (two rate tiles), or nullptr.  Without
+// the first tile's lo products it has the registers to stage the slot rows itself (ME = 2,
+// which every split-gate shape fits: at most 512 columns of three slots over 512 threads)
+// instead of by LDS DMA, whose wait at the end of a batch also waits for the batch's score
+// stores (forward 11.58 -> 10.85 ms at configuration 2).
 template <int HD, int NS, int SB, int MI, int ME, bool SILU, bool VR, bool PREC, bool GQ>
 constexpr auto fwd_kernel_cm2() {
     using K = decltype(&flash_ema_fwd_kernel<HD, NS, SB, MI, ME, SILU, VR, PREC, GQ>);
-    if constexpr (PREC && NS == 2 && HD <= 64) return (K)&flash_ema_fwd_kernel<HD, NS, SB, MI, ME, SILU, VR, PREC, GQ, 2>;
+    if constexpr (PREC && NS == 2 && HD <= 64) return (K)&flash_ema_fwd_kernel<HD, NS, SB, MI, 2, SILU, VR, PREC, GQ, 2>;
     else return (K) nullptr;
 }
 
@@ -512,6 +516,7 @@ static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullpt
     constexpr int NPAD = 32 * NS;
     const int mi = (SB * (kTB / 4) * (NPAD / 4) + nthr - 1) / nthr;
     const int nvec = SB * 2 * (width / 4);
+    const int me = (nvec + nthr - 1) / nthr;  // float4 row copies per thread
     size_t lds = fwd_lds_bytes<HD, NS, SB, PREC>(width, PREC ? nthr / 64 : (TW == 1 ? hpg : 0));
     if (GQ) lds = std::max(lds, gq_fwd_lds_bytes(a.H * HD, a.N));
     if (lds > 160 * 1024)
@@ -533,8 +538,11 @@ static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullpt
             *ws_need = need;
             return MB_OK;
         }
-        const FwdSplit sp{part, (ks > 1 && part && ws_bytes >= need) ? ks : 1, full ? 1 : 0};
-        if (kern2 && !full) {
+        // two instantiations only when the CM = 2 one exists and its row copy fits (me <= 2);
+        // otherwise the one launch corrects every rate tile (sp.full: no workgroup returns)
+        const bool two = kern2 && !full && me <= 2;
+        const FwdSplit sp{part, (ks > 1 && part && ws_bytes >= need) ? ks : 1, two ? 0 : 1};
+        if (two) {
             const int rc2 = launch_with_lds(kern2, dim3(G * sp.ksplit), nthr, lds, st, "mb_flash_ema_fwd", args, sp);
             if (rc2) return rc2;
         }
@@ -563,7 +571,6 @@ static int launch_fwd(const A& a0, bool vr, hipStream_t st, float* part = nullpt
     // rows staged through registers, 2 with the DMA; 13.10 -> 12.40 ms).  The single-product
     // gate keeps the register copy: the DMA's wait at the end of a batch (vmcnt(0)) also waits
     // for the batch's score stores, and that forward measured 9.47 -> 9.97 ms with it.
-    const int me = (nvec + nthr - 1) / nthr;
     if (mi > 4 || me > 4)
         return fail(MB_ERR_UNSUPPORTED, "mb_flash_ema_fwd: width %d, N=%d too wide for %d threads", width, a.N, nthr);
     if (PREC) {
